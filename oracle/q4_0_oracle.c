@@ -1,0 +1,478 @@
+/*
+ * q4_0_oracle.c — CPU restatement of hypno's Q4_0 / FP16 matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity checker and the CPU
+ * baseline.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it; the product library (hypno_amd) never
+ * links, calls or falls back to it.
+ *
+ * Every function cites the reference source it restates (paths relative to
+ * the hypno repository root, crates/hypno/src/).  The reference is Rust and
+ * cannot be built in this image (no rustc/cargo, no crate registry), so it is
+ * restated here in C and pinned by the tests in tests/test_oracle.py against
+ * the reference's own known-answer tests, IEEE definitions, numpy and
+ * brute-force fp64 sums.
+ *
+ * Parity status per function (what pins it):
+ *   orc_f16_to_f32      exact by definition; checked against numpy and F16C
+ *   orc_f32_to_f16      IEEE RNE; checked against numpy float16 and F16C
+ *   orc_quantize_q4_0   reference KATs quant.rs:213-237, sft_convert.rs:430-457,
+ *                       hand-computed blocks (half-away rounding, clamp, f16 d)
+ *   orc_dequantize_q4_0 closed form; hand-built blocks, nibble 0/8/15 cases
+ *   orc_matmul_q4_0_*   fp64 brute force on the dequantized matrix, exact
+ *                       integer-valued cases, straddling rows (K % 32 != 0),
+ *                       short-buffer semantics, bias; the exact fp32 bits of
+ *                       the AVX2 summation order are "parity unpinned" (only
+ *                       running hypno could pin them)
+ *   orc_matmul_f16_*    fp64 brute force; exact integer KAT (ops.rs:114-121)
+ *   orc_batch_matmul    per-token equality with the GEMV; turbo.rs KATs
+ *
+ * Build: oracle/Makefile (gcc, -ffp-contract=off, no fast-math; the AVX2
+ * kernels use target attributes so the library runs on any x86-64 host and
+ * dispatches at run time like kernels.rs:256-265).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <string.h>
+#include <stdlib.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+#if defined(__x86_64__)
+#include <immintrin.h>
+#endif
+
+#define Q4_BLOCK_ELEMS 32
+#define Q4_BLOCK_BYTES 18
+
+static int g_threads = 1;
+
+/* Number of OpenMP threads the matmul kernels use (rayon pool size in
+ * hypno: run.rs:56-59, bench.rs:20). */
+void orc_set_threads(int n) { g_threads = n > 0 ? n : 1; }
+int orc_get_threads(void) { return g_threads; }
+
+/* ------------------------------------------------------------------------ */
+/* half 2.7.1 f16 <-> f32 (third-party crate used at kernels.rs:297,376,561,  */
+/* 583 and quant.rs:26,57).  to_f32 is exact; from_f32 is IEEE-754          */
+/* round-to-nearest-even with overflow to infinity.                           */
+/* ------------------------------------------------------------------------ */
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1Fu;
+    uint32_t man = h & 0x3FFu;
+    uint32_t bits;
+    if (exp == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else {
+            /* subnormal: man * 2^-24; normalise so bit 10 is the implicit 1 */
+            int e = -1;
+            do { man <<= 1; e++; } while (!(man & 0x400u));
+            bits = sign | ((uint32_t)(112 - e) << 23) | ((man & 0x3FFu) << 13);
+        }
+    } else if (exp == 31) {
+        /* inf, or NaN made quiet with its payload kept */
+        bits = sign | 0x7F800000u | (man << 13) | (man ? 0x00400000u : 0u);
+    } else {
+        bits = sign | ((exp + 112u) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t exp = (x >> 23) & 0xFFu;
+    uint32_t man = x & 0x7FFFFFu;
+    if (exp == 0xFF) {
+        if (man == 0) return (uint16_t)(sign | 0x7C00u);
+        return (uint16_t)(sign | 0x7E00u | (man >> 13));
+    }
+    int e = (int)exp - 127 + 15;
+    if (e >= 31) return (uint16_t)(sign | 0x7C00u);
+    if (e <= 0) {
+        /* f16 subnormal (or zero): units of 2^-24 */
+        if (exp == 0) return (uint16_t)sign; /* f32 subnormal/zero < 2^-126 */
+        uint32_t full = man | 0x800000u;
+        int s = 126 - (int)exp; /* >= 14 */
+        if (s > 24) return (uint16_t)sign;
+        uint32_t hm = full >> s;
+        uint32_t rem = full & ((1u << s) - 1u);
+        uint32_t half = 1u << (s - 1);
+        if (rem > half || (rem == half && (hm & 1u))) hm++;
+        return (uint16_t)(sign | hm);
+    }
+    uint32_t hm = man >> 13;
+    uint32_t rem = man & 0x1FFFu;
+    uint32_t h = ((uint32_t)e << 10) + hm;
+    if (rem > 0x1000u || (rem == 0x1000u && (hm & 1u))) h++; /* carry may reach inf */
+    return (uint16_t)(sign | h);
+}
+
+void orc_f16_to_f32_array(const uint16_t* src, float* dst, size_t n) {
+    for (size_t i = 0; i < n; i++) dst[i] = orc_f16_to_f32(src[i]);
+}
+
+void orc_f32_to_f16_array(const float* src, uint16_t* dst, size_t n) {
+    for (size_t i = 0; i < n; i++) dst[i] = orc_f32_to_f16(src[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Q4_0 codec (quant.rs)                                                      */
+/* ------------------------------------------------------------------------ */
+
+/* Rust `f32 as i32` is a saturating cast with NaN -> 0. */
+static int32_t sat_f32_to_i32(float r) {
+    if (r != r) return 0;
+    if (r >= 2147483648.0f) return INT32_MAX;
+    if (r <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)r;
+}
+
+static int32_t clamp_i32(int32_t v, int32_t lo, int32_t hi) {
+    return v < lo ? lo : (v > hi ? hi : v);
+}
+
+/* Q4_0Block::quantize, quant.rs:49-71.
+ * amax = fold(0, f32::max) over |v| (f32::max ignores NaN, like fmaxf);
+ * s = amax/7 in f32 (1.0 when amax == 0); d = f16 RNE(s);
+ * q = clamp(round_half_away(v / s), -8, 7) — divides by the unrounded s;
+ * byte i = (q[2i]+8) | (q[2i+1]+8) << 4. */
+void orc_quantize_block_q4_0(const float* src, uint8_t* out) {
+    float max_abs = 0.0f;
+    for (int i = 0; i < Q4_BLOCK_ELEMS; i++) max_abs = fmaxf(max_abs, fabsf(src[i]));
+    float scale = max_abs > 0.0f ? max_abs / 7.0f : 1.0f;
+    uint16_t d = orc_f32_to_f16(scale);
+    out[0] = (uint8_t)(d & 0xFF);
+    out[1] = (uint8_t)(d >> 8);
+    for (int i = 0; i < 16; i++) {
+        float v0 = src[2 * i];
+        float v1 = src[2 * i + 1];
+        int32_t q0 = clamp_i32(sat_f32_to_i32(roundf(v0 / scale)), -8, 7);
+        int32_t q1 = clamp_i32(sat_f32_to_i32(roundf(v1 / scale)), -8, 7);
+        uint8_t nib0 = (uint8_t)((q0 + 8) & 0x0F);
+        uint8_t nib1 = (uint8_t)((q1 + 8) & 0x0F);
+        out[2 + i] = (uint8_t)(nib0 | (nib1 << 4));
+    }
+}
+
+/* quantize_f32_to_q4_0, quant.rs:108-117: floor(len/32) blocks; a trailing
+ * partial block is dropped.  Returns the number of bytes written. */
+size_t orc_quantize_q4_0(const float* src, size_t n, uint8_t* out) {
+    size_t nb = n / Q4_BLOCK_ELEMS;
+    for (size_t b = 0; b < nb; b++)
+        orc_quantize_block_q4_0(src + b * Q4_BLOCK_ELEMS, out + b * Q4_BLOCK_BYTES);
+    return nb * Q4_BLOCK_BYTES;
+}
+
+/* Q4_0Block::dequantize, quant.rs:25-34; dequantize_q4_0, quant.rs:120-132:
+ * floor(q_len/18) blocks; element 2i = (lo(byte i) - 8) * d,
+ * element 2i+1 = (hi(byte i) - 8) * d, computed in f32 (exact). */
+size_t orc_dequantize_q4_0(const uint8_t* q, size_t q_len, float* out) {
+    size_t nb = q_len / Q4_BLOCK_BYTES;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* blk = q + b * Q4_BLOCK_BYTES;
+        float scale = orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+        for (int i = 0; i < 16; i++) {
+            uint8_t byte = blk[2 + i];
+            out[b * 32 + 2 * i] = (float)((int32_t)(byte & 0x0F) - 8) * scale;
+            out[b * 32 + 2 * i + 1] = (float)((int32_t)((byte >> 4) & 0x0F) - 8) * scale;
+        }
+    }
+    return nb * Q4_BLOCK_ELEMS;
+}
+
+static void deq_block(const uint8_t* blk, float* deq) {
+    float scale = orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+    for (int i = 0; i < 16; i++) {
+        uint8_t byte = blk[2 + i];
+        deq[2 * i] = (float)((int32_t)(byte & 0x0F) - 8) * scale;
+        deq[2 * i + 1] = (float)((int32_t)((byte >> 4) & 0x0F) - 8) * scale;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* matmul_q4_0_scalar, kernels.rs:362-400.                                    */
+/* Row r covers flattened elements [r*m, (r+1)*m); it walks the blocks that    */
+/* overlap that range (blocks straddle rows when m % 32 != 0).  A block whose  */
+/* 18 bytes do not fit in w_len ends the row (`break`, kernels.rs:374).        */
+/* sum += deq*x in f32 without contraction; y = sum + (bias or 0.0).          */
+/* ------------------------------------------------------------------------ */
+static float row_q4_0_scalar(const uint8_t* w, size_t w_len, const float* x,
+                             size_t row, size_t m) {
+    size_t row_start = row * m;
+    size_t row_end = row_start + m;
+    size_t first_block = row_start / 32;
+    size_t last_block = (row_end > 0 ? row_end - 1 : 0) / 32;
+    float sum = 0.0f;
+    float deq[32];
+    for (size_t b = first_block; b <= last_block; b++) {
+        size_t bo = b * Q4_BLOCK_BYTES;
+        if (bo + Q4_BLOCK_BYTES > w_len) break;
+        deq_block(w + bo, deq);
+        size_t block_start = b * 32;
+        size_t ov_start = block_start < row_start ? row_start - block_start : 0;
+        size_t ov_end = block_start + 32 > row_end ? row_end - block_start : 32;
+        size_t x_off = block_start > row_start ? block_start - row_start : 0;
+        for (size_t i = ov_start; i < ov_end; i++) sum += deq[i] * x[x_off + (i - ov_start)];
+    }
+    return sum;
+}
+
+void orc_matmul_q4_0_scalar(float* y, const uint8_t* w, size_t w_len, const float* x,
+                            const float* bias, size_t n, size_t m) {
+    long long nn = (long long)n;
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (long long r = 0; r < nn; r++) {
+        float sum = row_q4_0_scalar(w, w_len, x, (size_t)r, m);
+        y[r] = sum + (bias ? bias[r] : 0.0f);
+    }
+}
+
+#if defined(__x86_64__)
+/* hsum256, kernels.rs:169-178: lo128+hi128, then two horizontal adds. */
+__attribute__((target("avx2,fma"))) static inline float hsum256(__m256 v) {
+    __m128 hi = _mm256_extractf128_ps(v, 1);
+    __m128 lo = _mm256_castps256_ps128(v);
+    __m128 s = _mm_add_ps(lo, hi);
+    s = _mm_hadd_ps(s, s);
+    s = _mm_hadd_ps(s, s);
+    return _mm_cvtss_f32(s);
+}
+
+/* matmul_q4_0_avx2, kernels.rs:270-359.  Same operation order: per full block
+ * four 8-wide FMAs into acc0..acc3 over a scalar-dequantised stack buffer;
+ * boundary blocks add deq*x into scalar_tail; at the end
+ * ((acc0+acc1)+(acc2+acc3)) -> hsum256 -> + scalar_tail -> + bias. */
+__attribute__((target("avx2,fma"))) static float row_q4_0_avx2(
+    const uint8_t* w, size_t w_len, const float* x, size_t row, size_t m) {
+    size_t row_start = row * m;
+    size_t row_end = row_start + m;
+    size_t first_block = row_start / 32;
+    size_t last_block = (row_end > 0 ? row_end - 1 : 0) / 32;
+    __m256 acc0 = _mm256_setzero_ps();
+    __m256 acc1 = _mm256_setzero_ps();
+    __m256 acc2 = _mm256_setzero_ps();
+    __m256 acc3 = _mm256_setzero_ps();
+    float scalar_tail = 0.0f;
+    float deq[32];
+    for (size_t b = first_block; b <= last_block; b++) {
+        size_t bo = b * Q4_BLOCK_BYTES;
+        if (bo + Q4_BLOCK_BYTES > w_len) break;
+        deq_block(w + bo, deq);
+        size_t block_start = b * 32;
+        size_t ov_start = block_start < row_start ? row_start - block_start : 0;
+        size_t ov_end = block_start + 32 > row_end ? row_end - block_start : 32;
+        size_t x_off = block_start > row_start ? block_start - row_start : 0;
+        if (ov_start == 0 && ov_end == 32) {
+            __m256 dv0 = _mm256_loadu_ps(deq);
+            __m256 dv1 = _mm256_loadu_ps(deq + 8);
+            __m256 dv2 = _mm256_loadu_ps(deq + 16);
+            __m256 dv3 = _mm256_loadu_ps(deq + 24);
+            __m256 xv0 = _mm256_loadu_ps(x + x_off);
+            __m256 xv1 = _mm256_loadu_ps(x + x_off + 8);
+            __m256 xv2 = _mm256_loadu_ps(x + x_off + 16);
+            __m256 xv3 = _mm256_loadu_ps(x + x_off + 24);
+            acc0 = _mm256_fmadd_ps(dv0, xv0, acc0);
+            acc1 = _mm256_fmadd_ps(dv1, xv1, acc1);
+            acc2 = _mm256_fmadd_ps(dv2, xv2, acc2);
+            acc3 = _mm256_fmadd_ps(dv3, xv3, acc3);
+        } else {
+            for (size_t i = ov_start; i < ov_end; i++)
+                scalar_tail += deq[i] * x[x_off + (i - ov_start)];
+        }
+    }
+    __m256 sum01 = _mm256_add_ps(acc0, acc1);
+    __m256 sum23 = _mm256_add_ps(acc2, acc3);
+    __m256 sumall = _mm256_add_ps(sum01, sum23);
+    return hsum256(sumall) + scalar_tail;
+}
+
+__attribute__((target("avx2,fma"))) void orc_matmul_q4_0_avx2(
+    float* y, const uint8_t* w, size_t w_len, const float* x, const float* bias,
+    size_t n, size_t m) {
+    size_t total_blocks = (n * m + 31) / 32;
+    if (w_len < total_blocks * Q4_BLOCK_BYTES) {
+        /* kernels.rs:275-277: a short buffer falls back to the scalar kernel */
+        orc_matmul_q4_0_scalar(y, w, w_len, x, bias, n, m);
+        return;
+    }
+    long long nn = (long long)n;
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (long long r = 0; r < nn; r++) {
+        float total = row_q4_0_avx2(w, w_len, x, (size_t)r, m);
+        if (bias) total += bias[r];
+        y[r] = total;
+    }
+}
+
+/* matmul_f16_avx2_fma, kernels.rs:543-565: one 8-wide FMA accumulator over
+ * F16C-converted weights, hsum256, scalar tail, + (bias or 0.0). */
+__attribute__((target("avx2,fma,f16c"))) void orc_matmul_f16_avx2(
+    float* y, const uint8_t* w, size_t w_len, const float* x, const float* bias,
+    size_t n, size_t m) {
+    (void)w_len;
+    const uint16_t* w16 = (const uint16_t*)w;
+    size_t m8 = m - (m % 8);
+    long long nn = (long long)n;
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (long long r = 0; r < nn; r++) {
+        const uint16_t* row = w16 + (size_t)r * m;
+        __m256 acc = _mm256_setzero_ps();
+        for (size_t j = 0; j < m8; j += 8) {
+            __m128i w128 = _mm_loadu_si128((const __m128i*)(row + j));
+            __m256 wf = _mm256_cvtph_ps(w128);
+            __m256 xv = _mm256_loadu_ps(x + j);
+            acc = _mm256_fmadd_ps(wf, xv, acc);
+        }
+        float sum = hsum256(acc);
+        for (size_t j = m8; j < m; j++) sum += orc_f16_to_f32(row[j]) * x[j];
+        y[r] = sum + (bias ? bias[r] : 0.0f);
+    }
+}
+
+/* Hardware F16C conversions, used only to cross-check orc_f32_to_f16 and
+ * orc_f16_to_f32 in the tests (an implementation independent of the C code
+ * above).  Round-to-nearest-even is requested explicitly. */
+__attribute__((target("f16c"))) void orc_f32_to_f16_f16c(const float* src, uint16_t* dst, size_t n) {
+    for (size_t i = 0; i < n; i++)
+        dst[i] = (uint16_t)_cvtss_sh(src[i], _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+}
+__attribute__((target("f16c"))) void orc_f16_to_f32_f16c(const uint16_t* src, float* dst, size_t n) {
+    for (size_t i = 0; i < n; i++) dst[i] = _cvtsh_ss(src[i]);
+}
+
+int orc_have_avx2_fma(void) {
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
+}
+int orc_have_f16c(void) {
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("f16c");
+}
+#else
+int orc_have_avx2_fma(void) { return 0; }
+int orc_have_f16c(void) { return 0; }
+void orc_matmul_q4_0_avx2(float* y, const uint8_t* w, size_t w_len, const float* x,
+                          const float* bias, size_t n, size_t m) {
+    orc_matmul_q4_0_scalar(y, w, w_len, x, bias, n, m);
+}
+void orc_matmul_f16_scalar(float* y, const uint8_t* w, size_t w_len, const float* x,
+                           const float* bias, size_t n, size_t m);
+void orc_matmul_f16_avx2(float* y, const uint8_t* w, size_t w_len, const float* x,
+                         const float* bias, size_t n, size_t m) {
+    orc_matmul_f16_scalar(y, w, w_len, x, bias, n, m);
+}
+#endif
+
+/* matmul_f16 scalar fallback, kernels.rs:578-585. */
+void orc_matmul_f16_scalar(float* y, const uint8_t* w, size_t w_len, const float* x,
+                           const float* bias, size_t n, size_t m) {
+    (void)w_len;
+    const uint16_t* w16 = (const uint16_t*)w;
+    long long nn = (long long)n;
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (long long r = 0; r < nn; r++) {
+        const uint16_t* row = w16 + (size_t)r * m;
+        float s = 0.0f;
+        for (size_t j = 0; j < m; j++) s += orc_f16_to_f32(row[j]) * x[j];
+        y[r] = s + (bias ? bias[r] : 0.0f);
+    }
+}
+
+/* matmul_q4_0 dispatch, kernels.rs:256-265: AVX2+FMA when present, else scalar. */
+void orc_matmul_q4_0(float* y, const uint8_t* w, size_t w_len, const float* x,
+                     const float* bias, size_t n, size_t m) {
+    if (orc_have_avx2_fma())
+        orc_matmul_q4_0_avx2(y, w, w_len, x, bias, n, m);
+    else
+        orc_matmul_q4_0_scalar(y, w, w_len, x, bias, n, m);
+}
+
+/* matmul_f16 dispatch, kernels.rs:571-586. */
+void orc_matmul_f16(float* y, const uint8_t* w, size_t w_len, const float* x,
+                    const float* bias, size_t n, size_t m) {
+    if (orc_have_avx2_fma() && orc_have_f16c())
+        orc_matmul_f16_avx2(y, w, w_len, x, bias, n, m);
+    else
+        orc_matmul_f16_scalar(y, w, w_len, x, bias, n, m);
+}
+
+/* turbo::batch_matmul Q4_0 / FP16 arms, turbo.rs:306-333: one GEMV per token,
+ * X [batch][m] -> Y [batch][n], no bias.  dtype uses hypno's DType codes
+ * (dtype.rs:4-15): 1 = FP16, 3 = Q4_0.  Returns 0, or -1 for another dtype. */
+int orc_batch_matmul(float* y, const uint8_t* w, size_t w_len, int dtype, const float* x,
+                     size_t n, size_t m, size_t batch) {
+    for (size_t t = 0; t < batch; t++) {
+        if (dtype == 3)
+            orc_matmul_q4_0(y + t * n, w, w_len, x + t * m, NULL, n, m);
+        else if (dtype == 1)
+            orc_matmul_f16(y + t * n, w, w_len, x + t * m, NULL, n, m);
+        else
+            return -1;
+    }
+    return 0;
+}
+
+/* fp64 brute force: dequantise the whole flattened tensor (quant.rs:120-132),
+ * then y[r] = sum_k w[r*m+k] * x[k] in double, + bias.  Elements beyond the
+ * last whole block in w_len contribute nothing (kernels.rs:374). */
+void orc_matmul_q4_0_f64(double* y, const uint8_t* w, size_t w_len, const float* x,
+                         const float* bias, size_t n, size_t m) {
+    size_t avail = (w_len / Q4_BLOCK_BYTES) * 32;
+    long long nn = (long long)n;
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (long long r = 0; r < nn; r++) {
+        double s = 0.0;
+        float deq[32];
+        size_t cur_block = (size_t)-1;
+        for (size_t k = 0; k < m; k++) {
+            size_t e = (size_t)r * m + k;
+            if (e >= avail) break;
+            size_t b = e / 32;
+            if (b != cur_block) { deq_block(w + b * Q4_BLOCK_BYTES, deq); cur_block = b; }
+            s += (double)deq[e % 32] * (double)x[k];
+        }
+        y[r] = s + (bias ? (double)bias[r] : 0.0);
+    }
+}
+
+void orc_matmul_f16_f64(double* y, const uint8_t* w, const float* x, const float* bias,
+                        size_t n, size_t m) {
+    const uint16_t* w16 = (const uint16_t*)w;
+    long long nn = (long long)n;
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (long long r = 0; r < nn; r++) {
+        double s = 0.0;
+        for (size_t k = 0; k < m; k++)
+            s += (double)orc_f16_to_f32(w16[(size_t)r * m + k]) * (double)x[k];
+        y[r] = s + (bias ? (double)bias[r] : 0.0);
+    }
+}
+
+/* Sum of |w_rk * x_k| per row (the conditioning denominator for the
+ * tolerance report). */
+void orc_matmul_q4_0_absdot_f64(double* y, const uint8_t* w, size_t w_len, const float* x,
+                                size_t n, size_t m) {
+    size_t avail = (w_len / Q4_BLOCK_BYTES) * 32;
+    long long nn = (long long)n;
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (long long r = 0; r < nn; r++) {
+        double s = 0.0;
+        float deq[32];
+        size_t cur_block = (size_t)-1;
+        for (size_t k = 0; k < m; k++) {
+            size_t e = (size_t)r * m + k;
+            if (e >= avail) break;
+            size_t b = e / 32;
+            if (b != cur_block) { deq_block(w + b * Q4_BLOCK_BYTES, deq); cur_block = b; }
+            s += fabs((double)deq[e % 32] * (double)x[k]);
+        }
+        y[r] = s;
+    }
+}
