@@ -1,0 +1,307 @@
+#!/usr/bin/env python3
+"""Q4_0 matmul benchmark on one MI355X.
+
+Headline workload: the full TinyLlama-1.1B decode
+step weight stream, M = 1, Q4_0, 22 layers x {q, k, v, o, gate, up, down}
+(544,997,376 weight bytes, larger than the 256 MB Infinity Cache, so every
+step streams from HBM).  One step = the 154 GEMVs in decode order, replayed
+from a HIP graph.  value = weight bytes / step time (GB/s).
+
+Also reported, in the same JSON line:
+  roofline      the decode GEMV kernel's weight bytes / its average launch
+                duration (HIP events around each launch on the launch stream)
+                against the 8 TB/s HBM peak;
+  cpu_baseline  the CPU restatement of hypno's AVX2 kernel (oracle/) on this
+                host, on a bounded sample (layer 0's seven matrices);
+  secondary     prefill GEMM TFLOP/s at Llama-3.2-3B MLP shapes (M = 512,
+                config 3) and Mistral-7B decode GEMV GB/s with >= 512 MB of
+                rotating weight copies (config 4).
+
+Inputs are synthetic: weights N(0, 0.02) from a seeded torch generator,
+quantised on the GPU by the bit-exact Q4_0 quantizer; activations N(0, 1).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "Q4_0 GEMV weight GB/s (% HBM peak); prefill GEMM TFLOPS at 7B shapes"
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+
+# TinyLlama-1.1B per-layer projections (n = output rows, m = input dim)
+TINYLLAMA = [("q", 2048, 2048), ("k", 256, 2048), ("v", 256, 2048), ("o", 2048, 2048),
+             ("gate", 5632, 2048), ("up", 5632, 2048), ("down", 2048, 5632)]
+LAYERS = 22
+ALIGN = 64  # .hypno tensor alignment (format.rs:10)
+
+
+def q4_bytes(n, m):
+    return n * m // 32 * 18
+
+
+class Lib:
+    def __init__(self):
+        from hypno_amd import _lib
+        self.lib = _lib.load()
+        self.check = _lib.check
+
+    def quantize(self, out_ptr, src, stream):
+        self.check(self.lib.hypno_hip_quantize_q4_0_dev(ctypes.c_void_p(out_ptr),
+                                                        ctypes.c_void_p(src.data_ptr()),
+                                                        src.numel(), stream), "quantize")
+
+    def q4(self, y, w, w_len, x, n, m, batch, stream):
+        return self.lib.hypno_hip_matmul_q4_0_dev(y, w, w_len, x, None, n, m, batch, stream)
+
+
+def make_q4_arena(torch, lib, shapes, seed, stream):
+    """Quantised weights for `shapes` packed at 64-byte aligned offsets in one
+    device buffer (the .hypno layout).  Returns (arena, [(offset, nbytes)])."""
+    offs, total = [], 0
+    for n, m in shapes:
+        total = (total + ALIGN - 1) // ALIGN * ALIGN
+        offs.append((total, q4_bytes(n, m)))
+        total += q4_bytes(n, m)
+    arena = torch.empty(total, dtype=torch.uint8, device="cuda")
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    for (n, m), (off, _) in zip(shapes, offs):
+        w = torch.randn(n * m, generator=gen, device="cuda", dtype=torch.float32).mul_(0.02)
+        lib.quantize(arena.data_ptr() + off, w, stream)
+        del w
+    torch.cuda.synchronize()
+    return arena, offs
+
+
+def time_graph(torch, fn, steps, warmup):
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps, g
+
+
+def decode_stream(torch, lib, steps, warmup):
+    stream0 = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    shapes = [(n, m) for _ in range(LAYERS) for (_, n, m) in TINYLLAMA]
+    arena, offs = make_q4_arena(torch, lib, shapes, seed=1234, stream=stream0)
+    gen = torch.Generator(device="cuda").manual_seed(99)
+    xs = {m: torch.randn(m, generator=gen, device="cuda") for m in (2048, 5632)}
+    ys = {n: torch.empty(n, device="cuda") for n in (256, 2048, 5632)}
+    base = arena.data_ptr()
+    calls = [(ctypes.c_void_p(ys[n].data_ptr()), ctypes.c_void_p(base + off), nb,
+              ctypes.c_void_p(xs[m].data_ptr()), n, m)
+             for (n, m), (off, nb) in zip(shapes, offs)]
+    weight_bytes = sum(nb for _, nb in offs)
+
+    def step():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for y, w, nb, x, n, m in calls:
+            rc = lib.q4(y, w, nb, x, n, m, 1, st)
+            if rc:
+                lib.check(rc, "decode GEMV")
+
+    ms, graph = time_graph(torch, step, steps, warmup)
+
+    # Per-launch kernel durations (events on the launch stream) for the roofline.
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in calls]
+    durs = []
+    for rep in range(3):
+        for (a, b), (y, w, nb, x, n, m) in zip(evs, calls):
+            a.record()
+            lib.q4(y, w, nb, x, n, m, 1, st)
+            b.record()
+        torch.cuda.synchronize()
+        durs.append(sum(a.elapsed_time(b) for a, b in evs))
+    kern_ms = min(durs)  # sum over the 154 launches of one step
+    del graph
+    host_sample = [arena[off:off + nb].cpu().numpy() for off, nb in offs[:len(TINYLLAMA)]]
+    x_host = {m: xs[m].cpu().numpy() for m in xs}
+    return {
+        "ms": ms, "weight_bytes": weight_bytes, "launches": len(calls), "kern_ms": kern_ms,
+        "sample": host_sample, "x_host": x_host,
+    }
+
+
+def prefill_gemm(torch, lib, reps=10):
+    """Config 3: M = 512 tokens, Llama-3.2-3B MLP (gate/up 8192x3072, down 3072x8192)."""
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    shapes = [(8192, 3072), (8192, 3072), (3072, 8192)]
+    arena, offs = make_q4_arena(torch, lib, shapes, seed=7, stream=st)
+    M = 512
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    out = {}
+    for name, (n, m), (off, nb) in zip(("gate", "up", "down"), shapes, offs):
+        x = torch.randn(M, m, generator=gen, device="cuda")
+        y = torch.empty(M, n, device="cuda")
+        args = (ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(arena.data_ptr() + off), nb,
+                ctypes.c_void_p(x.data_ptr()), n, m, M, st)
+        for _ in range(3):
+            lib.check(lib.q4(*args), "prefill GEMM")
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            lib.q4(*args)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        out[name] = round(2.0 * M * n * m / (ms * 1e-3) / 1e12, 2)
+    return {"workload": "Llama-3.2-3B MLP, M=512, Q4_0 (config 3); includes the fp16 "
+                        "activation pre-pass", "tflops": out,
+            "frac_fp16_peak": {k: round(v / FP16_PEAK_TFLOPS, 4) for k, v in out.items()}}
+
+
+def mistral_gemv(torch, lib, reps=20):
+    """Config 4 at M = 1: Mistral-7B projections, >= 512 MB of distinct copies rotated."""
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    res = {}
+    for name, n, m in (("q_o", 4096, 4096), ("k_v", 1024, 4096), ("gate_up", 14336, 4096),
+                       ("down", 4096, 14336)):
+        nb = q4_bytes(n, m)
+        copies = max(2, -(-512 * 2**20 // nb))
+        arena, offs = make_q4_arena(torch, lib, [(n, m)] * copies, seed=n + m, stream=st)
+        x = torch.randn(m, device="cuda")
+        y = torch.empty(n, device="cuda")
+        ptrs = [ctypes.c_void_p(arena.data_ptr() + off) for off, _ in offs]
+        xp, yp = ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr())
+        for p in ptrs[:4]:
+            lib.q4(yp, p, nb, xp, n, m, 1, st)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        total = 0
+        evs = []
+        for i in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            lib.q4(yp, ptrs[i % copies], nb, xp, n, m, 1, st)
+            b.record()
+            evs.append((a, b))
+        torch.cuda.synchronize()
+        durs = sorted(a.elapsed_time(b) for a, b in evs)
+        med = durs[len(durs) // 2]
+        res[name] = round(nb / (med * 1e-3) / 1e9, 1)
+        del arena
+        torch.cuda.empty_cache()
+    return {"workload": "Mistral-7B decode GEMV M=1 (config 4), median event time per launch, "
+                        f">= 512 MB rotating copies", "weight_gbs": res,
+            "frac_hbm_peak": {k: round(v / HBM_PEAK_GBS, 4) for k, v in res.items()}}
+
+
+def cpu_baseline(sample, x_host, seconds):
+    """hypno's AVX2 Q4_0 kernel (restated in oracle/) on this host's cores."""
+    from oracle import oracle as orc
+    threads = max(1, min(16, os.cpu_count() or 1))
+    orc.set_threads(threads)
+    mats = list(zip(sample, TINYLLAMA))
+    for q, (_, n, m) in mats:  # warm-up (bench.rs:121)
+        orc.matmul_q4_0(q, x_host[m], None, n, m)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        for q, (_, n, m) in mats:
+            orc.matmul_q4_0(q, x_host[m], None, n, m)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and reps >= 3:
+            break
+    layer_bytes = sum(q.size for q in sample)
+    gbs = layer_bytes * reps / el / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "avx2": orc.have_avx2_fma(),
+            "sample": f"TinyLlama layer 0 (7 GEMVs, {layer_bytes} weight bytes) x {reps} reps "
+                      f"in {el:.1f} s, OpenMP row-parallel"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              "(every GPU box here has one GPU)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    lib = Lib()
+
+    print("[bench] decode stream: building 545 MB of Q4_0 weights", file=sys.stderr, flush=True)
+    d = decode_stream(torch, lib, args.steps, args.warmup)
+    value = d["weight_bytes"] / (d["ms"] * 1e-3) / 1e9
+    achieved = d["weight_bytes"] / (d["kern_ms"] * 1e-3) / 1e9
+    print(f"[bench] decode stream {d['ms']:.4f} ms/step, {value:.1f} GB/s", file=sys.stderr,
+          flush=True)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(d["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic: weights N(0,0.02) seeded, Q4_0-quantised on GPU; x N(0,1)",
+        "config": {
+            "workload": "TinyLlama-1.1B decode-step Q4_0 weight stream (configs[1]): 22 layers "
+                        "x {q,k,v,o,gate,up,down} GEMV, M=1, replayed as one HIP graph",
+            "weight_bytes": d["weight_bytes"],
+            "launches_per_step": d["launches"],
+            "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "q4_0_gemv_fast_kernel",
+            "avg_launch_us": round(d["kern_ms"] * 1e3 / d["launches"], 3),
+            "bytes_per_launch_avg": d["weight_bytes"] // d["launches"],
+        },
+    }
+    if not args.no_secondary:
+        print("[bench] secondary: prefill GEMM and Mistral GEMV", file=sys.stderr, flush=True)
+        line["secondary"] = {"prefill_gemm": prefill_gemm(torch, lib),
+                             "mistral_gemv": mistral_gemv(torch, lib)}
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_baseline(d["sample"], d["x_host"], args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

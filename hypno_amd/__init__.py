@@ -1,0 +1,23 @@
+"""hypno_amd: hypno's Q4_0 / FP16 quantized matmul path, native on MI355X (gfx950).
+
+The computation lives in libhypno_hip.so (hand-written HIP kernels behind the
+C ABI of include/hypno_hip.h); this package is its Python face and mirrors
+the reference's function names (see hypno_amd.kernels).
+"""
+from .kernels import (  # noqa: F401
+    DType,
+    HypnoHipError,
+    batch_matmul,
+    dequantize_q4_0,
+    device_count,
+    matmul_f16,
+    matmul_q4_0,
+    matmul_vec_auto,
+    matmul_vec_f16,
+    matmul_vec_q4_0,
+    quantize_f32_to_q4_0,
+    register_weight,
+    unregister_weight,
+)
+
+__version__ = "0.1.0"

@@ -1,0 +1,68 @@
+"""Loads libhypno_hip.so (built in-tree by hypno_amd.build) through ctypes.
+
+There is no fallback: if the library is missing or does not export a symbol
+of include/hypno_hip.h, importing the matmul API raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libhypno_hip.so")
+
+# Every entry point of include/hypno_hip.h: name -> (restype, argtypes).
+_vp, _sz, _i, _u32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_uint32
+SIGNATURES = {
+    "hypno_hip_abi_version": (_i, []),
+    "hypno_hip_strerror": (ctypes.c_char_p, [_i]),
+    "hypno_hip_last_error": (ctypes.c_char_p, []),
+    "hypno_hip_device_count": (_i, []),
+    "hypno_hip_matmul_q4_0": (_i, [_vp, _vp, _sz, _vp, _vp, _sz, _sz]),
+    "hypno_hip_matmul_f16": (_i, [_vp, _vp, _sz, _vp, _vp, _sz, _sz]),
+    "hypno_hip_matmul_vec_auto": (_i, [_vp, _vp, _sz, _u32, _vp, _vp, _sz, _sz]),
+    "hypno_hip_batch_matmul": (_i, [_vp, _vp, _sz, _u32, _vp, _sz, _sz, _sz]),
+    "hypno_hip_weight_register": (_i, [_vp, _sz]),
+    "hypno_hip_weight_unregister": (_i, [_vp]),
+    "hypno_hip_matmul_q4_0_dev": (_i, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "hypno_hip_matmul_f16_dev": (_i, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "hypno_hip_quantize_q4_0_dev": (_i, [_vp, _vp, _sz, _vp]),
+    "hypno_hip_dequantize_q4_0_dev": (_i, [_vp, _vp, _sz, _vp]),
+    "hypno_hip_stream_synchronize": (_i, [_vp]),
+}
+
+_lib = None
+
+
+class HypnoHipError(RuntimeError):
+    """A non-zero status from libhypno_hip (the reference panics instead)."""
+
+    def __init__(self, status: int, where: str):
+        lib = _lib
+        detail = lib.hypno_hip_last_error().decode() if lib else ""
+        name = lib.hypno_hip_strerror(status).decode() if lib else str(status)
+        super().__init__(f"{where}: {name} (status {status}): {detail}")
+        self.status = status
+
+
+def load():
+    """Return the loaded library; raises if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python -m hypno_amd.build` "
+            "(hypno_amd has no CPU fallback)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)  # AttributeError if the export is missing
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(status: int, where: str) -> None:
+    if status != 0:
+        raise HypnoHipError(status, where)

@@ -1,0 +1,395 @@
+// C ABI of the gfx950 Q4_0 / FP16 matmul library (declared in
+// include/hypno_hip.h).  Validates arguments, picks a kernel by shape and
+// alignment, and owns the device-side state: per-device streams and staging
+// buffers for the host-slice entry points, per-stream GEMM workspaces, and the
+// weight-residency registry.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/hypno_hip.h"
+#include "common.hpp"
+
+namespace {
+
+using namespace hypno;
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int status, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return status;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  const int st = e == hipErrorOutOfMemory ? HYPNO_HIP_ENOMEM : HYPNO_HIP_EDEVICE;
+  return fail(st, "%s: %s", what, hipGetErrorString(e));
+}
+
+// Minimum token count routed to the MFMA GEMM.
+constexpr size_t kGemmMinBatch = 16;
+
+struct DevBuf {
+  void* p = nullptr;
+  size_t cap = 0;
+};
+
+// Grow-only device buffer; `sync` is the stream whose queued work may still use
+// the old allocation.
+hipError_t ensure(DevBuf& b, size_t bytes, hipStream_t sync) {
+  if (b.cap >= bytes && b.p) return hipSuccess;
+  if (b.p) {
+    hipError_t e = hipStreamSynchronize(sync);
+    if (e != hipSuccess) return e;
+    (void)hipFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+  }
+  const size_t want = bytes < 256 ? 256 : bytes;
+  hipError_t e = hipMalloc(&b.p, want);
+  if (e != hipSuccess) {
+    b.p = nullptr;
+    return e;
+  }
+  b.cap = want;
+  return hipSuccess;
+}
+
+struct DeviceState {
+  bool init = false;
+  int cus = 256;
+  hipStream_t stream = nullptr;  // used by the host-slice entry points
+  DevBuf w, x, y, bias;          // host-slice staging
+  std::map<hipStream_t, DevBuf> workspaces;
+};
+
+struct Registered {
+  void* dev_ptr;
+  size_t len;
+  int device;
+};
+
+std::mutex g_host_mu;  // serialises host-slice calls (staging buffers, registry copies)
+std::mutex g_mu;       // guards the maps below and the per-stream workspaces
+std::map<int, DeviceState> g_dev;
+std::map<const uint8_t*, Registered> g_weights;
+
+int current_device(int* dev) {
+  hipError_t e = hipGetDevice(dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  return HYPNO_HIP_OK;
+}
+
+// Caller holds g_mu.
+int device_state(DeviceState** out) {
+  int dev = 0;
+  int st = current_device(&dev);
+  if (st) return st;
+  DeviceState& d = g_dev[dev];
+  if (!d.init) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        cus > 0)
+      d.cus = cus;
+    hipError_t e = hipStreamCreateWithFlags(&d.stream, hipStreamNonBlocking);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamCreate");
+    d.init = true;
+  }
+  *out = &d;
+  return HYPNO_HIP_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+bool mul_overflows(size_t a, size_t b) { return a != 0 && b > SIZE_MAX / a; }
+
+// --- dispatch on device pointers (caller holds no lock) ---------------------
+
+int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const float* bias,
+             size_t n, size_t m, size_t batch, hipStream_t s) {
+  if (n == 0 || batch == 0) return HYPNO_HIP_OK;
+  if (!y || !x) return fail(HYPNO_HIP_EINVAL, "y and x must not be NULL");
+  if (!w && w_len) return fail(HYPNO_HIP_EINVAL, "w_q is NULL but w_len > 0");
+  if (mul_overflows(n, batch) || mul_overflows(m, batch) || mul_overflows(n, m))
+    return fail(HYPNO_HIP_EINVAL, "shape overflows size_t");
+  int cus = 256;
+  DeviceState* ds = nullptr;
+  {
+    std::lock_guard<std::mutex> g(g_mu);
+    int st = device_state(&ds);
+    if (st) return st;
+    cus = ds->cus;
+  }
+  hipError_t e;
+  if (batch >= kGemmMinBatch && q4_0_gemm_ok(w, w_len, n, m, batch)) {
+    void* ws = nullptr;
+    {
+      std::lock_guard<std::mutex> g(g_mu);
+      DevBuf& b = ds->workspaces[s];
+      e = ensure(b, gemm_workspace_bytes(batch, m), s);
+      if (e != hipSuccess) return hip_fail(e, "GEMM workspace");
+      ws = b.p;
+    }
+    e = launch_q4_0_gemm(y, w, x, bias, n, m, batch, ws, s);
+    if (e != hipSuccess) return hip_fail(e, "q4_0 GEMM launch");
+    return HYPNO_HIP_OK;
+  }
+  if (q4_0_gemv_fast_ok(w, w_len, n, m) && aligned16(x)) {
+    for (size_t t = 0; t < batch; t++) {
+      e = launch_q4_0_gemv_fast(y + t * n, w, x + t * m, bias, n, m, cus, s);
+      if (e != hipSuccess) return hip_fail(e, "q4_0 GEMV launch");
+    }
+    return HYPNO_HIP_OK;
+  }
+  e = launch_q4_0_generic(y, w, w_len, x, bias, n, m, batch, s);
+  if (e != hipSuccess) return hip_fail(e, "q4_0 generic launch");
+  return HYPNO_HIP_OK;
+}
+
+int f16_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const float* bias,
+            size_t n, size_t m, size_t batch, hipStream_t s) {
+  if (n == 0 || batch == 0) return HYPNO_HIP_OK;
+  if (!y || !x) return fail(HYPNO_HIP_EINVAL, "y and x must not be NULL");
+  if (mul_overflows(n, m) || mul_overflows(n * m, 2) || mul_overflows(n, batch) ||
+      mul_overflows(m, batch))
+    return fail(HYPNO_HIP_EINVAL, "shape overflows size_t");
+  // kernels.rs:550 slices w16[r*m..(r+1)*m]: a short buffer is a panic there.
+  if (w_len < 2 * n * m)
+    return fail(HYPNO_HIP_EINVAL, "fp16 weights: w_len %zu < 2*n*m = %zu", w_len, 2 * n * m);
+  if (!w && n * m) return fail(HYPNO_HIP_EINVAL, "w is NULL");
+  int cus = 256;
+  DeviceState* ds = nullptr;
+  {
+    std::lock_guard<std::mutex> g(g_mu);
+    int st = device_state(&ds);
+    if (st) return st;
+    cus = ds->cus;
+  }
+  hipError_t e;
+  if (batch >= kGemmMinBatch && f16_gemm_ok(w, n, m, batch)) {
+    void* ws = nullptr;
+    {
+      std::lock_guard<std::mutex> g(g_mu);
+      DevBuf& b = ds->workspaces[s];
+      e = ensure(b, gemm_workspace_bytes(batch, m), s);
+      if (e != hipSuccess) return hip_fail(e, "GEMM workspace");
+      ws = b.p;
+    }
+    e = launch_f16_gemm(y, w, x, bias, n, m, batch, ws, s);
+    if (e != hipSuccess) return hip_fail(e, "f16 GEMM launch");
+    return HYPNO_HIP_OK;
+  }
+  if (f16_gemv_fast_ok(w, n, m) && aligned16(x)) {
+    for (size_t t = 0; t < batch; t++) {
+      e = launch_f16_gemv_fast(y + t * n, w, x + t * m, bias, n, m, cus, s);
+      if (e != hipSuccess) return hip_fail(e, "f16 GEMV launch");
+    }
+    return HYPNO_HIP_OK;
+  }
+  e = launch_f16_generic(y, w, x, bias, n, m, batch, s);
+  if (e != hipSuccess) return hip_fail(e, "f16 generic launch");
+  return HYPNO_HIP_OK;
+}
+
+// --- host-slice path ----------------------------------------------------------
+
+int host_matmul(float* y, const uint8_t* w, size_t w_len, uint32_t dtype, const float* x,
+                const float* bias, size_t n, size_t m, size_t batch) {
+  if (dtype == HYPNO_DTYPE_FP32 || dtype == HYPNO_DTYPE_Q8_0)
+    return fail(HYPNO_HIP_ENOTSUP, "dtype %u is not on the Q4_0/FP16 path", dtype);
+  if (dtype != HYPNO_DTYPE_Q4_0 && dtype != HYPNO_DTYPE_FP16)
+    return fail(HYPNO_HIP_EINVAL, "unknown dtype %u", dtype);
+  if (n == 0 || batch == 0) return HYPNO_HIP_OK;
+  if (!y || (!x && m) || (!w && w_len))
+    return fail(HYPNO_HIP_EINVAL, "NULL pointer argument");
+  if (mul_overflows(n, batch) || mul_overflows(m, batch) || mul_overflows(n * batch, 4) ||
+      mul_overflows(m * batch, 4))
+    return fail(HYPNO_HIP_EINVAL, "shape overflows size_t");
+  if (dtype == HYPNO_DTYPE_FP16 && (mul_overflows(n, m) || w_len < 2 * n * m))
+    return fail(HYPNO_HIP_EINVAL, "fp16 weights: w_len %zu < 2*n*m", w_len);
+
+  // One host-slice call at a time: the staging buffers and the registry's
+  // device copies are shared by all callers.
+  std::lock_guard<std::mutex> hg(g_host_mu);
+  DeviceState* ds = nullptr;
+  int dev = 0;
+  const uint8_t* dw = nullptr;
+  bool resident = false;
+  {
+    std::lock_guard<std::mutex> g(g_mu);
+    int st = device_state(&ds);
+    if (st) return st;
+    (void)hipGetDevice(&dev);
+    auto it = g_weights.find(w);
+    if (it != g_weights.end() && it->second.len == w_len && it->second.device == dev) {
+      dw = (const uint8_t*)it->second.dev_ptr;
+      resident = true;
+    }
+  }
+  hipStream_t s = ds->stream;
+  hipError_t e;
+  int st;
+
+  if (!resident && w_len) {
+    if ((e = ensure(ds->w, w_len, s)) != hipSuccess) return hip_fail(e, "weight staging");
+    if ((e = hipMemcpyAsync(ds->w.p, w, w_len, hipMemcpyHostToDevice, s)) != hipSuccess)
+      return hip_fail(e, "weight upload");
+    dw = (const uint8_t*)ds->w.p;
+  }
+  const size_t xb = m * batch * 4, yb = n * batch * 4;
+  if ((e = ensure(ds->x, xb, s)) != hipSuccess) return hip_fail(e, "x staging");
+  if ((e = ensure(ds->y, yb, s)) != hipSuccess) return hip_fail(e, "y staging");
+  if (xb && (e = hipMemcpyAsync(ds->x.p, x, xb, hipMemcpyHostToDevice, s)) != hipSuccess)
+    return hip_fail(e, "x upload");
+  float* db = nullptr;
+  if (bias) {
+    if ((e = ensure(ds->bias, n * 4, s)) != hipSuccess) return hip_fail(e, "bias staging");
+    if ((e = hipMemcpyAsync(ds->bias.p, bias, n * 4, hipMemcpyHostToDevice, s)) != hipSuccess)
+      return hip_fail(e, "bias upload");
+    db = (float*)ds->bias.p;
+  }
+  if (dtype == HYPNO_DTYPE_Q4_0)
+    st = q4_0_dev((float*)ds->y.p, dw, w_len, (const float*)ds->x.p, db, n, m, batch, s);
+  else
+    st = f16_dev((float*)ds->y.p, dw, w_len, (const float*)ds->x.p, db, n, m, batch, s);
+  if (st) {
+    (void)hipStreamSynchronize(s);
+    return st;
+  }
+  if ((e = hipMemcpyAsync(y, ds->y.p, yb, hipMemcpyDeviceToHost, s)) != hipSuccess)
+    return hip_fail(e, "y download");
+  if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "stream synchronize");
+  return HYPNO_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hypno_hip_abi_version(void) { return HYPNO_HIP_ABI_VERSION; }
+
+const char* hypno_hip_strerror(int status) {
+  switch (status) {
+    case HYPNO_HIP_OK: return "ok";
+    case HYPNO_HIP_EINVAL: return "invalid argument";
+    case HYPNO_HIP_ENOMEM: return "out of memory";
+    case HYPNO_HIP_EDEVICE: return "device or HIP runtime error";
+    case HYPNO_HIP_ENOTSUP: return "dtype not supported on this path";
+    default: return "unknown status";
+  }
+}
+
+const char* hypno_hip_last_error(void) { return g_last_error.c_str(); }
+
+int hypno_hip_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+int hypno_hip_matmul_q4_0(float* y, const uint8_t* w_q, size_t w_len, const float* x,
+                          const float* bias, size_t n, size_t m) {
+  return host_matmul(y, w_q, w_len, HYPNO_DTYPE_Q4_0, x, bias, n, m, 1);
+}
+
+int hypno_hip_matmul_f16(float* y, const uint8_t* w, size_t w_len, const float* x,
+                         const float* bias, size_t n, size_t m) {
+  return host_matmul(y, w, w_len, HYPNO_DTYPE_FP16, x, bias, n, m, 1);
+}
+
+int hypno_hip_matmul_vec_auto(float* y, const uint8_t* w, size_t w_len, uint32_t dtype,
+                              const float* x, const float* bias, size_t n, size_t m) {
+  return host_matmul(y, w, w_len, dtype, x, bias, n, m, 1);
+}
+
+int hypno_hip_batch_matmul(float* y, const uint8_t* w, size_t w_len, uint32_t dtype,
+                           const float* x, size_t n, size_t dim, size_t batch) {
+  return host_matmul(y, w, w_len, dtype, x, nullptr, n, dim, batch);
+}
+
+int hypno_hip_weight_register(const uint8_t* host, size_t len) {
+  if (!host || !len) return fail(HYPNO_HIP_EINVAL, "register: NULL or empty buffer");
+  std::lock_guard<std::mutex> hg(g_host_mu);
+  std::lock_guard<std::mutex> g(g_mu);
+  DeviceState* ds = nullptr;
+  int st = device_state(&ds);
+  if (st) return st;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  auto it = g_weights.find(host);
+  if (it != g_weights.end()) {
+    if (it->second.len == len && it->second.device == dev) return HYPNO_HIP_OK;
+    (void)hipFree(it->second.dev_ptr);
+    g_weights.erase(it);
+  }
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, len);
+  if (e != hipSuccess) return hip_fail(e, "register: hipMalloc");
+  e = hipMemcpy(p, host, len, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return hip_fail(e, "register: upload");
+  }
+  g_weights[host] = Registered{p, len, dev};
+  return HYPNO_HIP_OK;
+}
+
+int hypno_hip_weight_unregister(const uint8_t* host) {
+  std::lock_guard<std::mutex> hg(g_host_mu);
+  std::lock_guard<std::mutex> g(g_mu);
+  auto it = g_weights.find(host);
+  if (it == g_weights.end()) return fail(HYPNO_HIP_EINVAL, "unregister: pointer not registered");
+  (void)hipDeviceSynchronize();
+  (void)hipFree(it->second.dev_ptr);
+  g_weights.erase(it);
+  return HYPNO_HIP_OK;
+}
+
+int hypno_hip_matmul_q4_0_dev(float* y, const uint8_t* w_q, size_t w_len, const float* x,
+                              const float* bias, size_t n, size_t m, size_t batch,
+                              void* stream) {
+  return q4_0_dev(y, w_q, w_len, x, bias, n, m, batch, (hipStream_t)stream);
+}
+
+int hypno_hip_matmul_f16_dev(float* y, const uint8_t* w, size_t w_len, const float* x,
+                             const float* bias, size_t n, size_t m, size_t batch, void* stream) {
+  return f16_dev(y, w, w_len, x, bias, n, m, batch, (hipStream_t)stream);
+}
+
+int hypno_hip_quantize_q4_0_dev(uint8_t* out, const float* src, size_t n_elems, void* stream) {
+  const size_t nb = n_elems / kBlockElems;
+  if (nb == 0) return HYPNO_HIP_OK;
+  if (!out || !src) return fail(HYPNO_HIP_EINVAL, "quantize: NULL pointer");
+  hipError_t e = launch_quantize_q4_0(out, src, nb, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "quantize launch");
+  return HYPNO_HIP_OK;
+}
+
+int hypno_hip_dequantize_q4_0_dev(float* out, const uint8_t* q, size_t q_len, void* stream) {
+  const size_t nb = q_len / kBlockBytes;
+  if (nb == 0) return HYPNO_HIP_OK;
+  if (!out || !q) return fail(HYPNO_HIP_EINVAL, "dequantize: NULL pointer");
+  hipError_t e = launch_dequantize_q4_0(out, q, nb, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "dequantize launch");
+  return HYPNO_HIP_OK;
+}
+
+int hypno_hip_stream_synchronize(void* stream) {
+  hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  return HYPNO_HIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,79 @@
+// Shared device helpers and internal launcher declarations for the gfx950
+// Q4_0 / FP16 matmul library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace hypno {
+
+constexpr int kBlockElems = 32;  // Q4_0 block: 32 weights (dtype.rs:40-45)
+constexpr int kBlockBytes = 18;  // fp16 scale + 16 packed bytes (dtype.rs:48-54)
+
+// f16 bits -> f32, exact (v_cvt_f32_f16).
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
+  _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits);
+  return (float)h;
+}
+
+// Wave-wide sum (wave64) with xor butterflies; every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Dot product of 8 nibbles of one packed dword with 8 activations:
+// byte i of `dw` holds element 2i (low nibble) and 2i+1 (high nibble);
+// returns sum_j nib_j * x_j (nibbles in 0..15, the -8 offset is applied by
+// the caller through the block's activation sum).
+__device__ __forceinline__ float dot8_nib(uint32_t dw, const float* x) {
+  uint32_t lo = dw & 0x0F0F0F0Fu;
+  uint32_t hi = (dw >> 4) & 0x0F0F0F0Fu;
+  // Opaque to the optimiser: otherwise it folds the byte masks into 4-bit
+  // field extracts and loses v_cvt_f32_ubyte{1,2,3} (one op per nibble).
+  asm volatile("" : "+v"(lo), "+v"(hi));
+  float a = (float)(lo & 0xFFu) * x[0];
+  a = fmaf((float)(hi & 0xFFu), x[1], a);
+  a = fmaf((float)((lo >> 8) & 0xFFu), x[2], a);
+  a = fmaf((float)((hi >> 8) & 0xFFu), x[3], a);
+  a = fmaf((float)((lo >> 16) & 0xFFu), x[4], a);
+  a = fmaf((float)((hi >> 16) & 0xFFu), x[5], a);
+  a = fmaf((float)(lo >> 24), x[6], a);
+  a = fmaf((float)(hi >> 24), x[7], a);
+  return a;
+}
+
+// Launchers (all asynchronous on `stream`; return hipSuccess or the launch error).
+hipError_t launch_quantize_q4_0(uint8_t* out, const float* src, size_t n_blocks, hipStream_t s);
+hipError_t launch_dequantize_q4_0(float* out, const uint8_t* q, size_t n_blocks, hipStream_t s);
+
+// Any shape / alignment / short buffer; one wave per (token, row).
+hipError_t launch_q4_0_generic(float* y, const uint8_t* w, size_t w_len, const float* x,
+                               const float* bias, size_t n, size_t m, size_t batch,
+                               hipStream_t s);
+// Fast decode GEMV for one token.  Requires m % 256 == 0, w 16-byte aligned,
+// w_len >= n*m/32*18, m <= 65536.
+bool q4_0_gemv_fast_ok(const uint8_t* w, size_t w_len, size_t n, size_t m);
+hipError_t launch_q4_0_gemv_fast(float* y, const uint8_t* w, const float* x, const float* bias,
+                                 size_t n, size_t m, int num_cus, hipStream_t s);
+
+// MFMA prefill GEMM.  Requires m % 64 == 0, w 4-byte aligned, w_len full.
+// `xh` is a device workspace of gemm_q4_0_workspace_bytes(batch, m) bytes.
+bool q4_0_gemm_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t batch);
+size_t gemm_workspace_bytes(size_t batch, size_t m);
+hipError_t launch_q4_0_gemm(float* y, const uint8_t* w, const float* x, const float* bias,
+                            size_t n, size_t m, size_t batch, void* workspace, hipStream_t s);
+
+// FP16 weights.
+hipError_t launch_f16_generic(float* y, const uint8_t* w, const float* x, const float* bias,
+                              size_t n, size_t m, size_t batch, hipStream_t s);
+bool f16_gemv_fast_ok(const uint8_t* w, size_t n, size_t m);
+hipError_t launch_f16_gemv_fast(float* y, const uint8_t* w, const float* x, const float* bias,
+                                size_t n, size_t m, int num_cus, hipStream_t s);
+bool f16_gemm_ok(const uint8_t* w, size_t n, size_t m, size_t batch);
+hipError_t launch_f16_gemm(float* y, const uint8_t* w, const float* x, const float* bias,
+                           size_t n, size_t m, size_t batch, void* workspace, hipStream_t s);
+
+}  // namespace hypno

@@ -1,0 +1,232 @@
+"""Python mirror of hypno's matmul interface for the Q4_0 / FP16 path.
+
+Same names, argument order and meaning as the reference (paths relative to
+crates/hypno/src/):
+
+    matmul_q4_0(y, w_q, x, bias, n, m)           kernels.rs:256
+    matmul_f16(y, w, x, bias, n, m)              kernels.rs:571
+    matmul_vec_q4_0 / matmul_vec_f16             ops.rs:15, ops.rs:20
+    matmul_vec_auto(y, w, dtype, x, bias, n, m)  ops.rs:25
+    batch_matmul(y, w, dtype, x, n, dim, batch, col_major)   turbo.rs:306
+    quantize_f32_to_q4_0(data) / dequantize_q4_0(q)          quant.rs:108 / :120
+
+`y` is written in place.  Arguments are either all torch tensors on the GPU
+(the device path: asynchronous on torch's current stream, no host copies) or
+all numpy arrays (the host-slice path of the C ABI: staged to the GPU and
+copied back).  Every computation runs in libhypno_hip on the GPU; there is
+no CPU implementation here.  Where the reference would panic (an
+out-of-bounds slice) these functions raise ValueError; a library failure
+raises HypnoHipError.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+
+import numpy as np
+
+from ._lib import HypnoHipError, check, load
+
+__all__ = [
+    "DType", "HypnoHipError", "matmul_q4_0", "matmul_f16", "matmul_vec_q4_0",
+    "matmul_vec_f16", "matmul_vec_auto", "batch_matmul", "quantize_f32_to_q4_0",
+    "dequantize_q4_0", "register_weight", "unregister_weight", "device_count",
+]
+
+
+class DType(enum.IntEnum):
+    """Tensor element types (dtype.rs:4-15), with the size rules of dtype.rs:40-70."""
+    FP32 = 0
+    FP16 = 1
+    Q8_0 = 2
+    Q4_0 = 3
+
+    def block_size(self) -> int:
+        return 32 if self in (DType.Q8_0, DType.Q4_0) else 1
+
+    def block_bytes(self) -> int:
+        return {DType.Q8_0: 34, DType.Q4_0: 18}.get(self, 0)
+
+    def data_bytes(self, n_elems: int) -> int:
+        if self == DType.FP32:
+            return n_elems * 4
+        if self == DType.FP16:
+            return n_elems * 2
+        return -(-n_elems // 32) * self.block_bytes()
+
+
+def device_count() -> int:
+    return int(load().hypno_hip_device_count())
+
+
+# --- argument handling ---------------------------------------------------------
+
+def _is_torch(a) -> bool:
+    return type(a).__module__.startswith("torch")
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _dev_ptr(t, dtype_name: str, what: str):
+    torch = _torch()
+    want = {"f32": torch.float32, "u8": torch.uint8}[dtype_name]
+    if not t.is_cuda:
+        raise ValueError(f"{what} must be a GPU tensor")
+    if t.dtype != want:
+        raise ValueError(f"{what} must be {want}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _host_ptr(a, dtype, what: str):
+    if not isinstance(a, np.ndarray):
+        raise ValueError(f"{what} must be a numpy array or a GPU torch tensor")
+    if a.dtype != dtype:
+        raise ValueError(f"{what} must be {np.dtype(dtype)}, got {a.dtype}")
+    if not a.flags.c_contiguous:
+        raise ValueError(f"{what} must be C-contiguous")
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _numel(a) -> int:
+    return int(a.numel()) if _is_torch(a) else int(a.size)
+
+
+def _nbytes(a) -> int:
+    return int(a.numel() * a.element_size()) if _is_torch(a) else int(a.nbytes)
+
+
+def _stream(device) -> ctypes.c_void_p:
+    torch = _torch()
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _check_lengths(y, x, bias, n, m, batch):
+    # The reference indexes y by row, x[..m] and bias[row]; a short slice panics.
+    if n < 0 or m < 0 or batch < 0:
+        raise ValueError("n, m and batch must be non-negative")
+    if _numel(y) != n * batch:
+        raise ValueError(f"y has {_numel(y)} elements, expected n*batch = {n * batch}")
+    if _numel(x) < m * batch:
+        raise ValueError(f"x has {_numel(x)} elements, expected at least {m * batch}")
+    if bias is not None and _numel(bias) < n:
+        raise ValueError(f"bias has {_numel(bias)} elements, expected at least {n}")
+
+
+def _matmul(y, w, dtype: DType, x, bias, n: int, m: int, batch: int) -> None:
+    _check_lengths(y, x, bias, n, m, batch)
+    lib = load()
+    tensors = [a for a in (y, w, x, bias) if a is not None]
+    on_gpu = [_is_torch(a) for a in tensors]
+    if all(on_gpu):
+        yp = _dev_ptr(y, "f32", "y")
+        wp = _dev_ptr(w, "u8", "w")
+        xp = _dev_ptr(x, "f32", "x")
+        bp = _dev_ptr(bias, "f32", "bias") if bias is not None else None
+        fn = {DType.Q4_0: lib.hypno_hip_matmul_q4_0_dev,
+              DType.FP16: lib.hypno_hip_matmul_f16_dev}.get(dtype)
+        if fn is None:
+            raise HypnoHipError(95, f"matmul dtype {dtype.name}")
+        check(fn(yp, wp, _nbytes(w), xp, bp, n, m, batch, _stream(y.device)),
+              f"matmul {dtype.name}")
+        return
+    if any(on_gpu):
+        raise ValueError("mixing GPU tensors and host arrays is not supported")
+    yp = _host_ptr(y, np.float32, "y")
+    wp = _host_ptr(w, np.uint8, "w")
+    xp = _host_ptr(x, np.float32, "x")
+    bp = _host_ptr(bias, np.float32, "bias") if bias is not None else None
+    if batch == 1:
+        check(lib.hypno_hip_matmul_vec_auto(yp, wp, w.nbytes, int(dtype), xp, bp, n, m),
+              f"matmul {dtype.name}")
+    else:
+        if bias is not None:
+            raise ValueError("batch_matmul takes no bias (turbo.rs:306-333)")
+        check(lib.hypno_hip_batch_matmul(yp, wp, w.nbytes, int(dtype), xp, n, m, batch),
+              f"batch_matmul {dtype.name}")
+
+
+# --- the reference's entry points --------------------------------------------------
+
+def matmul_q4_0(y, w_q, x, bias, n: int, m: int) -> None:
+    """y[n] = W_q[n][m] . x[m] (+ bias), Q4_0 weights (kernels.rs:256-265)."""
+    _matmul(y, w_q, DType.Q4_0, x, bias, n, m, 1)
+
+
+def matmul_f16(y, w, x, bias, n: int, m: int) -> None:
+    """y[n] = W[n][m] . x[m] (+ bias), fp16 weights as bytes (kernels.rs:571-586)."""
+    _matmul(y, w, DType.FP16, x, bias, n, m, 1)
+
+
+def matmul_vec_q4_0(y, w_q, x, bias, n: int, m: int) -> None:
+    """ops.rs:15-17."""
+    matmul_q4_0(y, w_q, x, bias, n, m)
+
+
+def matmul_vec_f16(y, w, x, bias, n: int, m: int) -> None:
+    """ops.rs:20-22."""
+    matmul_f16(y, w, x, bias, n, m)
+
+
+def matmul_vec_auto(y, w, dtype, x, bias, n: int, m: int) -> None:
+    """Dtype switch of ops.rs:25-38 for this path: FP16 and Q4_0.  FP32 and
+    Q8_0 weights are outside it and raise HypnoHipError (ENOTSUP)."""
+    dtype = DType(int(dtype))
+    if dtype not in (DType.Q4_0, DType.FP16):
+        raise HypnoHipError(95, f"matmul_vec_auto dtype {dtype.name}")
+    _matmul(y, w, dtype, x, bias, n, m, 1)
+
+
+def batch_matmul(y, w, dtype, x, n: int, dim: int, batch: int, col_major: bool = False) -> None:
+    """turbo::batch_matmul (turbo.rs:306-343) for FP16 / Q4_0 row-major weights:
+    X[batch][dim] -> Y[batch][n] in one GPU call.  The column-major Q4_0 layout
+    (kernels.rs:403-535) is outside this path and raises."""
+    dtype = DType(int(dtype))
+    if col_major:
+        raise HypnoHipError(95, "batch_matmul col_major")
+    if dtype not in (DType.Q4_0, DType.FP16):
+        raise HypnoHipError(95, f"batch_matmul dtype {dtype.name}")
+    _matmul(y, w, dtype, x, None, n, dim, batch)
+
+
+# --- codec (device) ---------------------------------------------------------------
+
+def quantize_f32_to_q4_0(data):
+    """quant.rs:108-117 on the GPU: floor(len/32) blocks, bit-exact.  `data` is
+    a float32 GPU tensor; returns a uint8 GPU tensor of blocks*18 bytes."""
+    torch = _torch()
+    src = data.reshape(-1)
+    nb = src.numel() // 32
+    out = torch.empty(nb * 18, dtype=torch.uint8, device=src.device)
+    check(load().hypno_hip_quantize_q4_0_dev(_dev_ptr(out, "u8", "out"),
+                                              _dev_ptr(src, "f32", "data"), src.numel(),
+                                              _stream(src.device)), "quantize_q4_0")
+    return out
+
+
+def dequantize_q4_0(q):
+    """quant.rs:120-132 on the GPU: floor(len/18) blocks -> fp32, bit-exact."""
+    torch = _torch()
+    nb = q.numel() // 18
+    out = torch.empty(nb * 32, dtype=torch.float32, device=q.device)
+    check(load().hypno_hip_dequantize_q4_0_dev(_dev_ptr(out, "f32", "out"),
+                                                _dev_ptr(q, "u8", "q"), q.numel(),
+                                                _stream(q.device)), "dequantize_q4_0")
+    return out
+
+
+# --- weight residency for the host-slice path -------------------------------------
+
+def register_weight(w: np.ndarray) -> None:
+    """Upload a host weight buffer once (the mmap'd slice of loader.rs:139-148);
+    later host-slice calls with the same array reuse the device copy."""
+    check(load().hypno_hip_weight_register(_host_ptr(w, np.uint8, "w"), w.nbytes),
+          "weight_register")
+
+
+def unregister_weight(w: np.ndarray) -> None:
+    check(load().hypno_hip_weight_unregister(_host_ptr(w, np.uint8, "w")), "weight_unregister")

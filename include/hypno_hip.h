@@ -1,0 +1,136 @@
+/*
+ * hypno_hip.h — C ABI of the MI355X (gfx950) Q4_0 / FP16 matmul library.
+ *
+ * Drop-in for hypno's quantized matmul path.  Paths in citations are relative
+ * to the hypno repository (crates/hypno/src/...).
+ *
+ * Conventions shared by every entry point:
+ *   - Rows are the flattened ranges [r*m, (r+1)*m) of the row-major weight
+ *     tensor, quantised in consecutive 32-element blocks (sft_convert.rs:261,
+ *     quant.rs:108).  A Q4_0 block is 18 bytes: fp16 scale d (little-endian)
+ *     then 16 bytes; byte i holds element 2i in its low nibble and element
+ *     2i+1 in its high nibble; weight = (nibble - 8) * d (quant.rs:10-34).
+ *     m need not be a multiple of 32: blocks then straddle rows
+ *     (kernels.rs:362-400).
+ *   - A weight buffer shorter than the tensor is not an error: a block whose
+ *     18 bytes lie past w_len contributes nothing (kernels.rs:275-277, :374).
+ *   - y is fully overwritten; bias may be NULL (kernels.rs:356).
+ *   - Results: fp32 accumulation for M = 1..15 tokens; for M >= 16 the Q4_0
+ *     and FP16 paths round activations to fp16 and run on MFMA (the scale of
+ *     each 32-block is applied to the MFMA partial in fp32).
+ *   - Every function returns a status (HYPNO_HIP_OK on success) and never
+ *     aborts the process.  hypno_hip_last_error() describes the last failure
+ *     on the calling thread.
+ *   - All functions are thread-safe.  Device-pointer ("_dev") entry points are
+ *     asynchronous on the given stream (NULL = the default stream).
+ */
+#ifndef HYPNO_HIP_H
+#define HYPNO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HYPNO_HIP_ABI_VERSION 1
+
+/* Status codes (errno-like values). */
+#define HYPNO_HIP_OK 0
+#define HYPNO_HIP_EINVAL 22   /* null pointer, bad shape or length, bad dtype */
+#define HYPNO_HIP_ENOMEM 12   /* device or pinned-host allocation failed */
+#define HYPNO_HIP_EDEVICE 5   /* HIP runtime / launch error, or no device */
+#define HYPNO_HIP_ENOTSUP 95  /* dtype outside this path (FP32, Q8_0) */
+
+/* Weight dtypes: hypno's DType codes (dtype.rs:4-15). */
+#define HYPNO_DTYPE_FP32 0u
+#define HYPNO_DTYPE_FP16 1u
+#define HYPNO_DTYPE_Q8_0 2u
+#define HYPNO_DTYPE_Q4_0 3u
+
+/* ABI version (HYPNO_HIP_ABI_VERSION of the built library). */
+int hypno_hip_abi_version(void);
+
+/* Static description of a status code. */
+const char* hypno_hip_strerror(int status);
+
+/* Detail of the last failure on the calling thread ("" if none). */
+const char* hypno_hip_last_error(void);
+
+/* Number of visible HIP devices (0 when there is none; never fails). */
+int hypno_hip_device_count(void);
+
+/* ---------------------------------------------------------------------------
+ * Host-slice entry points: same arguments as the reference functions, with
+ * the slice lengths the Rust signature carries made explicit.  Inputs are
+ * host memory; they are staged to the current device, computed there, and y
+ * is copied back before return.  A weight buffer registered with
+ * hypno_hip_weight_register() is not uploaded again.
+ * ------------------------------------------------------------------------- */
+
+/* Replaces kernels::matmul_q4_0(y, w_q, x, bias, n, m) (kernels.rs:256).
+ * y[n], w_q[w_len] (Q4_0 bytes), x[m], bias[n] or NULL. */
+int hypno_hip_matmul_q4_0(float* y, const uint8_t* w_q, size_t w_len, const float* x,
+                          const float* bias, size_t n, size_t m);
+
+/* Replaces kernels::matmul_f16(y, w, x, bias, n, m) (kernels.rs:571).
+ * w holds n*m fp16 values as little-endian bytes; w_len must be >= 2*n*m. */
+int hypno_hip_matmul_f16(float* y, const uint8_t* w, size_t w_len, const float* x,
+                         const float* bias, size_t n, size_t m);
+
+/* Replaces ops::matmul_vec_auto(y, w, dtype, x, bias, n, m) (ops.rs:25-38) for
+ * the dtypes of this path (FP16, Q4_0); FP32 and Q8_0 return ENOTSUP. */
+int hypno_hip_matmul_vec_auto(float* y, const uint8_t* w, size_t w_len, uint32_t dtype,
+                              const float* x, const float* bias, size_t n, size_t m);
+
+/* Replaces turbo::batch_matmul(y, w, dtype, x, n, dim, batch, false)
+ * (turbo.rs:306-333) for FP16 and Q4_0: X[batch][dim] -> Y[batch][n] in one
+ * device call instead of one GEMV per token.  No bias. */
+int hypno_hip_batch_matmul(float* y, const uint8_t* w, size_t w_len, uint32_t dtype,
+                           const float* x, size_t n, size_t dim, size_t batch);
+
+/* ---------------------------------------------------------------------------
+ * Weight residency.  hypno hands the kernel zero-copy slices of a read-only
+ * mmap (loader.rs:139-148).  Registering such a slice uploads it once; later
+ * host-slice calls whose w pointer and length match use the device copy.
+ * ------------------------------------------------------------------------- */
+
+/* Upload [host, host+len) to the current device and remember it by pointer. */
+int hypno_hip_weight_register(const uint8_t* host, size_t len);
+
+/* Forget (and free) a registration; EINVAL if it was not registered. */
+int hypno_hip_weight_unregister(const uint8_t* host);
+
+/* ---------------------------------------------------------------------------
+ * Device-pointer entry points (the serving path: inputs already in HBM).
+ * All pointers are device memory; `stream` is a hipStream_t or NULL.
+ * ------------------------------------------------------------------------- */
+
+/* Y[batch][n] = X[batch][m] . W^T (+ bias) with Q4_0 W (kernels.rs:256 for
+ * batch == 1; turbo.rs:306-333 semantics for batch > 1). */
+int hypno_hip_matmul_q4_0_dev(float* y, const uint8_t* w_q, size_t w_len, const float* x,
+                              const float* bias, size_t n, size_t m, size_t batch,
+                              void* stream);
+
+/* Same with FP16 W (kernels.rs:571; turbo.rs:316-320). */
+int hypno_hip_matmul_f16_dev(float* y, const uint8_t* w, size_t w_len, const float* x,
+                             const float* bias, size_t n, size_t m, size_t batch,
+                             void* stream);
+
+/* quantize_f32_to_q4_0 (quant.rs:108-117) on the device, bit-exact:
+ * floor(n_elems/32) blocks written to out (18 bytes each). */
+int hypno_hip_quantize_q4_0_dev(uint8_t* out, const float* src, size_t n_elems, void* stream);
+
+/* dequantize_q4_0 (quant.rs:120-132) on the device, bit-exact:
+ * floor(q_len/18) blocks -> 32 fp32 values each. */
+int hypno_hip_dequantize_q4_0_dev(float* out, const uint8_t* q, size_t q_len, void* stream);
+
+/* Block until all work this library queued on `stream` is done. */
+int hypno_hip_stream_synchronize(void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HYPNO_HIP_H */

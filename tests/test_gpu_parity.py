@@ -1,0 +1,334 @@
+"""GPU parity: libhypno_hip (through its C ABI) against the CPU oracle.
+
+Bars (from the north star):
+  * dequantize / quantize: bit-exact;
+  * GEMV (1..15 tokens, fp32 accumulation): max|y - r| / max|r| <= 1e-4 against
+    the oracle's restatement of matmul_q4_0 (kernels.rs:256), with r in fp32;
+  * MFMA GEMM (>= 16 tokens, activations rounded to fp16):
+    ||Y - R||_2 / ||R||_2 <= 2e-3 against the fp32 CPU reference on fp32 X.
+Inputs: seeded N(0, 0.02) weights quantised by the oracle's quantizer
+(quant.rs:108), N(0, 1) activations.
+"""
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 1e-4
+GEMM_TOL = 2e-3
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as _t
+    assert _t.cuda.is_available(), "GPU tests need a visible MI355X"
+    return _t
+
+
+@pytest.fixture(scope="module")
+def hk(torch):
+    import hypno_amd
+    from hypno_amd import _lib
+    _lib.load()
+    return hypno_amd
+
+
+@pytest.fixture(scope="module", autouse=True)
+def cpu_threads(orc):
+    orc.set_threads(min(16, os.cpu_count() or 1))
+    yield
+    orc.set_threads(1)
+
+
+def _q4(orc, n, m, seed):
+    """Q4_0 bytes of an n x m N(0, 0.02) matrix (zero-padded to a whole block)."""
+    w = orc.normal_f32(seed, n * m, 0.02)
+    pad = (-n * m) % 32
+    if pad:
+        w = np.concatenate([w, np.zeros(pad, np.float32)])
+    return orc.quantize_q4_0(w)
+
+
+def _gpu(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _run_q4(torch, hk, q, x, bias, n, m, batch=1):
+    y = torch.empty(batch * n, dtype=torch.float32, device="cuda")
+    if batch == 1:
+        hk.matmul_q4_0(y, q, x, bias, n, m)
+    else:
+        hk.batch_matmul(y, q, hk.DType.Q4_0, x, n, m, batch)
+    torch.cuda.synchronize()
+    return y.cpu().numpy().reshape(batch, n) if batch > 1 else y.cpu().numpy()
+
+
+# --- codec ------------------------------------------------------------------------
+
+def test_dequantize_bit_exact(torch, hk, orc):
+    rng = np.random.default_rng(1)
+    nb = 50_000
+    q = rng.integers(0, 256, size=nb * 18, dtype=np.uint8)
+    # include special scales: zero, subnormal, inf, NaN, negative
+    blocks = q.reshape(nb, 18)
+    for i, d in enumerate([0x0000, 0x0001, 0x03FF, 0x7C00, 0x7E00, 0xFC00, 0xBC00, 0x7BFF]):
+        blocks[i, 0], blocks[i, 1] = d & 0xFF, d >> 8
+    ref = orc.dequantize_q4_0(q)
+    got = hk.dequantize_q4_0(_gpu(torch, q)).cpu().numpy()
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    # trailing partial block ignored
+    assert hk.dequantize_q4_0(_gpu(torch, q[: 18 * 3 + 7])).numel() == 96
+
+
+def test_quantize_bit_exact(torch, hk, orc):
+    rng = np.random.default_rng(2)
+    w = (rng.standard_normal(32 * 40_000).astype(np.float32) * np.float32(0.02))
+    specials = w[: 32 * 8].reshape(8, 32)
+    specials[0] = 0.0                                 # all zero -> d = 1.0
+    specials[1, 3] = np.nan                           # NaN ignored by the max
+    specials[2] = np.float32(1e6)                     # d overflows to inf
+    specials[3] = np.float32(1e-40)                   # fp32 subnormals
+    specials[4, 0] = np.inf
+    specials[5] *= np.float32(1e-5)                   # f16-subnormal scales
+    specials[6] = np.arange(32, dtype=np.float32) - 15.5
+    specials[7] = np.float32(-7.0)
+    w[: 32 * 8] = specials.ravel()
+    ref = orc.quantize_q4_0(w)
+    got = hk.quantize_f32_to_q4_0(_gpu(torch, w)).cpu().numpy()
+    assert np.array_equal(got, ref)
+
+
+# --- decode GEMV ---------------------------------------------------------------------
+
+GEMV_SHAPES = [
+    (2048, 2048),    # TinyLlama q/o, config 1
+    (256, 2048),     # TinyLlama k/v
+    (5632, 2048),    # TinyLlama gate/up
+    (2048, 5632),    # TinyLlama down (m/64 = 88 pairs: rows span waves)
+    (1024, 4096),    # Mistral k/v
+    (3072, 8192),    # Llama-3.2-3B down
+    (4096, 14336),   # Mistral down (224 pairs)
+    (64, 256), (33, 512), (5, 3072), (1, 768),
+]
+
+
+@pytest.mark.parametrize("n,m", GEMV_SHAPES)
+def test_gemv_q4_0(torch, hk, orc, n, m):
+    q = _q4(orc, n, m, seed=n * 7 + m)
+    x = orc.normal_f32(m + 1, m)
+    bias = orc.normal_f32(n + 2, n) if n % 2 else None
+    ref = orc.matmul_q4_0(q, x, bias, n, m)
+    got = _run_q4(torch, hk, _gpu(torch, q), _gpu(torch, x),
+                  None if bias is None else _gpu(torch, bias), n, m)
+    err = orc.normwise_err(got, ref)
+    assert err <= GEMV_TOL, f"normwise error {err:.3e}"
+    ref64 = orc.matmul_q4_0_f64(q, x, bias, n, m)
+    assert orc.normwise_err(got, ref64) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("n,m", [(5, 48), (7, 40), (9, 100), (3, 13), (37, 96), (16, 4160),
+                                 (11, 320)])
+def test_gemv_generic_shapes(torch, hk, orc, n, m):
+    # m % 32 != 0 (blocks straddle rows), m % 256 != 0 (generic kernel)
+    q = _q4(orc, n, m, seed=m)
+    x = orc.normal_f32(5, m)
+    bias = orc.normal_f32(6, n)
+    ref = orc.matmul_q4_0(q, x, bias, n, m)
+    got = _run_q4(torch, hk, _gpu(torch, q), _gpu(torch, x), _gpu(torch, bias), n, m)
+    assert orc.normwise_err(got, ref) <= GEMV_TOL
+
+
+def test_gemv_exact_integers(torch, hk, orc):
+    # d = 1 and integer activations: exact in any order, so bit-equal
+    rng = np.random.default_rng(3)
+    for n, m in [(64, 256), (2048, 2048), (7, 48), (300, 5632)]:
+        nb = (n * m + 31) // 32
+        nib = rng.integers(0, 16, size=(nb, 32))
+        q = np.empty((nb, 18), np.uint8)
+        q[:, 0], q[:, 1] = 0x00, 0x3C
+        q[:, 2:] = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+        q = q.ravel()
+        x = rng.integers(-4, 5, size=m).astype(np.float32)
+        want = (nib - 8).ravel()[: n * m].reshape(n, m).astype(np.int64) @ x.astype(np.int64)
+        got = _run_q4(torch, hk, _gpu(torch, q), _gpu(torch, x), None, n, m)
+        assert np.array_equal(got, want.astype(np.float32)), (n, m)
+
+
+def test_gemv_unaligned_and_short(torch, hk, orc):
+    n, m = 64, 512
+    q = _q4(orc, n, m, seed=9)
+    x = orc.normal_f32(10, m)
+    # weights at an odd device address (generic kernel)
+    buf = torch.zeros(q.size + 1, dtype=torch.uint8, device="cuda")
+    buf[1:] = _gpu(torch, q)
+    got = _run_q4(torch, hk, buf[1:], _gpu(torch, x), None, n, m)
+    assert orc.normwise_err(got, orc.matmul_q4_0(q, x, None, n, m)) <= GEMV_TOL
+    # short buffer: blocks past the end contribute nothing (kernels.rs:275-277, :374)
+    short = q[: 18 * 500 + 5]
+    ref = orc.matmul_q4_0(short, x, None, n, m)
+    got = _run_q4(torch, hk, _gpu(torch, short), _gpu(torch, x), None, n, m)
+    assert np.allclose(got[32:], 0.0) and np.allclose(ref[32:], 0.0)
+    assert orc.normwise_err(got, ref) <= GEMV_TOL
+    # m = 0: y = bias (kernels.rs: empty row sums to 0)
+    y = torch.empty(4, dtype=torch.float32, device="cuda")
+    b = torch.arange(4, dtype=torch.float32, device="cuda")
+    hk.matmul_q4_0(y, _gpu(torch, q), _gpu(torch, x), b, 4, 0)
+    assert y.cpu().tolist() == [0.0, 1.0, 2.0, 3.0]
+
+
+@pytest.mark.parametrize("batch", [2, 8, 15])
+def test_small_batch_matches_per_token(torch, hk, orc, batch):
+    n, m = 1024, 4096
+    q = _q4(orc, n, m, seed=batch)
+    x = orc.normal_f32(20 + batch, (batch, m))
+    ref = orc.batch_matmul(q, 3, x, n, m, batch)
+    got = _run_q4(torch, hk, _gpu(torch, q), _gpu(torch, x), None, n, m, batch)
+    for t in range(batch):
+        assert orc.normwise_err(got[t], ref[t]) <= GEMV_TOL
+
+
+def test_gemv_linearity_and_determinism_full_size(torch, hk, orc):
+    # Mistral gate/up at full size: size-independent properties
+    n, m = 14336, 4096
+    q = _gpu(torch, _q4(orc, n, m, seed=11))
+    x1 = orc.normal_f32(12, m)
+    x2 = orc.normal_f32(13, m)
+    y1 = _run_q4(torch, hk, q, _gpu(torch, x1), None, n, m)
+    y1b = _run_q4(torch, hk, q, _gpu(torch, x1), None, n, m)
+    y2 = _run_q4(torch, hk, q, _gpu(torch, x2), None, n, m)
+    y12 = _run_q4(torch, hk, q, _gpu(torch, x1 + x2), None, n, m)
+    assert np.array_equal(y1, y1b)  # row-major: deterministic
+    assert orc.normwise_err(y12, y1.astype(np.float64) + y2) <= 1e-5
+    ref = orc.matmul_q4_0(q.cpu().numpy(), x1, None, n, m)
+    assert orc.normwise_err(y1, ref) <= GEMV_TOL
+
+
+# --- prefill GEMM (MFMA) -------------------------------------------------------------
+
+def _gemm_ref(orc, q, x, n, m):
+    """fp64 brute force of X . W^T over the dequantised weights."""
+    w = orc.dequantize_q4_0(q)[: n * m].reshape(n, m).astype(np.float64)
+    return x.astype(np.float64) @ w.T
+
+
+@pytest.mark.parametrize("batch,n,m", [
+    (16, 1024, 4096), (64, 4096, 4096), (100, 200, 512), (130, 4097, 256),
+    (512, 8192, 3072),   # Llama-3.2-3B gate/up, config 3
+    (512, 3072, 8192),   # Llama-3.2-3B down
+])
+def test_gemm_q4_0(torch, hk, orc, batch, n, m):
+    q = _q4(orc, n, m, seed=batch + n)
+    x = orc.normal_f32(batch * 3 + 1, (batch, m))
+    if batch == 512:  # config 3: 1% of channels scaled x20 as outliers
+        rng = np.random.default_rng(99)
+        ch = rng.permutation(m)[: round(0.01 * m)]
+        x[:, ch] *= np.float32(20.0)
+    got = _run_q4(torch, hk, _gpu(torch, q), _gpu(torch, x), None, n, m, batch)
+    ref = _gemm_ref(orc, q, x, n, m)
+    err = orc.rel_l2(got, ref)
+    assert err <= GEMM_TOL, f"rel L2 {err:.3e}"
+    # spot-check a few tokens against the oracle's per-token GEMV (turbo.rs:329-331)
+    for t in (0, batch - 1):
+        r32 = orc.matmul_q4_0(q, x[t], None, n, m)
+        assert orc.rel_l2(got[t], r32) <= GEMM_TOL
+
+
+def test_gemm_bias_and_tails(torch, hk, orc):
+    batch, n, m = 33, 130, 320   # M and N tails; m % 64 == 0 but not % 256
+    q = _q4(orc, n, m, seed=5)
+    x = orc.normal_f32(6, (batch, m))
+    bias = orc.normal_f32(7, n)
+    y = torch.empty(batch * n, dtype=torch.float32, device="cuda")
+    from hypno_amd import _lib
+    lib = _lib.load()
+    import ctypes
+    qg, xg, bg = _gpu(torch, q), _gpu(torch, x), _gpu(torch, bias)
+    st = lib.hypno_hip_matmul_q4_0_dev(ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(qg.data_ptr()),
+                                       q.size, ctypes.c_void_p(xg.data_ptr()),
+                                       ctypes.c_void_p(bg.data_ptr()), n, m, batch, None)
+    assert st == 0
+    torch.cuda.synchronize()
+    ref = _gemm_ref(orc, q, x, n, m) + bias.astype(np.float64)
+    assert orc.rel_l2(y.cpu().numpy().reshape(batch, n), ref) <= GEMM_TOL
+
+
+# --- FP16 weights (lm_head variant) --------------------------------------------------
+
+def _f16w(orc, n, m, seed):
+    return orc.normal_f32(seed, (n, m), 0.02).astype(np.float16)
+
+
+@pytest.mark.parametrize("n,m", [(4097, 4096), (1000, 4096), (7, 13), (64, 200), (333, 4104)])
+def test_gemv_f16(torch, hk, orc, n, m):
+    w = _f16w(orc, n, m, seed=n)
+    wb = w.view(np.uint8).ravel()
+    x = orc.normal_f32(3, m)
+    bias = orc.normal_f32(4, n)
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    hk.matmul_f16(y, _gpu(torch, wb), _gpu(torch, x), _gpu(torch, bias), n, m)
+    torch.cuda.synchronize()
+    ref = orc.matmul_f16(wb, x, bias, n, m)
+    assert orc.normwise_err(y.cpu().numpy(), ref) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("batch,n,m", [(128, 4097, 4096), (16, 256, 512)])
+def test_gemm_f16(torch, hk, orc, batch, n, m):
+    w = _f16w(orc, n, m, seed=n + 1)
+    wb = w.view(np.uint8).ravel()
+    x = orc.normal_f32(8, (batch, m))
+    y = torch.empty(batch * n, dtype=torch.float32, device="cuda")
+    hk.batch_matmul(y, _gpu(torch, wb), hk.DType.FP16, _gpu(torch, x), n, m, batch)
+    torch.cuda.synchronize()
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    assert orc.rel_l2(y.cpu().numpy().reshape(batch, n), ref) <= GEMM_TOL
+
+
+# --- host-slice ABI (drop-in for the &[f32]/&[u8] signature) --------------------------
+
+def test_host_slice_entry_points(hk, orc):
+    n, m = 300, 1024
+    q = _q4(orc, n, m, seed=77)
+    x = orc.normal_f32(78, m)
+    bias = orc.normal_f32(79, n)
+    y = np.empty(n, np.float32)
+    hk.matmul_q4_0(y, q, x, bias, n, m)
+    assert orc.normwise_err(y, orc.matmul_q4_0(q, x, bias, n, m)) <= GEMV_TOL
+    # registered (resident) weights give identical results
+    hk.register_weight(q)
+    y2 = np.empty(n, np.float32)
+    hk.matmul_vec_auto(y2, q, hk.DType.Q4_0, x, bias, n, m)
+    hk.unregister_weight(q)
+    assert np.array_equal(y, y2)
+    # batch_matmul on host arrays, fp16 and q4_0
+    xb = orc.normal_f32(80, (3, m))
+    yb = np.empty(3 * n, np.float32)
+    hk.batch_matmul(yb, q, hk.DType.Q4_0, xb, n, m, 3)
+    ref = orc.batch_matmul(q, 3, xb, n, m, 3)
+    for t in range(3):
+        assert orc.normwise_err(yb.reshape(3, n)[t], ref[t]) <= GEMV_TOL
+    w16 = _f16w(orc, n, m, 81).view(np.uint8).ravel()
+    yf = np.empty(n, np.float32)
+    hk.matmul_f16(yf, w16, x, None, n, m)
+    assert orc.normwise_err(yf, orc.matmul_f16(w16, x, None, n, m)) <= GEMV_TOL
+
+
+def test_error_paths(torch, hk, orc):
+    n, m = 8, 64
+    q = _gpu(torch, _q4(orc, n, m, 1))
+    x = torch.zeros(m, device="cuda")
+    y = torch.empty(n, device="cuda")
+    with pytest.raises(ValueError):
+        hk.matmul_q4_0(torch.empty(n + 1, device="cuda"), q, x, None, n, m)
+    with pytest.raises(ValueError):
+        hk.matmul_q4_0(y, q, torch.zeros(m - 1, device="cuda"), None, n, m)
+    with pytest.raises(hk.HypnoHipError) as e:
+        hk.matmul_vec_auto(y, q, hk.DType.Q8_0, x, None, n, m)
+    assert e.value.status == 95
+    with pytest.raises(hk.HypnoHipError) as e:   # fp16 buffer too short
+        hk.matmul_f16(y, torch.zeros(2 * n * m - 2, dtype=torch.uint8, device="cuda"), x, None,
+                      n, m)
+    assert e.value.status == 22
