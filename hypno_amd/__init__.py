@@ -6,6 +6,7 @@ the reference's function names (see hypno_amd.kernels).
 """
 from .kernels import (  # noqa: F401
     DType,
+    GemvPlan,
     HypnoHipError,
     batch_matmul,
     dequantize_q4_0,

@@ -28,8 +28,19 @@ SIGNATURES = {
     "hypno_hip_matmul_f16_dev": (_i, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _vp]),
     "hypno_hip_quantize_q4_0_dev": (_i, [_vp, _vp, _sz, _vp]),
     "hypno_hip_dequantize_q4_0_dev": (_i, [_vp, _vp, _sz, _vp]),
+    "hypno_hip_q4_0_gemv_plan_create": (_i, [_vp, _sz, _vp]),
+    "hypno_hip_q4_0_gemv_plan_run": (_i, [_vp, _vp]),
+    "hypno_hip_q4_0_gemv_plan_launches": (_i, [_vp]),
+    "hypno_hip_q4_0_gemv_plan_destroy": (_i, [_vp]),
     "hypno_hip_stream_synchronize": (_i, [_vp]),
 }
+
+
+class GemvDesc(ctypes.Structure):
+    """struct hypno_hip_gemv_desc of include/hypno_hip.h."""
+    _fields_ = [("y", ctypes.c_void_p), ("w_q", ctypes.c_void_p), ("w_len", ctypes.c_size_t),
+                ("x", ctypes.c_void_p), ("bias", ctypes.c_void_p), ("n", ctypes.c_size_t),
+                ("m", ctypes.c_size_t)]
 
 _lib = None
 

@@ -386,6 +386,151 @@ int hypno_hip_dequantize_q4_0_dev(float* out, const uint8_t* q, size_t q_len, vo
   return HYPNO_HIP_OK;
 }
 
+}  // extern "C"
+
+struct hypno_hip_gemv_plan {
+  struct Group {
+    GemvGroupGeom geom;
+    GemvJob* d_jobs = nullptr;  // device table (njobs > 1)
+    GemvJob job0;
+    int njobs = 0;
+    int total_steps = 0;
+  };
+  int device = 0;
+  int cus = 256;
+  std::vector<Group> groups;
+  std::vector<hypno_hip_gemv_desc> generic;  // run by the any-shape kernel
+};
+
+namespace {
+
+int close_group(hypno_hip_gemv_plan* pl, hypno_hip_gemv_plan::Group& grp,
+                std::vector<GemvJob>& jobs) {
+  if (jobs.empty()) return HYPNO_HIP_OK;
+  long long step = 0;
+  for (GemvJob& j : jobs) {
+    j.rps = grp.geom.T / j.B;
+    j.step0 = (int)step;
+    step += (j.n + j.rps - 1) / j.rps;
+  }
+  if (step > 0x7FFFFFFF) return fail(HYPNO_HIP_EINVAL, "plan: too many rows in one group");
+  grp.njobs = (int)jobs.size();
+  grp.total_steps = (int)step;
+  grp.job0 = jobs[0];
+  if (grp.njobs > 1) {
+    hipError_t e = hipMalloc(&grp.d_jobs, jobs.size() * sizeof(GemvJob));
+    if (e != hipSuccess) return hip_fail(e, "plan: job table");
+    e = hipMemcpy(grp.d_jobs, jobs.data(), jobs.size() * sizeof(GemvJob), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(grp.d_jobs);
+      grp.d_jobs = nullptr;
+      return hip_fail(e, "plan: job table upload");
+    }
+  }
+  pl->groups.push_back(grp);
+  grp = hypno_hip_gemv_plan::Group();
+  jobs.clear();
+  return HYPNO_HIP_OK;
+}
+
+void free_plan(hypno_hip_gemv_plan* pl) {
+  for (auto& g : pl->groups)
+    if (g.d_jobs) (void)hipFree(g.d_jobs);
+  delete pl;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hypno_hip_q4_0_gemv_plan_create(const hypno_hip_gemv_desc* descs, size_t count,
+                                    hypno_hip_gemv_plan** plan) {
+  if (!plan) return fail(HYPNO_HIP_EINVAL, "plan_create: NULL plan pointer");
+  *plan = nullptr;
+  if (!descs && count) return fail(HYPNO_HIP_EINVAL, "plan_create: NULL descriptors");
+  int cus = 256;
+  {
+    std::lock_guard<std::mutex> g(g_mu);
+    DeviceState* ds = nullptr;
+    int st = device_state(&ds);
+    if (st) return st;
+    cus = ds->cus;
+  }
+  hypno_hip_gemv_plan* pl = new hypno_hip_gemv_plan();
+  (void)hipGetDevice(&pl->device);
+  pl->cus = cus;
+  hypno_hip_gemv_plan::Group grp;
+  std::vector<GemvJob> jobs;
+  for (size_t i = 0; i < count; i++) {
+    const hypno_hip_gemv_desc& d = descs[i];
+    if (d.n == 0) continue;
+    if (!d.y || !d.x || (!d.w_q && d.w_len)) {
+      free_plan(pl);
+      return fail(HYPNO_HIP_EINVAL, "plan_create: descriptor %zu has a NULL pointer", i);
+    }
+    if (mul_overflows(d.n, d.m)) {
+      free_plan(pl);
+      return fail(HYPNO_HIP_EINVAL, "plan_create: descriptor %zu shape overflows", i);
+    }
+    if (!(q4_0_gemv_fast_ok(d.w_q, d.w_len, d.n, d.m) && aligned16(d.x))) {
+      pl->generic.push_back(d);
+      continue;
+    }
+    if (!gemv_group_add(grp.geom, d.m)) {
+      int st = close_group(pl, grp, jobs);
+      if (st) {
+        free_plan(pl);
+        return st;
+      }
+      gemv_group_add(grp.geom, d.m);
+    }
+    GemvJob j;
+    j.w = d.w_q;
+    j.x = d.x;
+    j.y = d.y;
+    j.bias = d.bias;
+    j.n = (int)d.n;
+    j.B = (int)(d.m / 32);
+    j.rps = 0;
+    j.step0 = 0;
+    jobs.push_back(j);
+  }
+  int st = close_group(pl, grp, jobs);
+  if (st) {
+    free_plan(pl);
+    return st;
+  }
+  *plan = pl;
+  return HYPNO_HIP_OK;
+}
+
+int hypno_hip_q4_0_gemv_plan_run(const hypno_hip_gemv_plan* plan, void* stream) {
+  if (!plan) return fail(HYPNO_HIP_EINVAL, "plan_run: NULL plan");
+  hipStream_t s = (hipStream_t)stream;
+  for (const auto& g : plan->groups) {
+    hipError_t e = launch_q4_0_gemv_group(g.geom, g.d_jobs, g.job0, g.njobs, g.total_steps,
+                                          plan->cus, s);
+    if (e != hipSuccess) return hip_fail(e, "plan_run: GEMV launch");
+  }
+  for (const auto& d : plan->generic) {
+    hipError_t e = launch_q4_0_generic(d.y, d.w_q, d.w_len, d.x, d.bias, d.n, d.m, 1, s);
+    if (e != hipSuccess) return hip_fail(e, "plan_run: generic launch");
+  }
+  return HYPNO_HIP_OK;
+}
+
+int hypno_hip_q4_0_gemv_plan_launches(const hypno_hip_gemv_plan* plan) {
+  if (!plan) return 0;
+  return (int)(plan->groups.size() + plan->generic.size());
+}
+
+int hypno_hip_q4_0_gemv_plan_destroy(hypno_hip_gemv_plan* plan) {
+  if (!plan) return HYPNO_HIP_OK;
+  (void)hipDeviceSynchronize();
+  free_plan(plan);
+  return HYPNO_HIP_OK;
+}
+
 int hypno_hip_stream_synchronize(void* stream) {
   hipError_t e = hipStreamSynchronize((hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");

@@ -8,6 +8,36 @@
 
 namespace hypno {
 
+// Native 4 x u32 vector: loads and stores of it are single instructions
+// (HIP's uint4 struct copies lower to memcpy and can keep values in scratch).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Load through the global address space (global_load_*, counted by vmcnt only;
+// a generic pointer would give flat_load_*, which also holds lgkmcnt).  The
+// address-space cast exists only in the device pass; the host pass never
+// runs kernel bodies.
+template <typename T>
+__device__ __forceinline__ T load_global(const void* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return *reinterpret_cast<const __attribute__((address_space(1))) T*>(
+      reinterpret_cast<uintptr_t>(p));
+#else
+  return *reinterpret_cast<const T*>(p);
+#endif
+}
+
+// Load of read-only, work-group-uniform data through the constant address
+// space (scalar s_load_* when the address is uniform).
+template <typename T>
+__device__ __forceinline__ T load_const(const void* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return *reinterpret_cast<const __attribute__((address_space(4))) T*>(
+      reinterpret_cast<uintptr_t>(p));
+#else
+  return *reinterpret_cast<const T*>(p);
+#endif
+}
+
 constexpr int kBlockElems = 32;  // Q4_0 block: 32 weights (dtype.rs:40-45)
 constexpr int kBlockBytes = 18;  // fp16 scale + 16 packed bytes (dtype.rs:48-54)
 
@@ -21,6 +51,15 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Sum over aligned groups of 8 lanes with DPP row shifts (VALU only, no LDS):
+// lane 8g+7 returns the sum of lanes 8g..8g+7 (other lanes: partial sums).
+__device__ __forceinline__ float group8_sum(float v) {
+  v += __builtin_amdgcn_update_dpp(0.0f, v, 0x111, 0xF, 0xF, true);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0.0f, v, 0x112, 0xF, 0xF, true);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0.0f, v, 0x114, 0xF, 0xF, true);  // row_shr:4
   return v;
 }
 
@@ -53,11 +92,48 @@ hipError_t launch_dequantize_q4_0(float* out, const uint8_t* q, size_t n_blocks,
 hipError_t launch_q4_0_generic(float* y, const uint8_t* w, size_t w_len, const float* x,
                                const float* bias, size_t n, size_t m, size_t batch,
                                hipStream_t s);
-// Fast decode GEMV for one token.  Requires m % 256 == 0, w 16-byte aligned,
-// w_len >= n*m/32*18, m <= 65536.
+// Streaming decode GEMV for one token.  Requires m % 256 == 0 (m <= 15360),
+// lcm(m/64, 64) <= 1024, w 16-byte aligned, x 16-byte aligned,
+// w_len >= n*m/32*18.
 bool q4_0_gemv_fast_ok(const uint8_t* w, size_t w_len, size_t n, size_t m);
 hipError_t launch_q4_0_gemv_fast(float* y, const uint8_t* w, const float* x, const float* bias,
                                  size_t n, size_t m, int num_cus, hipStream_t s);
+
+// One GEMV of a multi-job launch (device-side descriptor).
+struct GemvJob {
+  const uint8_t* w;
+  const float* x;
+  float* y;
+  const float* bias;
+  int n;      // rows
+  int B;      // blocks per row = m / 32
+  int rps;    // rows per step = T / B
+  int step0;  // first global step of this job
+};
+
+// Work-group shape shared by the jobs of one launch.
+struct GemvGroupGeom {
+  int Tbase = 0; // lcm over jobs of lcm(B, 64)
+  int T = 0;     // threads: Tbase doubled up to at least 256 (when it fits)
+  int W = 0;     // waves
+  int S = 0;     // steps per partial-sum chunk
+  int maxB = 0;  // largest B (activation staging size)
+  size_t lds = 0;
+};
+
+struct GemvLaunch {
+  const GemvJob* jobs;  // device table when njobs > 1
+  GemvJob job0;         // the job when njobs == 1
+  int njobs;
+  int total_steps;
+  int S;
+};
+
+// Adds a job with m columns to group g if the shared shape still fits.
+bool gemv_group_add(GemvGroupGeom& g, size_t m);
+hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
+                                  const GemvJob& job0, int njobs, int total_steps, int num_cus,
+                                  hipStream_t s);
 
 // MFMA prefill GEMM.  Requires m % 64 == 0, w 4-byte aligned, w_len full.
 // `xh` is a device workspace of gemm_q4_0_workspace_bytes(batch, m) bytes.

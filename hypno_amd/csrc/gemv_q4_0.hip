@@ -4,14 +4,8 @@
 //    weight buffers, bias, and any number of tokens.  One wave per
 //    (token, row); lanes walk the row's overlapping blocks.  Semantics follow
 //    matmul_q4_0_scalar (kernels.rs:362-400).
-//  * q4_0_gemv_fast_kernel: the decode GEMV (one token).  A work-group owns a
-//    fixed set of 64-element column ranges ("pairs" of two 18-byte blocks, 36
-//    bytes each) and keeps the matching 64 activations in registers; it then
-//    walks groups of rows.  Each step streams `rows*m/32*18` contiguous bytes
-//    with 16-byte loads (rows are 16-byte aligned because m % 256 == 0),
-//    stages them in LDS, and every thread decodes its 36-byte pair from LDS,
-//    unpacks the nibbles in registers and accumulates in fp32.  Per-row sums
-//    finish with wave shuffles (and an LDS hop when a row spans waves).
+//  * q4_0_gemv_jobs_kernel: the decode GEMV (one token) over one job or a
+//    table of independent jobs in a single launch.  See the comment above it.
 #include "common.hpp"
 
 namespace hypno {
@@ -65,14 +59,36 @@ hipError_t launch_q4_0_generic(float* y, const uint8_t* w, size_t w_len, const f
 }
 
 // ---------------------------------------------------------------------------
-// Fast decode GEMV
+// Streaming decode GEMV over a table of jobs (one token, m % 256 == 0)
+//
+// A row of m weights is B = m/32 blocks of 18 bytes.  A work-group of T
+// threads treats rps = T/B consecutive rows of a job (T blocks, contiguous in
+// memory) as one step; thread t owns block t % B of row t / B in every step
+// of that job, so its 32 activations stay in registers while the job lasts.
+// T is a multiple of lcm(B, 64) for every job of the launch, so every lane
+// has a block.
+//
+// The steps of all jobs form one global sequence; each work-group takes a
+// contiguous range of it (possibly spanning jobs).  A lane loads its own
+// block straight from HBM as the 20-byte window [18t & ~3, +20) (a 16-byte
+// and a 4-byte load; the 64 lanes of a wave cover one contiguous 1152-byte
+// span, so the loads coalesce), and keeps the next kDepth steps in flight in
+// a register ring that runs across job boundaries.  A lane-dependent byte
+// permute realigns the nibble dwords (a block starts at byte 0 or 2 of its
+// window), the nibbles are converted in registers (v_cvt_f32_ubyte*), sum(nib
+// * x) accumulates in fp32, and the block's scale is applied as
+// d * (sum - 8 * sum(x)).  Per-block partials of S steps are parked in LDS;
+// after one barrier each wave sums whole rows in a fixed order
+// (deterministic) and writes y.  Activations are restaged (coalesced, through
+// LDS with an XOR swizzle) only when the job changes.
+//
+// Bounds: a matrix of whole rows is a multiple of 144 bytes, so its last
+// block starts 2 bytes past a dword boundary and its window ends exactly at
+// the end of the matrix; every other window ends inside the next block.
 // ---------------------------------------------------------------------------
 
-// Work-group geometry for P = m/64 pairs per row: T threads, rps rows/step.
-struct GemvGeom {
-  int P, T, rps;
-  bool shuffle;  // rows are power-of-two lane segments inside one wave
-};
+constexpr int kDepth = 3;  // steps in flight per wave beyond the current one (the slot
+                           // dispatch in the step loop is written out for 3)
 
 static int gcd_int(int a, int b) {
   while (b) {
@@ -83,128 +99,267 @@ static int gcd_int(int a, int b) {
   return a;
 }
 
-static GemvGeom gemv_geom(size_t m) {
-  GemvGeom g;
-  g.P = (int)(m / 64);
-  if (g.P <= 64 && (g.P & (g.P - 1)) == 0) {
-    g.T = 256;
-    g.shuffle = true;
-  } else {
-    const int l = g.P / gcd_int(g.P, 64) * 64;  // lcm(P, 64)
-    g.T = l <= 1024 ? l : ((g.P + 63) / 64) * 64;
-    g.shuffle = false;
-  }
-  g.rps = g.T / g.P;
-  return g;
+static int lcm_int(int a, int b) { return a / gcd_int(a, b) * b; }
+
+// Threads needed so that every lane owns a block of a row with B blocks.
+static int job_threads(int B) {
+  const int l = lcm_int(B, 64);
+  return l <= 1024 ? l : -1;
+}
+
+static void finish_geometry(GemvGroupGeom& g) {
+  g.T = g.Tbase;
+  while (g.T < 256 && 2 * g.T <= 1024) g.T *= 2;
+  g.W = g.T / 64;
+  g.S = 32;
+  const size_t loop = (size_t)g.S * (g.T / 8) * 4;  // 8-lane group partials
+  const size_t xs = (size_t)g.maxB * 32 * 4;        // activations
+  g.lds = xs > loop ? xs : loop;
+}
+
+static const size_t kMaxLds = 160 * 1024;  // gfx950 LDS per work-group
+
+bool gemv_group_add(GemvGroupGeom& g, size_t m) {
+  if (m == 0 || m % 256 != 0 || m > 65536) return false;
+  const int B = (int)(m / 32);
+  const int T = job_threads(B);
+  if (T < 0) return false;
+  GemvGroupGeom t = g;
+  t.Tbase = t.Tbase ? lcm_int(t.Tbase, T) : T;
+  if (t.Tbase > 1024) return false;
+  t.maxB = t.maxB > B ? t.maxB : B;
+  finish_geometry(t);
+  if (t.lds > kMaxLds) return false;
+  g = t;
+  return true;
 }
 
 bool q4_0_gemv_fast_ok(const uint8_t* w, size_t w_len, size_t n, size_t m) {
-  if (m == 0 || m % 256 != 0 || m > 65536) return false;
-  if (n == 0 || n > (size_t)0x7FFFFFFF) return false;
+  if (n == 0 || n > (size_t)0x3FFFFFFF) return false;
   if (((uintptr_t)w & 15) != 0) return false;
+  GemvGroupGeom g;
+  if (!gemv_group_add(g, m)) return false;
   return w_len / kBlockBytes >= n * (m / kBlockElems);
 }
 
-template <bool kShuffle>
+// One ring slot: this lane's 20-byte window of one step.
+struct Slot {
+  u32x4 a;
+  uint32_t b;
+};
+
+// Cached description of the job the prefetch ring is reading (uniform).
+struct RingCursor {
+  const uint8_t* w;
+  int n, B, rps, step0, end, j;
+};
+
 __global__ void __launch_bounds__(1024)
-q4_0_gemv_fast_kernel(float* __restrict__ y, const uint8_t* __restrict__ w,
-                      const float* __restrict__ x, const float* __restrict__ bias, int n, int P,
-                      int rps) {
+q4_0_gemv_jobs_kernel(GemvLaunch L) {
   extern __shared__ __align__(16) uint8_t smem[];
-  uint4* stage = reinterpret_cast<uint4*>(smem);
   const int T = blockDim.x;
   const int t = threadIdx.x;
-  float* red = reinterpret_cast<float*>(smem + (size_t)rps * P * 36);
+  const int G = L.total_steps;
+  const int s_begin = (int)((long long)G * blockIdx.x / gridDim.x);
+  const int s_end = (int)((long long)G * (blockIdx.x + 1) / gridDim.x);
+  if (s_begin >= s_end) return;  // whole work-group
 
-  const int p = t % P;
-  const int rs = t / P;
-  const bool active = rs < rps;
-
-  // 64 activations of this thread's pair, and their two block sums (the -8
-  // offset of every nibble is applied once per block as -8 * sum(x)).
-  float xr[64];
-  {
-    const float4* xv = reinterpret_cast<const float4*>(x + (size_t)64 * p);
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const float4 v = xv[i];
-      xr[4 * i + 0] = v.x;
-      xr[4 * i + 1] = v.y;
-      xr[4 * i + 2] = v.z;
-      xr[4 * i + 3] = v.w;
+  auto get = [&](int j) -> GemvJob {
+    return L.njobs == 1 ? L.job0 : load_const<GemvJob>(L.jobs + j);
+  };
+  auto cursor = [&](int j) {
+    const GemvJob J = get(j);
+    RingCursor c;
+    c.w = J.w;
+    c.n = J.n;
+    c.B = J.B;
+    c.rps = J.rps;
+    c.step0 = J.step0;
+    c.end = J.step0 + (J.n + J.rps - 1) / J.rps;
+    c.j = j;
+    return c;
+  };
+  // First job of this work-group's range (binary search on step0).
+  int j0 = 0;
+  if (L.njobs > 1) {
+    int lo = 0, hi = L.njobs - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (load_const<int>(&L.jobs[mid].step0) <= s_begin)
+        lo = mid;
+      else
+        hi = mid - 1;
     }
-  }
-  float xs0 = 0.0f, xs1 = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 32; i++) {
-    xs0 += xr[i];
-    xs1 += xr[32 + i];
+    j0 = lo;
   }
 
-  const size_t row_bytes = (size_t)P * 36;
-  const int total_steps = (n + rps - 1) / rps;
-  for (int step = blockIdx.x; step < total_steps; step += gridDim.x) {
-    const int row0 = step * rps;
-    const int rows = min(rps, n - row0);
-    const int chunks = rows * P * 9 / 4;  // 16-byte chunks in this step
-    const uint4* src = reinterpret_cast<const uint4*>(w + (size_t)row0 * row_bytes);
-    for (int c = t; c < chunks; c += T) stage[c] = src[c];
+  // Ring loads are unconditional (a lane with nothing to fetch re-reads the
+  // first 20 bytes of a job's weights, always in bounds): a load under a
+  // branch is waited for at once, which would serialise the ring.  The job
+  // table is read only when the ring crosses into the next job.
+  RingCursor pc = cursor(j0);
+  const uint8_t* wsafe = pc.w;
+  const uint32_t win = (uint32_t)(18 * t) & ~3u;  // window start inside a step
+  auto issue = [&](int g) -> Slot {
+    const uint8_t* p = wsafe;
+    if (g < s_end) {
+      if (g >= pc.end) pc = cursor(pc.j + 1);
+      const int ls = g - pc.step0;
+      const int vu = min(pc.rps, pc.n - ls * pc.rps) * pc.B;  // valid blocks in the step
+      if (t < vu) p = pc.w + (size_t)ls * pc.rps * pc.B * 18 + win;
+    }
+    Slot r;
+    r.a = load_global<u32x4>(p);
+    r.b = load_global<uint32_t>(p + 16);
+    return r;
+  };
+  Slot ring[kDepth];
+#pragma unroll
+  for (int d = 0; d < kDepth; d++) ring[d] = issue(s_begin + d);
+
+  // Byte selectors for v_perm_b32: a block starts at byte 0 (t even) or 2
+  // (t odd) of its window; nibble dword j is bytes [2+4j, 6+4j) of the block.
+  const bool odd = (t & 1) != 0;
+  const uint32_t sel_q = odd ? 0x07060504u : 0x05040302u;
+  const uint32_t sh_d = odd ? 16u : 0u;
+
+  // [S][T/8] sums of 8-lane groups (a row of B blocks is B/8 whole groups
+  // because B % 8 == 0); aliases the activation staging area.
+  float* part = reinterpret_cast<float*>(smem);
+  const int T8 = T >> 3;
+
+  int cj = j0;
+  int s = s_begin;
+  while (s < s_end) {
+    const GemvJob J = get(cj);
+    const int B = J.B, rps = J.rps, n = J.n;
+    const int seg_end = min(s_end, J.step0 + (n + rps - 1) / rps);
+    const int kb = t % B;
+
+    // Activations of this job: coalesced copy to LDS (float4 q of block b is
+    // stored at 8b + (q ^ (b & 7)), so the per-lane reads below do not
+    // conflict), then this lane's 32 into registers.
+    {
+      float4* xs = reinterpret_cast<float4*>(smem);
+      const float4* xv = reinterpret_cast<const float4*>(J.x);
+      for (int i = t; i < B * 8; i += T) {
+        const int b = i >> 3;
+        xs[(b << 3) + ((i & 7) ^ (b & 7))] = load_global<float4>(xv + i);
+      }
+    }
     __syncthreads();
-
-    float part = 0.0f;
-    if (active && rs < rows) {
-      const uint32_t* u = reinterpret_cast<const uint32_t*>(smem) + 9 * t;
-      uint32_t d[9];
+    float xr[32];
+    {
+      const float4* xs = reinterpret_cast<const float4*>(smem) + (kb << 3);
 #pragma unroll
-      for (int j = 0; j < 9; j++) d[j] = u[j];
-      // block 0: bytes 0-1 scale, 2-17 nibbles; block 1: bytes 18-19, 20-35
-      const float s0 = f16_bits_to_f32(d[0] & 0xFFFFu);
-      const float s1 = f16_bits_to_f32(d[4] >> 16);
-      float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const uint32_t q0 = __builtin_amdgcn_alignbit(d[j + 1], d[j], 16);
-        a0 += dot8_nib(q0, xr + 8 * j);
-        a1 += dot8_nib(d[5 + j], xr + 32 + 8 * j);
+      for (int q = 0; q < 8; q++) {
+        const float4 v = xs[q ^ (kb & 7)];
+        xr[4 * q + 0] = v.x;
+        xr[4 * q + 1] = v.y;
+        xr[4 * q + 2] = v.z;
+        xr[4 * q + 3] = v.w;
       }
-      part = fmaf(s0, fmaf(-8.0f, xs0, a0), s1 * fmaf(-8.0f, xs1, a1));
     }
+    // The -8 offset of every nibble is applied once per block as -8 * sum(x).
+    float xsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) xsum += xr[i];
+    const float m8xsum = -8.0f * xsum;
+    __syncthreads();  // the activation region becomes partial space
 
-    if (kShuffle) {
-      // P is a power of two <= 64: each row is an aligned segment of P lanes.
-      for (int off = P >> 1; off > 0; off >>= 1) part += __shfl_xor(part, off, 64);
-      if (active && rs < rows && p == 0)
-        y[row0 + rs] = part + (bias ? bias[row0 + rs] : 0.0f);
+    // One step: decode this lane's block from its ring slot, refill the slot
+    // with step ss + kDepth (returned), park the partial.
+    auto step = [&](int ss, int c0, const Slot sl) -> Slot {
+      const Slot next = issue(ss + kDepth);
+      const int vu = min(rps, n - (ss - J.step0) * rps) * B;
+      float partial = 0.0f;
+      if (t < vu) {
+        const uint32_t d[5] = {sl.a.x, sl.a.y, sl.a.z, sl.a.w, sl.b};
+        const float scale = f16_bits_to_f32(d[0] >> sh_d);
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          acc += dot8_nib(__builtin_amdgcn_perm(d[j + 1], d[j], sel_q), xr + 8 * j);
+        partial = scale * (acc + m8xsum);
+      }
+      partial = group8_sum(partial);
+      if ((t & 7) == 7) part[(ss - c0) * T8 + (t >> 3)] = partial;
+      return next;
+    };
+
+    for (int c0 = s; c0 < seg_end; c0 += L.S) {
+      const int c1 = min(c0 + L.S, seg_end);
+      // ring[k] holds step ss with (ss - s_begin) % kDepth == k: rotate by
+      // value so the slot index stays a compile-time constant.
+      for (int ss = c0; ss < c1; ss++) {
+        const int k = (ss - s_begin) % kDepth;
+        if (k == 0) ring[0] = step(ss, c0, ring[0]);
+        else if (k == 1) ring[1] = step(ss, c0, ring[1]);
+        else ring[2] = step(ss, c0, ring[2]);
+      }
       __syncthreads();
-    } else {
-      red[t] = part;
-      __syncthreads();
-      const int wv = t >> 6, lane = t & 63, nw = T >> 6;
-      for (int r = wv; r < rows; r += nw) {  // wave-uniform loop
+      // One thread per row sums the row's B/8 group partials in a fixed order.
+      const int row0 = (c0 - J.step0) * rps;
+      const int nrows = min((c1 - c0) * rps, n - row0);
+      const int B8 = B >> 3;
+      for (int r = t; r < nrows; r += T) {
+        const int sl = r / rps;
+        const float* pr = part + sl * T8 + (r - sl * rps) * B8;
         float v = 0.0f;
-        for (int q = lane; q < P; q += 64) v += red[r * P + q];
-        v = wave_sum(v);
-        if (lane == 0) y[row0 + r] = v + (bias ? bias[row0 + r] : 0.0f);
+        for (int q = 0; q < B8; q++) v += pr[q];
+        J.y[row0 + r] = v + (J.bias ? J.bias[row0 + r] : 0.0f);
       }
       __syncthreads();
     }
+    s = seg_end;
+    cj++;
   }
+}
+
+static bool g_lds_attr_set = false;
+
+hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
+                                  const GemvJob& job0, int njobs, int total_steps, int num_cus,
+                                  hipStream_t s) {
+  if (!g_lds_attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(q4_0_gemv_jobs_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+    if (e != hipSuccess) return e;
+    g_lds_attr_set = true;
+  }
+  // As many work-groups as can be resident at once (registers and LDS).
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &per_cu, reinterpret_cast<const void*>(q4_0_gemv_jobs_kernel), g.T, g.lds) !=
+          hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  const int grid = total_steps < num_cus * per_cu ? total_steps : num_cus * per_cu;
+  GemvLaunch L;
+  L.jobs = d_jobs;
+  L.job0 = job0;
+  L.njobs = njobs;
+  L.total_steps = total_steps;
+  L.S = g.S;
+  hipLaunchKernelGGL(q4_0_gemv_jobs_kernel, dim3(grid), dim3(g.T), g.lds, s, L);
+  return hipGetLastError();
 }
 
 hipError_t launch_q4_0_gemv_fast(float* y, const uint8_t* w, const float* x, const float* bias,
                                  size_t n, size_t m, int num_cus, hipStream_t s) {
-  const GemvGeom g = gemv_geom(m);
-  const int total_steps = (int)((n + g.rps - 1) / g.rps);
-  const int per_cu = g.T <= 256 ? 4 : (g.T <= 512 ? 2 : 1);
-  const int grid = total_steps < num_cus * per_cu ? total_steps : num_cus * per_cu;
-  const size_t lds = (size_t)g.rps * g.P * 36 + (g.shuffle ? 0 : (size_t)g.T * 4);
-  if (g.shuffle)
-    hipLaunchKernelGGL(q4_0_gemv_fast_kernel<true>, dim3(grid), dim3(g.T), lds, s, y, w, x, bias,
-                       (int)n, g.P, g.rps);
-  else
-    hipLaunchKernelGGL(q4_0_gemv_fast_kernel<false>, dim3(grid), dim3(g.T), lds, s, y, w, x,
-                       bias, (int)n, g.P, g.rps);
-  return hipGetLastError();
+  GemvGroupGeom g;
+  gemv_group_add(g, m);
+  GemvJob J;
+  J.w = w;
+  J.x = x;
+  J.y = y;
+  J.bias = bias;
+  J.n = (int)n;
+  J.B = (int)(m / 32);
+  J.rps = g.T / J.B;
+  J.step0 = 0;
+  const int steps = (J.n + J.rps - 1) / J.rps;
+  return launch_q4_0_gemv_group(g, nullptr, J, 1, steps, num_cus, s);
 }
 
 }  // namespace hypno

@@ -30,7 +30,7 @@ from ._lib import HypnoHipError, check, load
 __all__ = [
     "DType", "HypnoHipError", "matmul_q4_0", "matmul_f16", "matmul_vec_q4_0",
     "matmul_vec_f16", "matmul_vec_auto", "batch_matmul", "quantize_f32_to_q4_0",
-    "dequantize_q4_0", "register_weight", "unregister_weight", "device_count",
+    "dequantize_q4_0", "register_weight", "unregister_weight", "device_count", "GemvPlan",
 ]
 
 
@@ -217,6 +217,56 @@ def dequantize_q4_0(q):
                                                 _dev_ptr(q, "u8", "q"), q.numel(),
                                                 _stream(q.device)), "dequantize_q4_0")
     return out
+
+
+# --- multi-GEMV plans ---------------------------------------------------------------
+
+class GemvPlan:
+    """Several independent Q4_0 GEMVs (one token each) run as one launch.
+
+    `jobs` is a sequence of (y, w_q, x, bias, n, m) with GPU tensors, each with
+    the meaning of matmul_q4_0's arguments.  The plan keeps the tensors'
+    addresses: refill the x tensors in place and call run() again."""
+
+    def __init__(self, jobs):
+        from ._lib import GemvDesc
+        lib = load()
+        self._keep = []
+        descs = (GemvDesc * len(jobs))()
+        for i, (y, w, x, bias, n, m) in enumerate(jobs):
+            _check_lengths(y, x, bias, n, m, 1)
+            descs[i].y = _dev_ptr(y, "f32", "y").value
+            descs[i].w_q = _dev_ptr(w, "u8", "w_q").value
+            descs[i].w_len = _nbytes(w)
+            descs[i].x = _dev_ptr(x, "f32", "x").value
+            descs[i].bias = _dev_ptr(bias, "f32", "bias").value if bias is not None else None
+            descs[i].n = n
+            descs[i].m = m
+            self._keep.append((y, w, x, bias))
+        self._plan = ctypes.c_void_p()
+        check(lib.hypno_hip_q4_0_gemv_plan_create(descs, len(jobs), ctypes.byref(self._plan)),
+              "gemv_plan_create")
+        self.device = self._keep[0][0].device if self._keep else None
+
+    @property
+    def launches(self) -> int:
+        return int(load().hypno_hip_q4_0_gemv_plan_launches(self._plan))
+
+    def run(self, stream=None) -> None:
+        st = ctypes.c_void_p(stream) if stream is not None else (
+            _stream(self.device) if self.device is not None else None)
+        check(load().hypno_hip_q4_0_gemv_plan_run(self._plan, st), "gemv_plan_run")
+
+    def close(self) -> None:
+        if self._plan:
+            load().hypno_hip_q4_0_gemv_plan_destroy(self._plan)
+            self._plan = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 # --- weight residency for the host-slice path -------------------------------------

@@ -126,6 +126,45 @@ int hypno_hip_quantize_q4_0_dev(uint8_t* out, const float* src, size_t n_elems, 
  * floor(q_len/18) blocks -> 32 fp32 values each. */
 int hypno_hip_dequantize_q4_0_dev(float* out, const uint8_t* q, size_t q_len, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Multi-GEMV plans (no counterpart in hypno, which calls matmul_q4_0 once per
+ * weight matrix: transformer.rs:305-453).  A decode step streams many
+ * independent Q4_0 GEMVs (q/k/v share one input, gate/up another); running
+ * them as one launch removes the per-launch cost (about 1.6 us per kernel in
+ * a HIP graph on MI355X) and keeps HBM busy across matrix boundaries.
+ * Each descriptor has the semantics of hypno_hip_matmul_q4_0_dev with
+ * batch = 1.  Jobs must be independent: no job's y may overlap another job's
+ * x, w or y.  Descriptors that the streaming kernel cannot take (m % 256 != 0,
+ * unaligned pointers, short buffers) are run by the generic kernel in the
+ * same plan.  A plan stores the pointers: update the x buffers in place and
+ * run it again (it is safe to capture plan_run in a HIP graph).
+ * ------------------------------------------------------------------------- */
+typedef struct hypno_hip_gemv_desc {
+  float* y;              /* [n] device */
+  const uint8_t* w_q;    /* Q4_0 bytes, device */
+  size_t w_len;
+  const float* x;        /* [m] device */
+  const float* bias;     /* [n] device or NULL */
+  size_t n;
+  size_t m;
+} hypno_hip_gemv_desc;
+
+typedef struct hypno_hip_gemv_plan hypno_hip_gemv_plan;
+
+/* Validate `count` descriptors on the current device and build the plan
+ * (uploads a small job table; the descriptors are copied). */
+int hypno_hip_q4_0_gemv_plan_create(const hypno_hip_gemv_desc* descs, size_t count,
+                                    hypno_hip_gemv_plan** plan);
+
+/* Run every GEMV of the plan on `stream` (usually one kernel launch). */
+int hypno_hip_q4_0_gemv_plan_run(const hypno_hip_gemv_plan* plan, void* stream);
+
+/* Number of kernel launches plan_run issues. */
+int hypno_hip_q4_0_gemv_plan_launches(const hypno_hip_gemv_plan* plan);
+
+/* Free the plan (waits for the device first). */
+int hypno_hip_q4_0_gemv_plan_destroy(hypno_hip_gemv_plan* plan);
+
 /* Block until all work this library queued on `stream` is done. */
 int hypno_hip_stream_synchronize(void* stream);
 

@@ -207,6 +207,66 @@ def test_gemv_linearity_and_determinism_full_size(torch, hk, orc):
     assert orc.normwise_err(y1, ref) <= GEMV_TOL
 
 
+def test_gemv_plan_mixed_jobs(torch, hk, orc):
+    # one TinyLlama layer (m = 2048 and 5632 share one launch), plus a bias job
+    # and a job the streaming kernel cannot take (m = 320 -> generic kernel)
+    shapes = [(2048, 2048), (256, 2048), (256, 2048), (2048, 2048), (5632, 2048),
+              (5632, 2048), (2048, 5632), (300, 2048), (40, 320)]
+    jobs, refs = [], []
+    for i, (n, m) in enumerate(shapes):
+        q = _q4(orc, n, m, seed=500 + i)
+        x = orc.normal_f32(600 + i, m)
+        bias = orc.normal_f32(700 + i, n) if i == 7 else None
+        y = torch.full((n,), float("nan"), device="cuda")
+        jobs.append((y, _gpu(torch, q), _gpu(torch, x), None if bias is None else _gpu(torch, bias),
+                     n, m))
+        refs.append(orc.matmul_q4_0(q, x, bias, n, m))
+    plan = hk.GemvPlan(jobs)
+    assert plan.launches == 2          # one streaming launch + one generic launch
+    for rep in range(3):               # plans are re-runnable
+        for j in jobs:
+            j[0].fill_(float("nan"))
+        plan.run()
+        torch.cuda.synchronize()
+        for (y, *_), ref in zip(jobs, refs):
+            assert orc.normwise_err(y.cpu().numpy(), ref) <= GEMV_TOL
+    plan.close()
+
+
+def test_gemv_plan_mistral_layer_in_graph(torch, hk, orc):
+    # Mistral-7B layer shapes (m = 4096 and 14336 share T = 448), captured in a
+    # HIP graph and replayed with fresh activations written in place
+    shapes = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096),
+              (14336, 4096), (4096, 14336)]
+    qs = [_q4(orc, n, m, seed=800 + i) for i, (n, m) in enumerate(shapes)]
+    xs = [torch.empty(m, device="cuda") for _, m in shapes]
+    ys = [torch.empty(n, device="cuda") for n, _ in shapes]
+    plan = hk.GemvPlan([(y, _gpu(torch, q), x, None, n, m)
+                        for y, q, x, (n, m) in zip(ys, qs, xs, shapes)])
+    assert plan.launches == 1
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    for x in xs:
+        x.zero_()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        plan.run()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        plan.run()
+    for rep in range(2):
+        xh = [orc.normal_f32(900 + 10 * rep + i, m) for i, (_, m) in enumerate(shapes)]
+        for x, h in zip(xs, xh):
+            x.copy_(torch.from_numpy(h))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for y, q, h, (n, m) in zip(ys, qs, xh, shapes):
+            assert orc.normwise_err(y.cpu().numpy(), orc.matmul_q4_0(q, h, None, n, m)) <= GEMV_TOL
+    plan.close()
+
+
 # --- prefill GEMM (MFMA) -------------------------------------------------------------
 
 def _gemm_ref(orc, q, x, n, m):
