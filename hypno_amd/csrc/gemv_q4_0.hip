@@ -72,23 +72,22 @@ hipError_t launch_q4_0_generic(float* y, const uint8_t* w, size_t w_len, const f
 // contiguous range of it (possibly spanning jobs).  A lane loads its own
 // block straight from HBM as the 20-byte window [18t & ~3, +20) (a 16-byte
 // and a 4-byte load; the 64 lanes of a wave cover one contiguous 1152-byte
-// span, so the loads coalesce), and keeps the next kDepth steps in flight in
+// span, so the loads coalesce), and keeps the next three steps in flight in
 // a register ring that runs across job boundaries.  A lane-dependent byte
 // permute realigns the nibble dwords (a block starts at byte 0 or 2 of its
 // window), the nibbles are converted in registers (v_cvt_f32_ubyte*), sum(nib
 // * x) accumulates in fp32, and the block's scale is applied as
-// d * (sum - 8 * sum(x)).  Per-block partials of S steps are parked in LDS;
-// after one barrier each wave sums whole rows in a fixed order
-// (deterministic) and writes y.  Activations are restaged (coalesced, through
-// LDS with an XOR swizzle) only when the job changes.
+// d * (sum - 8 * sum(x)).  Each step, DPP row shifts add the partials of
+// aligned 8-lane groups (a row is B/8 whole groups), and the group sums of S
+// steps are parked in LDS; after one barrier one thread per row adds its
+// groups in a fixed order (deterministic) and writes y.  Activations are
+// restaged (coalesced, through LDS with an XOR swizzle) only when the job
+// changes.
 //
 // Bounds: a matrix of whole rows is a multiple of 144 bytes, so its last
 // block starts 2 bytes past a dword boundary and its window ends exactly at
 // the end of the matrix; every other window ends inside the next block.
 // ---------------------------------------------------------------------------
-
-constexpr int kDepth = 3;  // steps in flight per wave beyond the current one (the slot
-                           // dispatch in the step loop is written out for 3)
 
 static int gcd_int(int a, int b) {
   while (b) {
@@ -148,11 +147,17 @@ struct Slot {
   uint32_t b;
 };
 
-// Cached description of the job the prefetch ring is reading (uniform).
+// Prefetch cursor (work-group uniform): the job the ring is reading and the
+// address of the next step to fetch.
 struct RingCursor {
-  const uint8_t* w;
-  int n, B, rps, step0, end, j;
+  const uint8_t* next;  // first byte of the next step to fetch
+  int bps;              // bytes per step = rps * B * 18
+  int end;              // one past the job's last global step
+  int last_units;       // blocks in the job's last (possibly partial) step
+  int j;
 };
+
+__device__ __forceinline__ int job_steps(const GemvJob& J) { return (J.n + J.rps - 1) / J.rps; }
 
 __global__ void __launch_bounds__(1024)
 q4_0_gemv_jobs_kernel(GemvLaunch L) {
@@ -167,15 +172,14 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
   auto get = [&](int j) -> GemvJob {
     return L.njobs == 1 ? L.job0 : load_const<GemvJob>(L.jobs + j);
   };
-  auto cursor = [&](int j) {
+  auto cursor_at = [&](int j, int g) {
     const GemvJob J = get(j);
+    const int steps = job_steps(J);
     RingCursor c;
-    c.w = J.w;
-    c.n = J.n;
-    c.B = J.B;
-    c.rps = J.rps;
-    c.step0 = J.step0;
-    c.end = J.step0 + (J.n + J.rps - 1) / J.rps;
+    c.bps = J.rps * J.B * 18;
+    c.next = J.w + (size_t)(g - J.step0) * c.bps;
+    c.end = J.step0 + steps;
+    c.last_units = (J.n - (steps - 1) * J.rps) * J.B;
     c.j = j;
     return c;
   };
@@ -197,25 +201,27 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
   // first 20 bytes of a job's weights, always in bounds): a load under a
   // branch is waited for at once, which would serialise the ring.  The job
   // table is read only when the ring crosses into the next job.
-  RingCursor pc = cursor(j0);
-  const uint8_t* wsafe = pc.w;
+  RingCursor pc = cursor_at(j0, s_begin);
+  int pg = s_begin;  // next step the ring fetches
+  const uint8_t* wsafe = pc.next;
   const uint32_t win = (uint32_t)(18 * t) & ~3u;  // window start inside a step
-  auto issue = [&](int g) -> Slot {
+  auto issue = [&]() -> Slot {
     const uint8_t* p = wsafe;
-    if (g < s_end) {
-      if (g >= pc.end) pc = cursor(pc.j + 1);
-      const int ls = g - pc.step0;
-      const int vu = min(pc.rps, pc.n - ls * pc.rps) * pc.B;  // valid blocks in the step
-      if (t < vu) p = pc.w + (size_t)ls * pc.rps * pc.B * 18 + win;
+    if (pg < s_end) {
+      if (pg == pc.end) pc = cursor_at(pc.j + 1, pg);
+      const int vu = pg == pc.end - 1 ? pc.last_units : T;
+      if (t < vu) p = pc.next + win;
+      pc.next += pc.bps;
     }
+    pg++;
     Slot r;
     r.a = load_global<u32x4>(p);
     r.b = load_global<uint32_t>(p + 16);
     return r;
   };
-  Slot ring[kDepth];
-#pragma unroll
-  for (int d = 0; d < kDepth; d++) ring[d] = issue(s_begin + d);
+  Slot ring0 = issue();  // ring0 holds steps s_begin, s_begin+3, ...
+  Slot ring1 = issue();
+  Slot ring2 = issue();
 
   // Byte selectors for v_perm_b32: a block starts at byte 0 (t even) or 2
   // (t odd) of its window; nibble dword j is bytes [2+4j, 6+4j) of the block.
@@ -228,92 +234,108 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
   float* part = reinterpret_cast<float*>(smem);
   const int T8 = T >> 3;
 
+  // State of the job being computed (work-group uniform except xr/m8xsum).
+  GemvJob J = get(j0);
   int cj = j0;
-  int s = s_begin;
-  while (s < s_end) {
-    const GemvJob J = get(cj);
-    const int B = J.B, rps = J.rps, n = J.n;
-    const int seg_end = min(s_end, J.step0 + (n + rps - 1) / rps);
-    const int kb = t % B;
+  int seg_end = s_begin;  // end of this work-group's steps of job cj
+  int job_last = 0;       // the job's last global step
+  int last_units = 0;     // blocks in that step
+  int c0 = s_begin;       // first step of the open partial-sum chunk
+  float xr[32];
+  float m8xsum = 0.0f;
 
-    // Activations of this job: coalesced copy to LDS (float4 q of block b is
-    // stored at 8b + (q ^ (b & 7)), so the per-lane reads below do not
-    // conflict), then this lane's 32 into registers.
-    {
-      float4* xs = reinterpret_cast<float4*>(smem);
-      const float4* xv = reinterpret_cast<const float4*>(J.x);
-      for (int i = t; i < B * 8; i += T) {
-        const int b = i >> 3;
-        xs[(b << 3) + ((i & 7) ^ (b & 7))] = load_global<float4>(xv + i);
-      }
+  // Sum the parked partials of steps [c0, c1) into y (one thread per row, in
+  // a fixed order).
+  auto flush = [&](int c1) {
+    __syncthreads();
+    const int rps = J.rps, B8 = J.B >> 3;
+    const int row0 = (c0 - J.step0) * rps;
+    const int nrows = min((c1 - c0) * rps, J.n - row0);
+    for (int r = t; r < nrows; r += T) {
+      const int sl = r / rps;
+      const float* pr = part + sl * T8 + (r - sl * rps) * B8;
+      float v = 0.0f;
+      for (int q = 0; q < B8; q++) v += pr[q];
+      J.y[row0 + r] = v + (J.bias ? J.bias[row0 + r] : 0.0f);
     }
     __syncthreads();
-    float xr[32];
-    {
-      const float4* xs = reinterpret_cast<const float4*>(smem) + (kb << 3);
+  };
+  // Make job j current at global step g: stage its activations (coalesced,
+  // through LDS: float4 q of block b at 8b + (q ^ (b & 7)), so the per-lane
+  // reads do not conflict) and keep this lane's 32 in registers.
+  auto enter = [&](int j, int g) {
+    J = get(j);
+    cj = j;
+    const int steps = job_steps(J);
+    job_last = J.step0 + steps - 1;
+    last_units = (J.n - (steps - 1) * J.rps) * J.B;
+    seg_end = min(s_end, J.step0 + steps);
+    c0 = g;
+    const int B = J.B;
+    float4* xs = reinterpret_cast<float4*>(smem);
+    const float4* xv = reinterpret_cast<const float4*>(J.x);
+    for (int i = t; i < B * 8; i += T) {
+      const int b = i >> 3;
+      xs[(b << 3) + ((i & 7) ^ (b & 7))] = load_global<float4>(xv + i);
+    }
+    __syncthreads();
+    const int kb = t % B;
+    const float4* mine = xs + (kb << 3);
 #pragma unroll
-      for (int q = 0; q < 8; q++) {
-        const float4 v = xs[q ^ (kb & 7)];
-        xr[4 * q + 0] = v.x;
-        xr[4 * q + 1] = v.y;
-        xr[4 * q + 2] = v.z;
-        xr[4 * q + 3] = v.w;
-      }
+    for (int q = 0; q < 8; q++) {
+      const float4 v = mine[q ^ (kb & 7)];
+      xr[4 * q + 0] = v.x;
+      xr[4 * q + 1] = v.y;
+      xr[4 * q + 2] = v.z;
+      xr[4 * q + 3] = v.w;
     }
     // The -8 offset of every nibble is applied once per block as -8 * sum(x).
     float xsum = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; i++) xsum += xr[i];
-    const float m8xsum = -8.0f * xsum;
+    m8xsum = -8.0f * xsum;
     __syncthreads();  // the activation region becomes partial space
+  };
 
-    // One step: decode this lane's block from its ring slot, refill the slot
-    // with step ss + kDepth (returned), park the partial.
-    auto step = [&](int ss, int c0, const Slot sl) -> Slot {
-      const Slot next = issue(ss + kDepth);
-      const int vu = min(rps, n - (ss - J.step0) * rps) * B;
-      float partial = 0.0f;
-      if (t < vu) {
-        const uint32_t d[5] = {sl.a.x, sl.a.y, sl.a.z, sl.a.w, sl.b};
-        const float scale = f16_bits_to_f32(d[0] >> sh_d);
-        float acc = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-          acc += dot8_nib(__builtin_amdgcn_perm(d[j + 1], d[j], sel_q), xr + 8 * j);
-        partial = scale * (acc + m8xsum);
-      }
-      partial = group8_sum(partial);
-      if ((t & 7) == 7) part[(ss - c0) * T8 + (t >> 3)] = partial;
-      return next;
-    };
-
-    for (int c0 = s; c0 < seg_end; c0 += L.S) {
-      const int c1 = min(c0 + L.S, seg_end);
-      // ring[k] holds step ss with (ss - s_begin) % kDepth == k: rotate by
-      // value so the slot index stays a compile-time constant.
-      for (int ss = c0; ss < c1; ss++) {
-        const int k = (ss - s_begin) % kDepth;
-        if (k == 0) ring[0] = step(ss, c0, ring[0]);
-        else if (k == 1) ring[1] = step(ss, c0, ring[1]);
-        else ring[2] = step(ss, c0, ring[2]);
-      }
-      __syncthreads();
-      // One thread per row sums the row's B/8 group partials in a fixed order.
-      const int row0 = (c0 - J.step0) * rps;
-      const int nrows = min((c1 - c0) * rps, n - row0);
-      const int B8 = B >> 3;
-      for (int r = t; r < nrows; r += T) {
-        const int sl = r / rps;
-        const float* pr = part + sl * T8 + (r - sl * rps) * B8;
-        float v = 0.0f;
-        for (int q = 0; q < B8; q++) v += pr[q];
-        J.y[row0 + r] = v + (J.bias ? J.bias[row0 + r] : 0.0f);
-      }
-      __syncthreads();
+  // One step: close the chunk / switch job when due (uniform branches),
+  // refill the ring slot with the step kDepth ahead (returned), decode this
+  // lane's block and park its 8-lane group sum.
+  auto step = [&](int ss, const Slot sl) -> Slot {
+    if (ss == seg_end) {
+      flush(ss);
+      enter(cj + 1, ss);
+    } else if (ss == c0 + L.S) {
+      flush(ss);
+      c0 = ss;
     }
-    s = seg_end;
-    cj++;
+    const Slot next = issue();
+    const int vu = ss == job_last ? last_units : T;
+    float partial = 0.0f;
+    if (t < vu) {
+      const uint32_t d[5] = {sl.a.x, sl.a.y, sl.a.z, sl.a.w, sl.b};
+      const float scale = f16_bits_to_f32(d[0] >> sh_d);
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        acc += dot8_nib(__builtin_amdgcn_perm(d[j + 1], d[j], sel_q), xr + 8 * j);
+      partial = scale * (acc + m8xsum);
+    }
+    partial = group8_sum(partial);
+    if ((t & 7) == 7) part[(ss - c0) * T8 + (t >> 3)] = partial;
+    return next;
+  };
+
+  enter(j0, s_begin);
+  int ss = s_begin;
+  for (;;) {  // unrolled by the ring depth so every slot index is static
+    ring0 = step(ss, ring0);
+    if (++ss == s_end) break;
+    ring1 = step(ss, ring1);
+    if (++ss == s_end) break;
+    ring2 = step(ss, ring2);
+    if (++ss == s_end) break;
   }
+  flush(s_end);
 }
 
 static bool g_lds_attr_set = false;
