@@ -142,7 +142,7 @@ int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
       if (e != hipSuccess) return hip_fail(e, "GEMM workspace");
       ws = b.p;
     }
-    e = launch_q4_0_gemm(y, w, x, bias, n, m, batch, ws, s);
+    e = launch_q4_0_gemm(y, w, x, bias, n, m, batch, ws, cus, s);
     if (e != hipSuccess) return hip_fail(e, "q4_0 GEMM launch");
     return HYPNO_HIP_OK;
   }
@@ -187,7 +187,7 @@ int f16_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const floa
       if (e != hipSuccess) return hip_fail(e, "GEMM workspace");
       ws = b.p;
     }
-    e = launch_f16_gemm(y, w, x, bias, n, m, batch, ws, s);
+    e = launch_f16_gemm(y, w, x, bias, n, m, batch, ws, cus, s);
     if (e != hipSuccess) return hip_fail(e, "f16 GEMM launch");
     return HYPNO_HIP_OK;
   }

@@ -140,7 +140,8 @@ hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
 bool q4_0_gemm_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t batch);
 size_t gemm_workspace_bytes(size_t batch, size_t m);
 hipError_t launch_q4_0_gemm(float* y, const uint8_t* w, const float* x, const float* bias,
-                            size_t n, size_t m, size_t batch, void* workspace, hipStream_t s);
+                            size_t n, size_t m, size_t batch, void* workspace, int num_cus,
+                            hipStream_t s);
 
 // FP16 weights.
 hipError_t launch_f16_generic(float* y, const uint8_t* w, const float* x, const float* bias,
@@ -150,6 +151,7 @@ hipError_t launch_f16_gemv_fast(float* y, const uint8_t* w, const float* x, cons
                                 size_t n, size_t m, int num_cus, hipStream_t s);
 bool f16_gemm_ok(const uint8_t* w, size_t n, size_t m, size_t batch);
 hipError_t launch_f16_gemm(float* y, const uint8_t* w, const float* x, const float* bias,
-                           size_t n, size_t m, size_t batch, void* workspace, hipStream_t s);
+                           size_t n, size_t m, size_t batch, void* workspace, int num_cus,
+                           hipStream_t s);
 
 }  // namespace hypno

@@ -1,20 +1,29 @@
 // Batched-prefill GEMM on CDNA4 MFMA: Y[M][N] = X[M][K] . W[N][K]^T (+ bias).
 //
-// X (fp32) is first rounded to fp16 into a workspace padded to a multiple of
-// the 128-row tile.  For Q4_0 weights each 8-column group of X is stored in
-// the order [0,4,1,5,2,6,3,7], which is the order in which one packed nibble
-// dword unpacks into fp16 pairs (see unpack_nib8); both MFMA operands then
-// list the same columns in the same slots.
+// Pre-pass: X (fp32) is rounded to fp16 into a workspace padded to a multiple
+// of the 128-row tile (float4 loads, one 16-byte store per 8 columns).  For
+// Q4_0 weights each 8-column group is stored in the order [0,4,1,5,2,6,3,7],
+// the order in which one packed nibble dword unpacks into fp16 pairs (see
+// unpack_nib8), so both MFMA operands list the same columns in the same
+// slots.  When the GEMM splits K in two, the pre-pass also zeroes Y.
 //
-// Q4_0 path: per 64-column K step the work-group stages X (fp16) and the
-// packed weight bytes in LDS, expands every weight row's two blocks into
-// exact fp16 integers (nibble - 8) plus one fp32 scale per (row, block), and
-// each wave runs v_mfma_f32_16x16x32_f16 once per 32-column block (K = 32 is
-// exactly one Q4_0 block) with a zero accumulator; the block partial is then
-// scaled by the fp32 block scale into the fp32 accumulators.
-//
-// FP16 path: the same tiling with the fp16 weights copied to LDS as-is and
-// the MFMA accumulating directly across K (there is no per-block scale).
+// Main kernel: a 256-thread work-group computes a 128 x 128 tile of Y with
+// 2 x 2 waves of 64 x 64.  K advances in steps of 64 (two Q4_0 blocks)
+// through two LDS buffers: while the waves compute step s from one buffer,
+// the global loads of step s+1 are already in flight into registers, and are
+// then written to the other buffer (one barrier per step).
+//   Q4_0: each thread takes one (row, block) of the step's 128 x 2 weight
+//   blocks, loads its 20-byte window (the 64 threads of a wave read
+//   contiguous memory), expands the 32 nibbles to exact fp16 integers
+//   (nibble - 8) into LDS, and stores the fp32 scale.  Every 32-column block
+//   is one v_mfma_f32_16x16x32_f16 with a zero accumulator per 16 x 16 tile;
+//   the partial is multiplied by the block's fp32 scale into fp32
+//   accumulators.
+//   FP16: the weight tile is copied to LDS as is and the MFMA accumulates
+//   across K directly.
+// Split-K: when the tile grid has fewer than two work-groups per CU, K is
+// split in two and the halves are added into the zeroed Y with atomics (two
+// addends onto zero: the sum is the same in either order).
 #include "common.hpp"
 
 namespace hypno {
@@ -22,10 +31,11 @@ namespace hypno {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 128;    // rows of X per work-group
-constexpr int kBN = 128;    // rows of W per work-group
-constexpr int kBK = 64;     // K per step (two Q4_0 blocks)
-constexpr int kLdsRow = 72; // halves per LDS row: 64 + 8 padding (144 B)
+constexpr int kBM = 128;     // rows of X per work-group
+constexpr int kBN = 128;     // rows of W per work-group
+constexpr int kBK = 64;      // K per step (two Q4_0 blocks)
+constexpr int kLdsRow = 72;  // halves per LDS row: 64 + 8 padding (144 bytes)
+constexpr int kTileHalves = kBM * kLdsRow;
 
 static size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
@@ -44,27 +54,38 @@ bool f16_gemm_ok(const uint8_t* w, size_t n, size_t m, size_t batch) {
   return n <= (size_t)0x7FFFFFFF && m <= (size_t)0x7FFFFFFF && batch <= (size_t)0x7FFFFFFF;
 }
 
-// X fp32 [M][K] -> Xh fp16 [Mp][K], zero rows M..Mp-1.  One thread per
-// 8-column group; kPermute applies the nibble-unpack column order.
+// X fp32 [M][K] -> Xh fp16 [Mp][K] (zero rows M..Mp-1); optionally zero Y.
+// One thread per 8-column group.
 template <bool kPermute>
 __global__ void __launch_bounds__(256)
-x_to_f16_kernel(uint4* __restrict__ xh, const float* __restrict__ x, int M, int Mp, int K) {
+x_to_f16_kernel(u32x4* __restrict__ xh, const float* __restrict__ x, int M, int Mp, int K,
+                float* __restrict__ y_zero, size_t y_elems) {
   const size_t groups = (size_t)K / 8;
   const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (y_zero) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = idx; i < y_elems; i += stride) y_zero[i] = 0.0f;
+  }
   if (idx >= (size_t)Mp * groups) return;
   const size_t row = idx / groups;
-  const size_t g = idx - row * groups;
   float v[8];
   if (row < (size_t)M) {
-    const float* src = x + row * K + g * 8;
+    const float* src = x + idx * 8;  // row * K + g * 8
+    if (((uintptr_t)src & 15) == 0) {
+      const float4 a = load_global<float4>(src);
+      const float4 b = load_global<float4>(src + 4);
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
 #pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = src[i];
+      for (int i = 0; i < 8; i++) v[i] = src[i];
+    }
   } else {
 #pragma unroll
     for (int i = 0; i < 8; i++) v[i] = 0.0f;
   }
   constexpr int perm_q4[8] = {0, 4, 1, 5, 2, 6, 3, 7};
-  uint32_t packed[4];
+  u32x4 packed;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const int a = kPermute ? perm_q4[2 * j] : 2 * j;
@@ -73,16 +94,16 @@ x_to_f16_kernel(uint4* __restrict__ xh, const float* __restrict__ x, int M, int 
     const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)v[b]);
     packed[j] = lo | (hi << 16);
   }
-  xh[idx] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  xh[idx] = packed;
 }
 
 // One packed nibble dword (elements e0..e7, byte i = e[2i] | e[2i+1] << 4)
 // -> 8 exact fp16 values (e - 8) in slot order e0,e4,e1,e5,e2,e6,e3,e7.
 // (0x6400 | n) is the fp16 value 1024 + n; subtracting 1032 is exact.
-__device__ __forceinline__ uint4 unpack_nib8(uint32_t dw) {
+__device__ __forceinline__ u32x4 unpack_nib8(uint32_t dw) {
   typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
   const half2_t off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-  uint32_t r[4];
+  u32x4 r;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const uint32_t bits = ((dw >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
@@ -90,26 +111,99 @@ __device__ __forceinline__ uint4 unpack_nib8(uint32_t dw) {
     h = h + off;
     r[j] = __builtin_bit_cast(uint32_t, h);
   }
-  return make_uint4(r[0], r[1], r[2], r[3]);
+  return r;
 }
+
+// Global loads of one K step held in registers until they are written to LDS.
+struct StepRegs {
+  u32x4 a[4];  // X: 4 x 16 bytes
+  u32x4 b[4];  // W: Q4_0 uses b[0] + bw (20-byte window); FP16 uses all four
+  uint32_t bw;
+};
 
 template <bool kQ4>
 __global__ void __launch_bounds__(256, 2)
-gemm_kernel(float* __restrict__ y, const uint8_t* __restrict__ w, const uint4* __restrict__ xh,
-            const float* __restrict__ bias, int M, int N, int K) {
-  __shared__ __align__(16) _Float16 As[kBM * kLdsRow];
-  __shared__ __align__(16) _Float16 Bs[kBN * kLdsRow];
-  __shared__ __align__(16) uint32_t Bq[kBN * 9];  // raw Q4_0 bytes: 2 blocks per row
-  __shared__ float Sc[2][kBN];                     // fp32 block scales
+gemm_kernel(float* __restrict__ y, const uint8_t* __restrict__ w, const u32x4* __restrict__ xh,
+            const float* __restrict__ bias, int M, int N, int K, int ksplit) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  // LDS: 2 x {A tile, B tile} fp16 + 2 x scales [2 blocks][128]
+  _Float16* As0 = reinterpret_cast<_Float16*>(smem);
+  const size_t buf_bytes = (size_t)2 * kTileHalves * 2 + (kQ4 ? 2 * kBN * 4 : 0);
 
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;  // 2x2 waves, 64x64 each
+  const int wm = wave >> 1, wn = wave & 1;
   const int m0 = blockIdx.y * kBM;
   const int n0 = blockIdx.x * kBN;
+  const int kz = blockIdx.z;
+  const int k_len = K / ksplit;
+  const int k_begin = kz * k_len;
+  const int steps = k_len / kBK;
   const size_t row_bytes = kQ4 ? (size_t)K / 32 * 18 : (size_t)K * 2;
-  const int kgroups = K / 8;  // uint4 per X row
+  const int kgroups = K / 8;
+
+  // Q4_0 staging role: (row, block) of the step's 128 x 2 blocks
+  const int qrow = t & 127, qkb = t >> 7;
+  const bool qvalid = n0 + qrow < N;
+  const uint8_t* qrow_ptr = w + (size_t)(qvalid ? n0 + qrow : 0) * row_bytes;
+  const bool qodd = (qkb & 1) != 0;  // odd block: starts 2 bytes into its window
+  const uint32_t sel_q = qodd ? 0x07060504u : 0x05040302u;
+  const uint32_t sh_d = qodd ? 16u : 0u;
+
+  auto load_step = [&](int s, StepRegs& r) {
+    const int k0 = k_begin + s * kBK;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int c = t + 256 * i;
+      const int row = c >> 3, col = c & 7;
+      r.a[i] = load_global<u32x4>(xh + (size_t)(m0 + row) * kgroups + k0 / 8 + col);
+    }
+    if (kQ4) {
+      const size_t boff = (size_t)(k0 / 32 + qkb) * 18;
+      const uint8_t* p = qrow_ptr + (boff & ~(size_t)3);
+      r.b[0] = load_global<u32x4>(p);
+      r.bw = load_global<uint32_t>(p + 16);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int c = t + 256 * i;
+        const int row = c >> 3, col = c & 7;
+        const int rr = n0 + row < N ? n0 + row : 0;
+        r.b[i] = load_global<u32x4>(w + (size_t)rr * row_bytes + (size_t)(k0 + col * 8) * 2);
+      }
+    }
+  };
+
+  auto store_step = [&](int buf, const StepRegs& r) {
+    _Float16* As = As0 + (size_t)buf * (buf_bytes / 2);
+    _Float16* Bs = As + kTileHalves;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int c = t + 256 * i;
+      const int row = c >> 3, col = c & 7;
+      *reinterpret_cast<u32x4*>(&As[row * kLdsRow + col * 8]) = r.a[i];
+    }
+    if (kQ4) {
+      float* Sc = reinterpret_cast<float*>(Bs + kTileHalves);
+      const uint32_t d[5] = {r.b[0].x, r.b[0].y, r.b[0].z, r.b[0].w, r.bw};
+      Sc[qkb * kBN + qrow] = qvalid ? f16_bits_to_f32(d[0] >> sh_d) : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t q = __builtin_amdgcn_perm(d[j + 1], d[j], sel_q);
+        *reinterpret_cast<u32x4*>(&Bs[qrow * kLdsRow + qkb * 32 + j * 8]) = unpack_nib8(q);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int c = t + 256 * i;
+        const int row = c >> 3, col = c & 7;
+        u32x4 v = r.b[i];
+        if (n0 + row >= N) v = u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(&Bs[row * kLdsRow + col * 8]) = v;
+      }
+    }
+  };
 
   floatx4 acc[4][4];
 #pragma unroll
@@ -120,67 +214,10 @@ gemm_kernel(float* __restrict__ y, const uint8_t* __restrict__ w, const uint4* _
   const int frag_row = lane & 15;
   const int frag_k = (lane >> 4) * 8;
 
-  for (int k0 = 0; k0 < K; k0 += kBK) {
-    // --- stage X: 128 rows x 64 halves = 1024 uint4, 4 per thread
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int c = t + 256 * i;
-      const int row = c >> 3, col = c & 7;
-      const uint4 v = xh[(size_t)(m0 + row) * kgroups + k0 / 8 + col];
-      *reinterpret_cast<uint4*>(&As[row * kLdsRow + col * 8]) = v;
-    }
-    if (kQ4) {
-      // --- stage packed W: 128 rows x 36 bytes = 1152 dwords
-      const size_t kb_off = (size_t)(k0 / 32) * 18;
-#pragma unroll
-      for (int i = 0; i < 5; i++) {
-        const int c = t + 256 * i;
-        if (c < kBN * 9) {
-          const int row = c / 9, j = c - row * 9;
-          uint32_t v = 0;
-          if (n0 + row < N)
-            v = *reinterpret_cast<const uint32_t*>(w + (size_t)(n0 + row) * row_bytes + kb_off +
-                                                   4 * j);
-          Bq[c] = v;
-        }
-      }
-      __syncthreads();
-      // --- expand: thread -> (row n, block kb)
-      {
-        const int n = t & 127, kb = t >> 7;
-        const uint32_t* q = Bq + n * 9;
-        float sc;
-        uint32_t dw[4];
-        if (kb == 0) {
-          sc = f16_bits_to_f32(q[0] & 0xFFFFu);
-#pragma unroll
-          for (int j = 0; j < 4; j++) dw[j] = __builtin_amdgcn_alignbit(q[j + 1], q[j], 16);
-        } else {
-          sc = f16_bits_to_f32(q[4] >> 16);
-#pragma unroll
-          for (int j = 0; j < 4; j++) dw[j] = q[5 + j];
-        }
-        Sc[kb][n] = sc;
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-          *reinterpret_cast<uint4*>(&Bs[n * kLdsRow + kb * 32 + j * 8]) = unpack_nib8(dw[j]);
-      }
-    } else {
-      // --- stage fp16 W: 128 rows x 64 halves = 1024 uint4
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int c = t + 256 * i;
-        const int row = c >> 3, col = c & 7;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (n0 + row < N)
-          v = *reinterpret_cast<const uint4*>(w + (size_t)(n0 + row) * row_bytes +
-                                              (size_t)(k0 + col * 8) * 2);
-        *reinterpret_cast<uint4*>(&Bs[row * kLdsRow + col * 8]) = v;
-      }
-    }
-    __syncthreads();
-
-    // --- MFMA: one 16x16x32 per (16-row X tile, 16-row W tile, 32-col block)
+  auto compute_step = [&](int buf) {
+    const _Float16* As = As0 + (size_t)buf * (buf_bytes / 2);
+    const _Float16* Bs = As + kTileHalves;
+    const float* Sc = reinterpret_cast<const float*>(Bs + kTileHalves);
 #pragma unroll
     for (int kb = 0; kb < 2; kb++) {
       half8 a[4], b[4];
@@ -195,7 +232,7 @@ gemm_kernel(float* __restrict__ y, const uint8_t* __restrict__ w, const uint4* _
       if (kQ4) {
         float sc[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) sc[j] = Sc[kb][wn * 64 + j * 16 + frag_row];
+        for (int j = 0; j < 4; j++) sc[j] = Sc[kb * kBN + wn * 64 + j * 16 + frag_row];
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -213,57 +250,95 @@ gemm_kernel(float* __restrict__ y, const uint8_t* __restrict__ w, const uint4* _
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
       }
     }
+  };
+
+  StepRegs regs;
+  load_step(0, regs);
+  store_step(0, regs);
+  __syncthreads();
+  for (int s = 0; s < steps; s++) {
+    const bool more = s + 1 < steps;
+    if (more) load_step(s + 1, regs);
+    compute_step(s & 1);
+    if (more) store_step((s + 1) & 1, regs);
     __syncthreads();
   }
 
-  // --- epilogue: lane holds D[4*(lane/16)+r][lane%16] of each 16x16 tile
+  // Epilogue: lane holds D[4*(lane/16)+r][lane%16] of each 16x16 tile.
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const int n = n0 + wn * 64 + j * 16 + (lane & 15);
     if (n >= N) continue;
-    const float bv = bias ? bias[n] : 0.0f;
+    const float bv = (bias && kz == 0) ? bias[n] : 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int mrow = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + r;
-        if (mrow < M) y[(size_t)mrow * N + n] = acc[i][j][r] + bv;
+        if (mrow >= M) continue;
+        float* dst = y + (size_t)mrow * N + n;
+        if (ksplit == 1)
+          *dst = acc[i][j][r] + bv;
+        else
+          atomicAdd(dst, acc[i][j][r] + bv);
       }
   }
 }
 
+// Two K halves when the tile grid leaves CUs idle and K allows it.
+static int pick_ksplit(size_t tiles, size_t m, int num_cus) {
+  if (tiles < (size_t)num_cus * 2 && m % (2 * kBK) == 0) return 2;
+  return 1;
+}
+
 static hipError_t launch_x_prepass(const float* x, size_t batch, size_t m, void* ws, bool permute,
-                                   hipStream_t s) {
+                                   float* y_zero, size_t y_elems, hipStream_t s) {
   const size_t mp = round_up(batch, kBM);
   const size_t work = mp * (m / 8);
   const size_t grid = (work + 255) / 256;
   if (permute)
     hipLaunchKernelGGL(x_to_f16_kernel<true>, dim3((unsigned)grid), dim3(256), 0, s,
-                       (uint4*)ws, x, (int)batch, (int)mp, (int)m);
+                       (u32x4*)ws, x, (int)batch, (int)mp, (int)m, y_zero, y_elems);
   else
     hipLaunchKernelGGL(x_to_f16_kernel<false>, dim3((unsigned)grid), dim3(256), 0, s,
-                       (uint4*)ws, x, (int)batch, (int)mp, (int)m);
+                       (u32x4*)ws, x, (int)batch, (int)mp, (int)m, y_zero, y_elems);
+  return hipGetLastError();
+}
+
+template <bool kQ4>
+static hipError_t launch_gemm(float* y, const uint8_t* w, const float* x, const float* bias,
+                              size_t n, size_t m, size_t batch, void* ws, int num_cus,
+                              hipStream_t s) {
+  const size_t tiles_n = (n + kBN - 1) / kBN;
+  const size_t tiles_m = round_up(batch, kBM) / kBM;
+  const int ksplit = pick_ksplit(tiles_n * tiles_m, m, num_cus);
+  hipError_t e = launch_x_prepass(x, batch, m, ws, kQ4, ksplit > 1 ? y : nullptr,
+                                  ksplit > 1 ? n * batch : 0, s);
+  if (e != hipSuccess) return e;
+  const size_t lds = 2 * ((size_t)2 * kTileHalves * 2 + (kQ4 ? 2 * kBN * 4 : 0));
+  static bool attr_set = false;
+  if (!attr_set) {
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_kernel<kQ4>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const dim3 grid((unsigned)tiles_n, (unsigned)tiles_m, (unsigned)ksplit);
+  hipLaunchKernelGGL(gemm_kernel<kQ4>, grid, dim3(256), lds, s, y, w, (const u32x4*)ws, bias,
+                     (int)batch, (int)n, (int)m, ksplit);
   return hipGetLastError();
 }
 
 hipError_t launch_q4_0_gemm(float* y, const uint8_t* w, const float* x, const float* bias,
-                            size_t n, size_t m, size_t batch, void* ws, hipStream_t s) {
-  hipError_t e = launch_x_prepass(x, batch, m, ws, true, s);
-  if (e != hipSuccess) return e;
-  const dim3 grid((unsigned)((n + kBN - 1) / kBN), (unsigned)(round_up(batch, kBM) / kBM));
-  hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(256), 0, s, y, w, (const uint4*)ws, bias,
-                     (int)batch, (int)n, (int)m);
-  return hipGetLastError();
+                            size_t n, size_t m, size_t batch, void* ws, int num_cus,
+                            hipStream_t s) {
+  return launch_gemm<true>(y, w, x, bias, n, m, batch, ws, num_cus, s);
 }
 
 hipError_t launch_f16_gemm(float* y, const uint8_t* w, const float* x, const float* bias,
-                           size_t n, size_t m, size_t batch, void* ws, hipStream_t s) {
-  hipError_t e = launch_x_prepass(x, batch, m, ws, false, s);
-  if (e != hipSuccess) return e;
-  const dim3 grid((unsigned)((n + kBN - 1) / kBN), (unsigned)(round_up(batch, kBM) / kBM));
-  hipLaunchKernelGGL(gemm_kernel<false>, grid, dim3(256), 0, s, y, w, (const uint4*)ws, bias,
-                     (int)batch, (int)n, (int)m);
-  return hipGetLastError();
+                           size_t n, size_t m, size_t batch, void* ws, int num_cus,
+                           hipStream_t s) {
+  return launch_gemm<false>(y, w, x, bias, n, m, batch, ws, num_cus, s);
 }
 
 }  // namespace hypno
