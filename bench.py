@@ -4,13 +4,15 @@
 Headline workload: the full TinyLlama-1.1B decode
 step weight stream, M = 1, Q4_0, 22 layers x {q, k, v, o, gate, up, down}
 (544,997,376 weight bytes, larger than the 256 MB Infinity Cache, so every
-step streams from HBM).  One step = the 154 GEMVs in decode order, replayed
-from a HIP graph.  value = weight bytes / step time (GB/s).
+step streams from HBM).  One step = the 154 GEMVs as one multi-GEMV plan
+launch; steps are launched back to back on one stream and timed with HIP
+events on that stream.  value = weight bytes / step time (GB/s).
 
 Also reported, in the same JSON line:
-  roofline      the decode GEMV kernel's weight bytes / its average launch
-                duration (HIP events around each launch on the launch stream)
-                against the 8 TB/s HBM peak;
+  roofline      the decode GEMV kernel's weight bytes per launch / its average
+                launch duration over the timed region, against the 8 TB/s HBM
+                peak; traffic = measured HBM bytes per launch (rocprofv3 --pmc,
+                read from the committed profile summary);
   cpu_baseline  the CPU restatement of hypno's AVX2 kernel (oracle/) on this
                 host, on a bounded sample (layer 0's seven matrices);
   secondary     prefill GEMM TFLOP/s at Llama-3.2-3B MLP shapes (M = 512,
@@ -105,7 +107,23 @@ def time_graph(torch, fn, steps, warmup):
     return e0.elapsed_time(e1) / steps, g
 
 
-def decode_stream(torch, lib, steps, warmup):
+def time_launches(torch, fn, steps, warmup):
+    """Average ms per call of `fn` over `steps` back-to-back calls on the
+    current stream, bracketed by HIP events on that stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def decode_stream(torch, lib, steps, warmup, value_only=False):
     """22 layers x 7 Q4_0 GEMVs.  Each matrix has its own output
     buffer; each layer has its own activation vectors (x for q/k/v/gate/up
     and for o share m = 2048, down has m = 5632)."""
@@ -127,9 +145,17 @@ def decode_stream(torch, lib, steps, warmup):
         jobs.append((layer, name, ys[i], arena[off:off + nb], xs[layer][x_of[name]], n, m))
     weight_bytes = sum(nb for _, nb in offs)
 
-    # (a) the whole weight stream as one plan: one launch per step (the value)
+    # (a) the whole weight stream as one plan: one launch per step (the value),
+    # launched back to back on the current stream
     plan_all = hk.GemvPlan([(y, w, x, None, n, m) for _, _, y, w, x, n, m in jobs])
-    ms_all, g_all = time_graph(torch, plan_all.run, steps, warmup)
+    ms_all = time_launches(torch, plan_all.run, steps, warmup)
+    res = {"ms": ms_all, "weight_bytes": weight_bytes, "launches": plan_all.launches}
+    host_sample = [w.cpu().numpy() for _, _, _, w, _, _, _ in jobs[:len(TINYLLAMA)]]
+    res["sample"] = host_sample
+    res["x_host"] = {m: jobs[0][4].cpu().numpy() if m == 2048 else jobs[6][4].cpu().numpy()
+                     for m in (2048, 5632)}
+    if value_only:
+        return res
     # (b) dependency-respecting decode step: per layer [q,k,v] [o] [gate,up] [down]
     groups = []
     for layer in range(LAYERS):
@@ -155,27 +181,10 @@ def decode_stream(torch, lib, steps, warmup):
                 lib.check(rc, "decode GEMV")
 
     ms_call, g_call = time_graph(torch, per_call, steps, warmup)
-
-    # Kernel duration of the value's single launch: events on the launch stream.
-    durs = []
-    for _ in range(5):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        plan_all.run()
-        b.record()
-        torch.cuda.synchronize()
-        durs.append(a.elapsed_time(b))
-    kern_ms = min(durs)
-    del g_all, g_grp, g_call
-    host_sample = [w.cpu().numpy() for _, _, _, w, _, _, _ in jobs[:len(TINYLLAMA)]]
-    x_host = {m: jobs[0][4].cpu().numpy() if m == 2048 else jobs[6][4].cpu().numpy()
-              for m in (2048, 5632)}
-    return {
-        "ms": ms_all, "weight_bytes": weight_bytes, "launches": plan_all.launches,
-        "kern_ms": kern_ms, "ms_grouped": ms_grp,
-        "launches_grouped": sum(p.launches for p in groups), "ms_per_call": ms_call,
-        "launches_per_call": len(calls), "sample": host_sample, "x_host": x_host,
-    }
+    del g_grp, g_call
+    res.update({"ms_grouped": ms_grp, "launches_grouped": sum(p.launches for p in groups),
+                "ms_per_call": ms_call, "launches_per_call": len(calls)})
+    return res
 
 
 def prefill_gemm(torch, lib, reps=10):
@@ -241,6 +250,36 @@ def mistral_gemv(torch, lib, reps=20):
             "frac_hbm_peak": {k: round(v / HBM_PEAK_GBS, 4) for k, v in res.items()}}
 
 
+def copy_probe(torch, nbytes=1 << 30, reps=20):
+    """A plain device copy of known size: its FETCH_SIZE / WRITE_SIZE per
+    dispatch calibrate the HBM counters (expected nbytes each way)."""
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    ms = time_launches(torch, lambda: dst.copy_(src), reps, 2)
+    print(json.dumps({"copy_probe_bytes": nbytes, "ms": round(ms, 4),
+                      "gbs_each_way": round(nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_0_gemv_jobs_kernel_tinyllama_stream_traffic.txt")
+
+
+def stream_traffic():
+    """HBM bytes per launch of the decode-stream GEMV, from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE per dispatch, each divided
+    by the factor the same counter reads on a plain copy of known size)."""
+    try:
+        kv = {}
+        with open(TRAFFIC_FILE) as f:
+            for ln in f:
+                if "=" in ln and not ln.startswith("#"):
+                    k, v = ln.split("=", 1)
+                    kv[k.strip()] = v.strip()
+        return int(float(kv["traffic_bytes_per_launch"]))
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(sample, x_host, seconds):
     """hypno's AVX2 Q4_0 kernel (restated in oracle/) on this host's cores."""
     from oracle import oracle as orc
@@ -273,23 +312,60 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--value-only", action="store_true",
+                    help="time only the value's launches (no grouped/per-call variants, "
+                         "no secondary, no CPU baseline)")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="run only a plain 1 GiB device copy, 20 times (HBM counter "
+                         "calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
               "(every GPU box here has one GPU)", file=sys.stderr)
         sys.exit(2)
 
+    if args.value_only:
+        args.no_secondary = args.no_cpu_baseline = True
+
     import torch
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
+    if args.copy_probe:
+        copy_probe(torch)
+        return
     lib = Lib()
 
     print("[bench] decode stream: building 545 MB of Q4_0 weights", file=sys.stderr, flush=True)
-    d = decode_stream(torch, lib, args.steps, args.warmup)
+    d = decode_stream(torch, lib, args.steps, args.warmup, value_only=args.value_only)
     value = d["weight_bytes"] / (d["ms"] * 1e-3) / 1e9
-    achieved = d["weight_bytes"] / (d["kern_ms"] * 1e-3) / 1e9
     print(f"[bench] decode stream {d['ms']:.4f} ms/step, {value:.1f} GB/s", file=sys.stderr,
           flush=True)
+    config = {
+        "workload": "TinyLlama-1.1B decode-step Q4_0 weight stream (configs[1]): 22 layers "
+                    "x {q,k,v,o,gate,up,down} GEMV, M=1, all 154 GEMVs as one "
+                    "multi-GEMV plan launch",
+        "weight_bytes": d["weight_bytes"],
+        "launches_per_step": d["launches"],
+        "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+    }
+    if "ms_grouped" in d:
+        config["decode_step_grouped"] = {
+            "desc": "dependency-respecting decode step: per layer [q,k,v], [o], [gate,up], "
+                    "[down] plans, replayed as one HIP graph",
+            "launches": d["launches_grouped"],
+            "ms_per_step": round(d["ms_grouped"], 5),
+            "gbs": round(d["weight_bytes"] / (d["ms_grouped"] * 1e-3) / 1e9, 2)}
+        config["per_call"] = {
+            "desc": "drop-in path: one hypno_hip_matmul_q4_0_dev call per matrix, "
+                    "replayed as one HIP graph",
+            "launches": d["launches_per_call"],
+            "ms_per_step": round(d["ms_per_call"], 5),
+            "gbs": round(d["weight_bytes"] / (d["ms_per_call"] * 1e-3) / 1e9, 2)}
+    # One kernel launch per step: the launch's average duration over the timed
+    # region is the step time (it includes the few-microsecond gap between
+    # back-to-back launches).
+    launch_ms = d["ms"] / d["launches"]
+    achieved = d["weight_bytes"] / d["launches"] / (launch_ms * 1e-3) / 1e9
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -303,36 +379,17 @@ def main():
         "vs_baseline": None,
         "dtype": "fp32",
         "data": "synthetic: weights N(0,0.02) seeded, Q4_0-quantised on GPU; x N(0,1)",
-        "config": {
-            "workload": "TinyLlama-1.1B decode-step Q4_0 weight stream (configs[1]): 22 layers "
-                        "x {q,k,v,o,gate,up,down} GEMV, M=1, all 154 GEMVs as one "
-                        "multi-GEMV plan launch",
-            "weight_bytes": d["weight_bytes"],
-            "launches_per_step": d["launches"],
-            "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
-            "decode_step_grouped": {
-                "desc": "dependency-respecting decode step: per layer [q,k,v], [o], [gate,up], "
-                        "[down] plans, replayed as one HIP graph",
-                "launches": d["launches_grouped"],
-                "ms_per_step": round(d["ms_grouped"], 5),
-                "gbs": round(d["weight_bytes"] / (d["ms_grouped"] * 1e-3) / 1e9, 2)},
-            "per_call": {
-                "desc": "drop-in path: one hypno_hip_matmul_q4_0_dev call per matrix, "
-                        "replayed as one HIP graph",
-                "launches": d["launches_per_call"],
-                "ms_per_step": round(d["ms_per_call"], 5),
-                "gbs": round(d["weight_bytes"] / (d["ms_per_call"] * 1e-3) / 1e9, 2)},
-        },
+        "config": config,
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": stream_traffic(),
             "kernel": "q4_0_gemv_jobs_kernel",
-            "launch_us": round(d["kern_ms"] * 1e3, 2),
-            "bytes_per_launch": d["weight_bytes"],
+            "launch_us": round(launch_ms * 1e3, 2),
+            "bytes_per_launch": d["weight_bytes"] // d["launches"],
         },
     }
     if not args.no_secondary:
