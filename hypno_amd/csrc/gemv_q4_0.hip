@@ -89,6 +89,20 @@ hipError_t launch_q4_0_generic(float* y, const uint8_t* w, size_t w_len, const f
 // the end of the matrix; every other window ends inside the next block.
 // ---------------------------------------------------------------------------
 
+// Activations as exact integer limbs.  For each block of 32 activations let
+// e be the exponent of its largest |x| (amax < 2^e).  m = rint(x * 2^(22-e))
+// has |m| <= 2^22, and m + kDigitBias (kDigitBias = sum_l 8 * 16^l) lies in
+// [0, 16^6), so m = sum_l 16^l * (u_l - 8) with u_l its base-16 digits; the
+// signed digit u_l - 8 is stored as the i4 value u_l ^ 8.  The dot product of
+// a block with (nib - 8) is then 2^(e-22) * sum_l 16^l * D_l with D_l an
+// exact integer dot product of i4 values (|D_l| <= 32 * 64).  The only
+// rounding besides fp32 arithmetic on the block result is the 2^-22-relative
+// rounding of x to m.
+constexpr int kLimbs = 6;
+constexpr int kMantBits = 22;
+constexpr int kDigitBias = 0x888888;
+constexpr int kBadExp = -100000;  // block with inf or NaN activations
+
 static int gcd_int(int a, int b) {
   while (b) {
     int t = a % b;
@@ -110,9 +124,9 @@ static void finish_geometry(GemvGroupGeom& g) {
   g.T = g.Tbase;
   while (g.T < 256 && 2 * g.T <= 1024) g.T *= 2;
   g.W = g.T / 64;
-  g.S = 32;
+  g.S = 64;
   const size_t loop = (size_t)g.S * (g.T / 8) * 4;  // 8-lane group partials
-  const size_t xs = (size_t)g.maxB * 32 * 4;        // activations
+  const size_t xs = (size_t)g.maxB * (16 * kLimbs + 4);  // activation limbs, exponents
   g.lds = xs > loop ? xs : loop;
 }
 
@@ -234,35 +248,72 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
   float* part = reinterpret_cast<float*>(smem);
   const int T8 = T >> 3;
 
-  // State of the job being computed (work-group uniform except xr/m8xsum).
+  // State of the job being computed (work-group uniform except the limbs).
   GemvJob J = get(j0);
   int cj = j0;
   int seg_end = s_begin;  // end of this work-group's steps of job cj
   int job_last = 0;       // the job's last global step
   int last_units = 0;     // blocks in that step
   int c0 = s_begin;       // first step of the open partial-sum chunk
-  float xr[32];
-  float m8xsum = 0.0f;
+  u32x4 xl[kLimbs];     // this lane's block column of x as i4 limbs
+  int xe = 0;           // its exponent: x = 2^xe * sum_k 16^k * digit_k
+  float xnan = 0.0f;    // NaN when the block holds a non-finite activation
 
   // Sum the parked partials of steps [c0, c1) into y (one thread per row, in
-  // a fixed order).
+  // a fixed order).  Row starts in `part` are 16-byte aligned when B8 % 4 == 0
+  // and 8-byte aligned when B8 is even (T8 is a multiple of 8), so the reads
+  // are vectorised with independent partial sums.  The bias branch is
+  // uniform and kept apart: a bias load waited for in the common path would
+  // also wait for every ring load in flight.
+  auto row_sum = [&](const float* pr, int B8) -> float {
+    if ((B8 & 3) == 0) {
+      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+      const float4* p4 = reinterpret_cast<const float4*>(pr);
+#pragma unroll 1
+      for (int q = 0; q < (B8 >> 2); q++) {
+        const float4 v = p4[q];
+        a0 += v.x; a1 += v.y; a2 += v.z; a3 += v.w;
+      }
+      return (a0 + a1) + (a2 + a3);
+    }
+    if ((B8 & 1) == 0) {
+      float a0 = 0.0f, a1 = 0.0f;
+      const float2* p2 = reinterpret_cast<const float2*>(pr);
+#pragma unroll 1
+      for (int q = 0; q < (B8 >> 1); q++) {
+        const float2 v = p2[q];
+        a0 += v.x; a1 += v.y;
+      }
+      return a0 + a1;
+    }
+    float a0 = 0.0f;
+    for (int q = 0; q < B8; q++) a0 += pr[q];
+    return a0;
+  };
   auto flush = [&](int c1) {
     __syncthreads();
     const int rps = J.rps, B8 = J.B >> 3;
     const int row0 = (c0 - J.step0) * rps;
     const int nrows = min((c1 - c0) * rps, J.n - row0);
-    for (int r = t; r < nrows; r += T) {
-      const int sl = r / rps;
-      const float* pr = part + sl * T8 + (r - sl * rps) * B8;
-      float v = 0.0f;
-      for (int q = 0; q < B8; q++) v += pr[q];
-      J.y[row0 + r] = v + (J.bias ? J.bias[row0 + r] : 0.0f);
+    float* yr = J.y + row0;
+    if (J.bias == nullptr) {
+      for (int r = t; r < nrows; r += T) {
+        const int sl = r / rps;
+        yr[r] = row_sum(part + sl * T8 + (r - sl * rps) * B8, B8);
+      }
+    } else {
+      const float* br = J.bias + row0;
+      for (int r = t; r < nrows; r += T) {
+        const int sl = r / rps;
+        yr[r] = row_sum(part + sl * T8 + (r - sl * rps) * B8, B8) + br[r];
+      }
     }
     __syncthreads();
   };
-  // Make job j current at global step g: stage its activations (coalesced,
-  // through LDS: float4 q of block b at 8b + (q ^ (b & 7)), so the per-lane
-  // reads do not conflict) and keep this lane's 32 in registers.
+  // Make job j current at global step g: convert its activations to i4 limbs
+  // (cooperatively: thread i handles elements [8i, 8i+8) of x, four threads
+  // per block), park them in LDS as [limb][block][4 dwords] plus one
+  // exponent per block, and keep this lane's block column in registers.
   auto enter = [&](int j, int g) {
     J = get(j);
     cj = j;
@@ -272,28 +323,42 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
     seg_end = min(s_end, J.step0 + steps);
     c0 = g;
     const int B = J.B;
-    float4* xs = reinterpret_cast<float4*>(smem);
+    uint32_t* limbs = reinterpret_cast<uint32_t*>(smem);
+    int* exps = reinterpret_cast<int*>(smem + (size_t)kLimbs * 16 * B);
     const float4* xv = reinterpret_cast<const float4*>(J.x);
-    for (int i = t; i < B * 8; i += T) {
-      const int b = i >> 3;
-      xs[(b << 3) + ((i & 7) ^ (b & 7))] = load_global<float4>(xv + i);
+    for (int i = t; i < B * 4; i += T) {  // whole 4-thread groups stay together
+      const float4 v0 = load_global<float4>(xv + 2 * i);
+      const float4 v1 = load_global<float4>(xv + 2 * i + 1);
+      const float xs[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+      // Largest |x| of the block by its bit pattern (ordered like the value
+      // for non-negative floats; inf and NaN compare above every finite).
+      uint32_t mb = 0;
+#pragma unroll
+      for (int k = 0; k < 8; k++) mb = max(mb, __float_as_uint(xs[k]) & 0x7FFFFFFFu);
+      mb = max(mb, (uint32_t)__shfl_xor((int)mb, 1, 64));
+      mb = max(mb, (uint32_t)__shfl_xor((int)mb, 2, 64));
+      const int e = __builtin_amdgcn_frexp_expf(__uint_as_float(mb));  // amax < 2^e
+      uint32_t u[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++)
+        u[k] = (uint32_t)((int)rintf(ldexpf(xs[k], kMantBits - e)) + kDigitBias);
+#pragma unroll
+      for (int l = 0; l < kLimbs; l++) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) w |= ((u[k] >> (4 * l)) & 15u) << (4 * k);
+        limbs[(l * B * 4) + i] = w ^ 0x88888888u;
+      }
+      if ((i & 3) == 0) exps[i >> 2] = mb >= 0x7F800000u ? kBadExp : e - kMantBits;
     }
     __syncthreads();
     const int kb = t % B;
-    const float4* mine = xs + (kb << 3);
 #pragma unroll
-    for (int q = 0; q < 8; q++) {
-      const float4 v = mine[q ^ (kb & 7)];
-      xr[4 * q + 0] = v.x;
-      xr[4 * q + 1] = v.y;
-      xr[4 * q + 2] = v.z;
-      xr[4 * q + 3] = v.w;
-    }
-    // The -8 offset of every nibble is applied once per block as -8 * sum(x).
-    float xsum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; i++) xsum += xr[i];
-    m8xsum = -8.0f * xsum;
+    for (int l = 0; l < kLimbs; l++)
+      xl[l] = *reinterpret_cast<const u32x4*>(limbs + l * B * 4 + kb * 4);
+    const int ex = exps[kb];
+    xe = ex == kBadExp ? 0 : ex;
+    xnan = ex == kBadExp ? __builtin_nanf("") : 0.0f;
     __syncthreads();  // the activation region becomes partial space
   };
 
@@ -314,11 +379,23 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
     if (t < vu) {
       const uint32_t d[5] = {sl.a.x, sl.a.y, sl.a.z, sl.a.w, sl.b};
       const float scale = f16_bits_to_f32(d[0] >> sh_d);
-      float acc = 0.0f;
+      // D_l = sum_i (nib_i - 8) * digit_l(x_i): nib ^ 8 read as signed i4 is
+      // nib - 8; eight products per v_dot8_i32_i4, exact in int32.
+      int acc[kLimbs] = {};
 #pragma unroll
-      for (int j = 0; j < 4; j++)
-        acc += dot8_nib(__builtin_amdgcn_perm(d[j + 1], d[j], sel_q), xr + 8 * j);
-      partial = scale * (acc + m8xsum);
+      for (int j = 0; j < 4; j++) {
+        const uint32_t q = __builtin_amdgcn_perm(d[j + 1], d[j], sel_q) ^ 0x88888888u;
+#pragma unroll
+        for (int l = 0; l < kLimbs; l++)
+          acc[l] = __builtin_amdgcn_sdot8((int)q, (int)xl[l][j], acc[l], false);
+      }
+      // sum_l 16^l * D_l: the top five limbs in int32 (|h| < 2^28), the last
+      // step in fp32.
+      int h = acc[kLimbs - 1];
+#pragma unroll
+      for (int l = kLimbs - 2; l >= 1; l--) h = (h << 4) + acc[l];
+      const float r = fmaf((float)h, 16.0f, (float)acc[0]);
+      partial = ldexpf(scale * r, xe) + xnan;
     }
     partial = group8_sum(partial);
     if ((t & 7) == 7) part[(ss - c0) * T8 + (t >> 3)] = partial;
