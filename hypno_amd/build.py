@@ -21,7 +21,7 @@ OBJ_DIR = os.path.join(HERE, "_build")
 LIB_NAME = "libhypno_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 
-SOURCES = ["codec.hip", "gemv_q4_0.hip", "gemv_f16.hip", "gemm.hip", "api.cpp"]
+SOURCES = ["codec.hip", "gemv_q4_0.hip", "gemv_f16.hip", "gemm.hip", "gemm_q4.hip", "api.cpp"]
 
 ARCH = "gfx950"
 COMMON_FLAGS = [
@@ -33,6 +33,9 @@ COMMON_FLAGS = [
     "-Wno-unused-function",
     # Packed FP32 (v_pk_{add,mul,fma}_f32) stays off in all device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: the fp32 epilogue math reads them directly
+    # instead of copying each accumulator out of AGPRs first.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{os.path.join(ROOT, 'include')}",
 ]
 

@@ -133,7 +133,8 @@ int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
     cus = ds->cus;
   }
   hipError_t e;
-  if (batch >= kGemmMinBatch && q4_0_gemm_ok(w, w_len, n, m, batch)) {
+  const bool v3 = batch >= kGemmMinBatch && q4_0_gemm_v3_ok(w, w_len, n, m, batch);
+  if (v3 || (batch >= kGemmMinBatch && q4_0_gemm_ok(w, w_len, n, m, batch))) {
     void* ws = nullptr;
     {
       std::lock_guard<std::mutex> g(g_mu);
@@ -142,7 +143,8 @@ int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
       if (e != hipSuccess) return hip_fail(e, "GEMM workspace");
       ws = b.p;
     }
-    e = launch_q4_0_gemm(y, w, x, bias, n, m, batch, ws, cus, s);
+    e = v3 ? launch_q4_0_gemm_v3(y, w, x, bias, n, m, batch, ws, cus, s)
+           : launch_q4_0_gemm(y, w, x, bias, n, m, batch, ws, cus, s);
     if (e != hipSuccess) return hip_fail(e, "q4_0 GEMM launch");
     return HYPNO_HIP_OK;
   }

@@ -229,8 +229,8 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
     }
     pg++;
     Slot r;
-    r.a = load_global<u32x4>(p);
-    r.b = load_global<uint32_t>(p + 16);
+    r.a = load_global_nt<u32x4>(p);
+    r.b = load_global_nt<uint32_t>(p + 16);
     return r;
   };
   Slot ring0 = issue();  // ring0 holds steps s_begin, s_begin+3, ...

@@ -297,8 +297,11 @@ def test_gemm_q4_0(torch, hk, orc, batch, n, m):
         assert orc.rel_l2(got[t], r32) <= GEMM_TOL
 
 
-def test_gemm_bias_and_tails(torch, hk, orc):
-    batch, n, m = 33, 130, 320   # M and N tails; m % 64 == 0 but not % 256
+@pytest.mark.parametrize("m", [320, 384])
+def test_gemm_bias_and_tails(torch, hk, orc, m):
+    # M and N tails with a bias; m = 320 takes the 64-column kernel, m = 384
+    # the 128-column-stage kernel
+    batch, n = 33, 130
     q = _q4(orc, n, m, seed=5)
     x = orc.normal_f32(6, (batch, m))
     bias = orc.normal_f32(7, n)
