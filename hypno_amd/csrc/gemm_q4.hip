@@ -6,34 +6,37 @@
 // accumulator, and the block's partial sum is scaled by the block's fp32
 // scale into fp32 accumulators (acc += d * partial).  That scale FMA is one
 // VALU op per output per block -- as much issue time as the MFMA itself -- so
-// the kernel is organised to keep VALU work besides it small and to overlap
-// it with the matrix pipe:
+// the kernel keeps other VALU work small and overlaps the FMAs with the
+// matrix pipe:
 //
-//  * Work-group = 512 threads (8 waves) on a 128 x 128 tile of Y; one
-//    work-group per CU, two waves per SIMD.  Waves 0-3 and 4-7 form two
-//    K-groups: each stage holds 128 columns of K (four Q4_0 blocks) and
-//    K-group g multiplies blocks 2g and 2g+1 of it, with its four waves in a
-//    2 x 2 grid of 64 x 64 sub-tiles (4 x 4 MFMA tiles per wave).  At the end
-//    K-group 1 hands its accumulators to K-group 0 through LDS (a fixed-order
-//    sum: deterministic, no atomics, no zeroed output).
-//  * Activations: a pre-pass rounds X to fp16 once, permuting each group of 8
-//    columns into the order in which the nibble unpack below emits weights.
-//    Each stage's 128 x 128 fp16 X tile is copied straight into LDS with
-//    global_load_lds_dwordx4 (no registers, no VALU); the source address of
-//    each lane is chosen so that 16-byte chunk c of row r lands in slot
-//    c ^ (r & 15) of that row (conflict-free MFMA operand reads).
-//  * Weights: each thread fetches one block (a 20-byte window: dwordx4 +
-//    dword) two stages ahead into registers, and one stage ahead expands it
-//    into LDS as exact fp16 (nib - 8) with two and-or ops and one packed fp16
-//    op per pair of weights, plus the block's fp32 scale.  The expansion is
-//    done once per work-group and shared by all 128 rows of X.
-//  * Two LDS stages (A tile, B tile, scales = 66 KB each) alternate; one
-//    barrier per stage.
+//  * Work-group = 512 threads (8 waves) on a 128 x 128 tile of Y, one per CU,
+//    two waves per SIMD.  A stage is 64 columns of K (two Q4_0 blocks); waves
+//    0-3 (K-group 0) multiply block 0 of every stage and waves 4-7 block 1,
+//    each wave a 64 x 64 sub-tile (4 x 4 MFMA tiles).  At the end K-group 1
+//    hands its accumulators to K-group 0 through LDS (fixed-order sum:
+//    deterministic, no atomics, no zeroed output).
+//  * All global reads are LDS DMA (global_load_lds_dwordx4), issued
+//    kPrefetch stages ahead into LDS rings: no staging registers, and every
+//    wave issues exactly three DMA instructions per stage, so one
+//    s_waitcnt vmcnt(3) per stage waits for precisely the data the next
+//    stage needs.
+//      - X: a pre-pass rounds X to fp16 once, permuting each group of 8
+//        columns into the order the nibble unpack emits weights.  Each
+//        stage's 128 x 64 tile lands with 16-byte chunk c of row r in slot
+//        c ^ ((r >> 1) & 7) (conflict-free MFMA operand reads).
+//      - W: each row's 36 bytes of the stage arrive as a 64-byte window
+//        starting at the 16-byte boundary at or below them.
+//  * Two stages ahead, every thread expands a quarter of a row's stage (one
+//    half block) from the raw window into an fp16 (nib - 8) tile with one
+//    and-or op and one packed fp16 op per pair of weights, plus the block
+//    scale as fp32.  The expansion is shared by all 128 rows of X.
+//  * While a stage's MFMAs run from registers, the operands of the next
+//    stage are already being read from LDS into a second register set, so
+//    LDS latency hides behind the matrix work.  One barrier per stage.
 //
-// Requirements (checked by q4_0_gemm_v3_ok): K % 128 == 0, w 4-byte aligned,
-// w holds N whole rows.  Tiles at the N and M edges are handled by clamping
-// the rows read (their scale is zeroed) and not storing rows/columns past
-// the edge.
+// Requirements (q4_0_gemm_v3_ok): K % 256 == 0 (rows of W start on 16-byte
+// boundaries), w 16-byte aligned, w holds N whole rows.  Rows past N read
+// row N-1 with a zero scale; rows/columns past M/N are not stored.
 #include "common.hpp"
 
 namespace hypno {
@@ -46,17 +49,54 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128;
 constexpr int BN = 128;
-constexpr int BK = 128;                      // four Q4_0 blocks per stage
+constexpr int BK = 64;          // two Q4_0 blocks per stage
 constexpr int kThreads = 512;
-constexpr int kRowBytes = BK * 2;            // one LDS tile row: 128 fp16
-constexpr int kTileBytes = BM * kRowBytes;   // 32 KB
-constexpr int kScaleBytes = (BK / 32) * BN * 4;
-constexpr int kStageBytes = 2 * kTileBytes + kScaleBytes;
-constexpr int kLdsBytes = 2 * kStageBytes;   // 132 KB (< 160 KB)
+constexpr int kPrefetch = 4;    // stages of DMA in flight ahead of the compute
+constexpr int kARing = kPrefetch;       // stage s+1 read while s+2..s+4 land
+constexpr int kRawRing = kPrefetch - 1; // stage s+2 expanded while s+3, s+4 land
+constexpr int kBRing = 2;               // stage s+1 read while s+2 is written
+constexpr int kRowBytes = BK * 2;           // 128 B: one fp16 tile row
+constexpr int kTileBytes = BM * kRowBytes;  // 16 KB
+constexpr int kRawRow = 64;                 // raw W window per row and stage
+constexpr int kRawBytes = BN * kRawRow;     // 8 KB
+constexpr int kScaleBytes = 2 * BN * 4;     // 1 KB
+constexpr int kOffA = 0;
+constexpr int kOffRaw = kOffA + kARing * kTileBytes;
+constexpr int kOffB = kOffRaw + kRawRing * kRawBytes;
+constexpr int kOffS = kOffB + kBRing * kTileBytes;
+constexpr int kLdsBytes = kOffS + kBRing * kScaleBytes;  // 122 KB (< 160 KB)
+static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+static_assert(4 * 64 * 64 * 4 <= kOffRaw, "K-group reduction fits in the A ring");
 
-// Byte offset of 16-byte chunk c of tile row r (XOR-swizzled by the row).
+// End of stage s: every wave waits until its DMAs of all stages but the
+// newest (s + kPrefetch) have landed -- vmcnt counts this wave's outstanding
+// DMAs, three per stage -- and its LDS writes are done; then the work-group
+// meets at the barrier.  One asm statement with a memory clobber: the
+// compiler neither moves LDS accesses across it nor adds the vmcnt(0) that a
+// fence-based __syncthreads() would (which would drain the prefetch ring).
+static_assert(kPrefetch == 4, "stage_barrier's vmcnt(3) is one stage of DMAs");
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+// The same, split around LDS reads that need only this wave's own DMAs:
+// stage_wait() before them, then barrier_only().
+__device__ __forceinline__ void stage_wait() {
+  asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)" ::: "memory");
+}
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
+// Byte offset of 16-byte chunk c (0..7) of tile row r.
 __device__ __forceinline__ uint32_t tile_off(int r, int c) {
-  return (uint32_t)(r * kRowBytes + ((c ^ (r & 15)) << 4));
+  return (uint32_t)(r * kRowBytes + ((c ^ ((r >> 1) & 7)) << 4));
+}
+
+// (a & b) | c in one v_and_or_b32 (the compiler emits two ops when b and c
+// are both literals).  VOP3 reads at most one SGPR here, so the mask b sits
+// in a VGPR and c in an SGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(c));
+  return r;
 }
 
 // Eight nibbles (byte i of q = e[2i] | e[2i+1] << 4) -> eight exact fp16
@@ -68,10 +108,10 @@ __device__ __forceinline__ u32x4 unpack8(uint32_t q) {
   const half2v hi_mul = {(_Float16)0.0625f, (_Float16)0.0625f};
   const half2v hi_off = {(_Float16)-72.0f, (_Float16)-72.0f};
   const uint32_t q8 = q >> 8;
-  const uint32_t p0 = (q & 0x000F000Fu) | 0x64006400u;   // e0, e4
-  const uint32_t p1 = (q & 0x00F000F0u) | 0x64006400u;   // e1, e5 (x16)
-  const uint32_t p2 = (q8 & 0x000F000Fu) | 0x64006400u;  // e2, e6
-  const uint32_t p3 = (q8 & 0x00F000F0u) | 0x64006400u;  // e3, e7 (x16)
+  const uint32_t p0 = and_or(q, 0x000F000Fu, 0x64006400u);   // e0, e4
+  const uint32_t p1 = and_or(q, 0x00F000F0u, 0x64006400u);   // e1, e5 (x16)
+  const uint32_t p2 = and_or(q8, 0x000F000Fu, 0x64006400u);  // e2, e6
+  const uint32_t p3 = and_or(q8, 0x00F000F0u, 0x64006400u);  // e3, e7 (x16)
   u32x4 r;
   r[0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, p0) + lo_off);
   r[1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
@@ -82,10 +122,12 @@ __device__ __forceinline__ u32x4 unpack8(uint32_t q) {
   return r;
 }
 
-struct Raw {  // one thread's 20-byte window of one stage
-  u32x4 a;
-  uint32_t b;
-};
+// One wave-wide 16-byte-per-lane DMA: lane i's 16 bytes at `src` land at
+// lds_wave_base + 16 * i.
+__device__ __forceinline__ void dma16(const void* src, uint8_t* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_wave_base,
+                                   16, 0, 0);
+}
 
 struct Args {
   float* y;
@@ -101,7 +143,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   extern __shared__ __align__(16) uint8_t smem[];
   const int t = threadIdx.x;
   const int lane = t & 63;
-  const int wave = t >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int kgrp = wave >> 2;
   const int wm = (wave >> 1) & 1;
   const int wn = wave & 1;
@@ -117,52 +159,99 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   if (a.xcd_map) tile = (tile & 7) * (ntiles >> 3) + (tile >> 3);
   const int m0 = (tile % a.tiles_m) * BM;
   const int n0 = (tile / a.tiles_m) * BN;
-  const int K = a.K;
-  const int steps = K / BK;
-  const size_t x_row = (size_t)K * 2;
-  const size_t w_row = (size_t)(K / 32) * 18;
+  const int steps = a.K / BK;
+  const size_t x_row = (size_t)a.K * 2;
+  const size_t w_row = (size_t)(a.K / 32) * 18;
 
-  // --- activation copy (LDS DMA): wave w, instruction i fills LDS segment
-  // i*8 + w (rows 4*seg .. 4*seg+3 of the tile, 1 KB); lane -> row
-  // 4*seg + lq, physical chunk lr, i.e. logical chunk lr ^ (row & 15).
-  const int arow0 = 4 * wave + lq;               // row for i = 0 (row & 15 same for all i)
-  const int achunk = lr ^ (arow0 & 15);
-  const uint8_t* xsrc = a.xh + (size_t)(m0 + arow0) * x_row + achunk * 16;
-  auto copy_a = [&](int s, int buf) {
-    const uint8_t* src = xsrc + (size_t)s * BK * 2;
-    uint8_t* dst = smem + buf * kStageBytes + wave * 1024;
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-      __builtin_amdgcn_global_load_lds(
-          (const void*)(src + (size_t)i * 32 * x_row),
-          (__attribute__((address_space(3))) void*)(dst + i * 8 * 1024), 16, 0, 0);
+  // --- X DMA: wave w, instruction i fills rows 64i + 8w .. +7 (1 KB); lane
+  // -> row 64i + 8w + (lane >> 3), slot lane & 7 = logical chunk
+  // (lane & 7) ^ ((row >> 1) & 7), and (row >> 1) & 7 does not depend on i.
+  const int xr = 8 * wave + (lane >> 3);
+  const int xc = (lane & 7) ^ ((xr >> 1) & 7);
+  const uint8_t* xsrc = a.xh + (size_t)(m0 + xr) * x_row + xc * 16;
+  // --- W DMA: wave w fills rows 16w .. 16w+15 (1 KB): lane -> row
+  // 16w + (lane >> 2) (rows past N read row N-1), 16-byte piece lane & 3 of
+  // the row's 64-byte window at the 16-byte boundary at or below the stage's
+  // 36 bytes.  At the last stage that window would run 16 bytes past the
+  // row (and past the end of W for row N-1), so there every window starts
+  // 16 bytes earlier: it then ends exactly at the row's end.
+  const int wrow = min(n0 + 16 * wave + (lane >> 2), a.N - 1);
+  const uint8_t* wsrc = a.w + (size_t)wrow * w_row + (lane & 3) * 16;
+  auto win_start = [&](int s) -> int {  // window start relative to the row
+    return ((s * 36) & ~15) - (s == steps - 1 ? 16 : 0);
+  };
+  auto issue = [&](int s) {  // DMA of stage min(s, steps-1) into the ring slots of s
+    const int sc = s < steps ? s : steps - 1;
+    uint8_t* adst = smem + kOffA + (s % kARing) * kTileBytes + wave * 1024;
+    const uint8_t* asrc = xsrc + (size_t)sc * kRowBytes;
+    dma16(asrc, adst);
+    dma16(asrc + 64 * x_row, adst + 8 * 1024);
+    uint8_t* rdst = smem + kOffRaw + (s % kRawRing) * kRawBytes + wave * 1024;
+    dma16(wsrc + win_start(sc), rdst);
   };
 
-  // --- weight fetch: thread -> (row br, block bb) of the stage
-  const int br = t >> 2, bb = t & 3;
-  const bool bvalid = n0 + br < a.N;
-  const uint8_t* wsrc = a.w + (size_t)(bvalid ? n0 + br : a.N - 1) * w_row + ((18 * bb) & ~3);
-  const bool bodd = (bb & 1) != 0;  // block starts 2 bytes into its window
-  const uint32_t sel = bodd ? 0x07060504u : 0x05040302u;
-  const uint32_t dsh = bodd ? 16u : 0u;
-  auto fetch_b = [&](int s) -> Raw {
-    const uint8_t* p = wsrc + (size_t)s * (BK / 32) * 18;
-    Raw r;
-    r.a = load_global<u32x4>(p);
-    r.b = load_global<uint32_t>(p + 16);
-    return r;
+  // --- expansion role: thread -> row er, block eb of the stage, half eh
+  const int er = t >> 2, eb = (t >> 1) & 1, eh = t & 1;
+  const bool evalid = n0 + er < a.N;
+  const uint32_t esel = eb ? 0x07060504u : 0x05040302u;  // block at byte 0 / 2 mod 4
+  // byte of the row's window where this thread's 12 bytes start, minus the
+  // stage's window offset (a multiple of 4); 18 * eb + 8 * eh = 2 mod 4 for
+  // eb = 1, so the dword-aligned start is 18 * eb + 8 * eh - 2 * eb
+  const uint32_t eoff = er * kRawRow + 16 * eb + 8 * eh;
+  const uint32_t boff0 = tile_off(er, 4 * eb + 2 * eh);
+  const uint32_t boff1 = tile_off(er, 4 * eb + 2 * eh + 1);
+  const uint32_t soff = (((eb * 2 + (er >> 6)) * 16 + (er & 15)) * 4 + ((er & 63) >> 4)) * 4;
+
+  // Expansion in two parts: the raw reads go out first in a stage, the
+  // unpack (VALU) is interleaved with that stage's MFMAs, the writes close it.
+  struct RawW {
+    uint32_t d0, d1, d2;
   };
-  auto expand_b = [&](const Raw& r, int buf) {
-    uint8_t* bt = smem + buf * kStageBytes + kTileBytes;
-    float* sc = reinterpret_cast<float*>(smem + buf * kStageBytes + 2 * kTileBytes);
-    const uint32_t d[5] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b};
-    sc[((bb * 2 + (br >> 6)) * 16 + (br & 15)) * 4 + ((br & 63) >> 4)] =
-        bvalid ? f16_bits_to_f32((d[0] >> dsh) & 0xFFFFu) : 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const uint32_t q = __builtin_amdgcn_perm(d[j + 1], d[j], sel);
-      *reinterpret_cast<u32x4*>(bt + tile_off(br, 4 * bb + j)) = unpack8(q);
-    }
+  auto expand_read = [&](int s) -> RawW {
+    // offset of the stage's first byte in the window: 0, 4, 8 or 12; 28 at
+    // the last stage
+    const int o = s * 36 - win_start(s);
+    const uint8_t* p = smem + kOffRaw + (s % kRawRing) * kRawBytes + o + eoff;
+    const uint32_t* d = reinterpret_cast<const uint32_t*>(p);
+    return RawW{d[0], d[1], d[2]};
+  };
+  struct Expanded {
+    u32x4 lo, hi;
+    float scale;
+  };
+  auto expand_unpack = [&](const RawW& r) -> Expanded {
+    Expanded e;
+    e.lo = unpack8(__builtin_amdgcn_perm(r.d1, r.d0, esel));
+    e.hi = unpack8(__builtin_amdgcn_perm(r.d2, r.d1, esel));
+    const uint32_t dbits = (r.d0 >> (eb ? 16 : 0)) & 0xFFFFu;
+    e.scale = evalid ? f16_bits_to_f32(dbits) : 0.0f;
+    return e;
+  };
+  auto expand_write = [&](int s, const Expanded& e) {
+    uint8_t* bt = smem + kOffB + (s % kBRing) * kTileBytes;
+    *reinterpret_cast<u32x4*>(bt + boff0) = e.lo;
+    *reinterpret_cast<u32x4*>(bt + boff1) = e.hi;
+    if (eh == 0)
+      *reinterpret_cast<float*>(smem + kOffS + (s % kBRing) * kScaleBytes + soff) = e.scale;
+  };
+  auto expand = [&](int s) { expand_write(s, expand_unpack(expand_read(s))); };
+
+  // MFMA operands of this wave's block (kb = kgrp) of one stage: one
+  // register set for A and one for B, each operand reloaded in place for the
+  // next stage right after its last MFMA of this stage; the block scales are
+  // double-buffered.
+  const uint32_t fchunk = ((4 * kgrp + lq) ^ ((lr >> 1) & 7)) << 4;
+  const uint32_t fa_off = (wm * 64 + lr) * kRowBytes + fchunk;
+  const uint32_t fb_off = (wn * 64 + lr) * kRowBytes + fchunk;
+  const uint32_t fs_off = ((kgrp * 2 + wn) * 16 + lr) * 16;
+  auto a_addr = [&](int s, int i) -> uint32_t {
+    return (uint32_t)(kOffA + (s % kARing) * kTileBytes) + fa_off + i * 16 * kRowBytes;
+  };
+  auto b_addr = [&](int s, int j) -> uint32_t {
+    return (uint32_t)(kOffB + (s % kBRing) * kTileBytes) + fb_off + j * 16 * kRowBytes;
+  };
+  auto read_sc = [&](int s) -> floatx4 {
+    return *reinterpret_cast<const floatx4*>(smem + kOffS + (s % kBRing) * kScaleBytes + fs_off);
   };
 
   floatx4 acc[4][4];
@@ -171,95 +260,107 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // One stage for this wave: its two blocks kb = 2*kgrp, 2*kgrp + 1.  The
-  // operands of the second block are read from LDS before the first block's
-  // MFMAs start.  MFMA q = 4i + j; its partial is scaled in after MFMA
+  // Stage s's MFMAs.  MFMA q = 4i + j; its partial is scaled in after MFMA
   // q + kLag has been issued, so the FMAs do not wait on the matrix pipe and
-  // at most kLag + 1 partials are live.  Hard scheduling barriers keep this
-  // order (the default scheduler would issue all 32 MFMAs first).
-  struct Frags {
-    half8 a[4], b[4];
-    floatx4 sc;
-  };
-  auto read_frags = [&](int buf, int kb) -> Frags {
-    const uint8_t* at = smem + buf * kStageBytes;
-    const uint8_t* bt = at + kTileBytes;
-    const uint8_t* st = at + 2 * kTileBytes;
-    const int c = ((4 * kb + lq) ^ lr) << 4;
-    Frags f;
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-      f.a[i] = *reinterpret_cast<const half8*>(at + (wm * 64 + 16 * i + lr) * kRowBytes + c);
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-      f.b[j] = *reinterpret_cast<const half8*>(bt + (wn * 64 + 16 * j + lr) * kRowBytes + c);
-    f.sc = *reinterpret_cast<const floatx4*>(st + ((kb * 2 + wn) * 16 + lr) * 16);
-    return f;
-  };
+  // at most kLag + 2 partials are live.  The order is pinned by one empty
+  // asm statement per step (the default schedule would issue all MFMAs first
+  // and hold every partial at once, or scale a partial right behind its own
+  // MFMA and stall): statement q comes after MFMA q (it reads partial q),
+  // after the FMAs of partial q - kLag - 1 (it passes that accumulator
+  // through), and before the FMAs of partial q - kLag and MFMA q + 1 (it
+  // passes their operands through).  The scheduling groups then place up to
+  // six VALU ops after each MFMA -- the scale FMAs plus the weight unpack.
+  // A operand i is reloaded for stage `nx` right after MFMA 4i+3 and B
+  // operand j right after MFMA 12+j, from one base address per tile that
+  // also passes through the statements (which orders the loads); the
+  // unpacked weights of stage `xs` (raw words `rw`) go to LDS early.
   constexpr int kLag = 3;
-  auto mma_block = [&](Frags f) {
+  auto mma = [&](half8 (&fa)[4], half8 (&fb)[4], const floatx4& sc, int nx, const RawW& rw,
+                 int xs) {
     floatx4 part[16];
+    uint32_t abase = a_addr(nx < 0 ? 0 : nx, 0);
+    uint32_t bbase = b_addr(nx < 0 ? 0 : nx, 0);
 #pragma unroll
     for (int q = 0; q < 16 + kLag; q++) {
-      if (q < 16)
-        part[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.a[q >> 2], f.b[q & 3],
+      const int u = q - kLag;
+      if (q < 16) {
+        part[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[q >> 2], fb[q & 3],
                                                          floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-      if (q >= kLag) {
-        const int u = q - kLag;
+        const int i1 = (q + 1 < 16) ? (q + 1) >> 2 : 3;
+        if (u >= 1)
+          asm volatile("" : "+v"(fa[i1]), "+v"(part[u]), "+v"(acc[(u - 1) >> 2][(u - 1) & 3]),
+                       "+v"(abase), "+v"(bbase) : "v"(part[q]));
+        else if (u == 0)
+          asm volatile("" : "+v"(fa[i1]), "+v"(part[u]), "+v"(abase), "+v"(bbase)
+                       : "v"(part[q]));
+        else
+          asm volatile("" : "+v"(fa[i1]), "+v"(abase), "+v"(bbase) : "v"(part[q]));
+        if (nx >= 0) {
+          if ((q & 3) == 3)
+            fa[q >> 2] = *reinterpret_cast<const half8*>(smem + abase + (q >> 2) * 16 * kRowBytes);
+          if (q >= 12)
+            fb[q & 3] = *reinterpret_cast<const half8*>(smem + bbase + (q & 3) * 16 * kRowBytes);
+        }
+      }
+      if (u >= 0) {
 #pragma unroll
         for (int r = 0; r < 4; r++)
-          acc[u >> 2][u & 3][r] = fmaf(f.sc[u & 3], part[u][r], acc[u >> 2][u & 3][r]);
-        // Order MFMA q+1 after these FMAs: its A operand passes through an
-        // (empty) statement that also takes the accumulator just written.
-        if (q + 1 < 16) asm volatile("" : "+v"(f.a[(q + 1) >> 2]), "+v"(acc[u >> 2][u & 3]));
+          acc[u >> 2][u & 3][r] = fmaf(sc[u & 3], part[u][r], acc[u >> 2][u & 3][r]);
       }
+      if (q == 2 && xs >= 0) expand_write(xs, expand_unpack(rw));
+      if (q < 16) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
     }
   };
-  auto compute = [&](int buf) {
-    const Frags f0 = read_frags(buf, 2 * kgrp);
-    const Frags f1 = read_frags(buf, 2 * kgrp + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    mma_block(f0);
-    mma_block(f1);
-  };
 
-  // Prologue: stage 0 in LDS buffer 0, stage 1's weights in registers.
-  Raw raw0 = fetch_b(0);
-  Raw raw1 = raw0;
-  if (steps > 1) raw1 = fetch_b(1);
-  copy_a(0, 0);
-  expand_b(raw0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  // Stage s: start the copy of stage s+1's activations into the other buffer
-  // and the fetch of stage s+2's weights, compute stage s, expand stage s+1's
-  // weights (fetched a stage ago), then wait for everything and barrier.
-  // Unrolled by two so the register double buffer has static names.
-  for (int s = 0; s < steps; s += 2) {
-    {
-      const bool more = s + 1 < steps;
-      if (more) copy_a(s + 1, 1);
-      if (s + 2 < steps) raw0 = fetch_b(s + 2);
-      compute(0);
-      if (more) expand_b(raw1, 1);
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      if (!more) break;
-    }
-    {
-      const bool more = s + 2 < steps;
-      if (more) copy_a(s + 2, 0);
-      if (s + 3 < steps) raw1 = fetch_b(s + 3);
-      compute(1);
-      if (more) expand_b(raw0, 0);
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-    }
+  // Prologue: DMA of stages 0..2 (the raw ring holds three stages), B tiles
+  // of stages 0 and 1, operands of stage 0, then stage 3's DMA (its raw
+  // bytes reuse stage 0's slot, free once stage 0 is expanded).
+  issue(0);
+  issue(1);
+  issue(2);
+  __syncthreads();  // all of it landed (vmcnt(0))
+  expand(0);
+  expand(1);
+  stage_barrier();
+  half8 fa[4], fb[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    fa[i] = *reinterpret_cast<const half8*>(smem + a_addr(0, i));
+    fb[i] = *reinterpret_cast<const half8*>(smem + b_addr(0, i));
   }
+  floatx4 sc0 = read_sc(0), sc1;
+  issue(3);
+  stage_barrier();
+
+  // Stage s (operands of s and raw words of s+2 already in registers): DMA
+  // of stage s+4; LDS read of stage s+1's scales; MFMAs of stage s with the
+  // reloads of stage s+1's operands and the unpack/writes of stage s+2's B
+  // tile woven in; then wait for stage s+3's DMAs (stage s+2's X, s+3's W),
+  // read stage s+3's raw words and barrier.  Unrolled by two so the scale
+  // double buffer has static names (steps is even).
+  // A wave expands exactly the W rows its own DMAs fetched, so the raw reads
+  // for the next stage need only this wave's DMA wait, not the barrier:
+  // they are issued between the two and are in flight across the barrier.
+  RawW rw = expand_read(2);
+  for (int s = 0; s < steps; s += 2) {
+    issue(s + kPrefetch);
+    sc1 = read_sc(s + 1);
+    mma(fa, fb, sc0, s + 1, rw, s + 2 < steps ? s + 2 : -1);
+    stage_wait();
+    rw = expand_read(min(s + 3, steps - 1));
+    barrier_only();
+    issue(s + 1 + kPrefetch);
+    if (s + 2 < steps) sc0 = read_sc(s + 2);
+    mma(fa, fb, sc1, s + 2 < steps ? s + 2 : -1, rw, s + 3 < steps ? s + 3 : -1);
+    stage_wait();
+    rw = expand_read(min(s + 4, steps - 1));
+    barrier_only();
+  }
+  __syncthreads();  // trailing DMAs (re-loads of the last stage) have landed
 
   // K-group 1 -> LDS -> K-group 0 adds (fixed order) and stores.
-  float* red = reinterpret_cast<float*>(smem);
+  float* red = reinterpret_cast<float*>(smem + kOffA);
   const int wig = wave & 3;
   if (kgrp == 1) {
 #pragma unroll
@@ -291,8 +392,8 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
 }  // namespace
 
 bool q4_0_gemm_v3_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t batch) {
-  if (m == 0 || m % BK != 0 || n == 0 || batch == 0) return false;
-  if (((uintptr_t)w & 3) != 0) return false;
+  if (m == 0 || m % 256 != 0 || n == 0 || batch == 0) return false;
+  if (((uintptr_t)w & 15) != 0) return false;
   if (n > (size_t)0x7FFFFFFF || m > (size_t)0x7FFFFFF || batch > (size_t)0x7FFFFFFF) return false;
   const size_t tiles = ((n + BN - 1) / BN) * ((batch + BM - 1) / BM);
   if (tiles > (size_t)0x7FFFFFFF) return false;
