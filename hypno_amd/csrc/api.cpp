@@ -38,7 +38,9 @@ int hip_fail(hipError_t e, const char* what) {
   return fail(st, "%s: %s", what, hipGetErrorString(e));
 }
 
-// Minimum token count routed to the MFMA GEMM.
+// Token counts 2 .. kSkinnyMaxBatch go to the weight-streaming MFMA kernel,
+// larger ones (from kGemmMinBatch) to the tiled prefill GEMM.
+constexpr size_t kSkinnyMaxBatch = 64;
 constexpr size_t kGemmMinBatch = 16;
 
 struct DevBuf {
@@ -133,6 +135,20 @@ int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
     cus = ds->cus;
   }
   hipError_t e;
+  if (batch >= 2 && batch <= kSkinnyMaxBatch && q4_0_skinny_ok(w, w_len, n, m, batch, cus) &&
+      aligned16(x)) {
+    void* ws = nullptr;
+    {
+      std::lock_guard<std::mutex> g(g_mu);
+      DevBuf& b = ds->workspaces[s];
+      e = ensure(b, skinny_workspace_bytes(batch, m), s);
+      if (e != hipSuccess) return hip_fail(e, "skinny workspace");
+      ws = b.p;
+    }
+    e = launch_q4_0_skinny(y, w, x, bias, n, m, batch, ws, cus, s);
+    if (e != hipSuccess) return hip_fail(e, "q4_0 skinny launch");
+    return HYPNO_HIP_OK;
+  }
   const bool v3 = batch >= kGemmMinBatch && q4_0_gemm_v3_ok(w, w_len, n, m, batch);
   if (v3 || (batch >= kGemmMinBatch && q4_0_gemm_ok(w, w_len, n, m, batch))) {
     void* ws = nullptr;

@@ -167,6 +167,14 @@ hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const
                                size_t n, size_t m, size_t batch, void* workspace, int num_cus,
                                hipStream_t s);
 
+// A few tokens (2 <= batch <= 64): weight-streaming MFMA kernel (skinny_q4.hip).
+bool q4_0_skinny_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t batch,
+                    int num_cus);
+size_t skinny_workspace_bytes(size_t batch, size_t m);
+hipError_t launch_q4_0_skinny(float* y, const uint8_t* w, const float* x, const float* bias,
+                              size_t n, size_t m, size_t batch, void* workspace, int num_cus,
+                              hipStream_t s);
+
 // FP16 weights.
 hipError_t launch_f16_generic(float* y, const uint8_t* w, const float* x, const float* bias,
                               size_t n, size_t m, size_t batch, hipStream_t s);

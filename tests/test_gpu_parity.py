@@ -191,6 +191,59 @@ def test_small_batch_matches_per_token(torch, hk, orc, batch):
         assert orc.normwise_err(got[t], ref[t]) <= GEMV_TOL
 
 
+# --- a few tokens (weight-streaming MFMA kernel) -------------------------------------
+
+@pytest.mark.parametrize("batch,n,m", [
+    (2, 37, 512), (7, 1000, 1024), (8, 4096, 4096), (9, 130, 2048), (15, 4097, 256),
+    (16, 64, 768), (17, 300, 4096), (32, 1024, 3072), (33, 2048, 1024), (64, 4096, 4096),
+])
+def test_skinny_q4_0(torch, hk, orc, batch, n, m):
+    """2..64 tokens: against the oracle's per-token GEMVs (turbo.rs:329-331).
+    Up to 15 tokens the bar is the GEMV's (fp32 activations, 1e-4 normwise
+    per token); from 16 the prefill GEMM's (fp16 activations, 2e-3 rel L2)."""
+    q = _q4(orc, n, m, seed=batch * 7 + n)
+    x = orc.normal_f32(batch + 100, (batch, m))
+    bias = orc.normal_f32(batch + 200, n)
+    y = torch.empty(batch * n, dtype=torch.float32, device="cuda")
+    from hypno_amd import _lib
+    import ctypes
+    lib = _lib.load()
+    qg, xg, bg = _gpu(torch, q), _gpu(torch, x), _gpu(torch, bias)
+    st = lib.hypno_hip_matmul_q4_0_dev(ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(qg.data_ptr()),
+                                       q.size, ctypes.c_void_p(xg.data_ptr()),
+                                       ctypes.c_void_p(bg.data_ptr()), n, m, batch, None)
+    assert st == 0
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().reshape(batch, n)
+    ref = orc.batch_matmul(q, 3, x, n, m, batch) + bias
+    if batch < 16:
+        for t in range(batch):
+            assert orc.normwise_err(got[t], ref[t]) <= GEMV_TOL, t
+    else:
+        assert orc.rel_l2(got, ref) <= GEMM_TOL
+
+
+def test_skinny_wide_range_activations(torch, hk, orc):
+    """Per-token power-of-two scaling: tokens of very different magnitude,
+    a 1e4 outlier channel, tiny values and an all-zero token stay within the
+    GEMV bar."""
+    batch, n, m = 6, 512, 2048
+    q = _q4(orc, n, m, seed=77)
+    x = orc.normal_f32(78, (batch, m))
+    x[0] *= np.float32(1e-6)
+    x[1] *= np.float32(3e3)
+    x[2, 17] = np.float32(1e4)
+    x[3] = 0.0
+    x[4, ::2] *= np.float32(1e-3)
+    got = _run_q4(torch, hk, _gpu(torch, q), _gpu(torch, x), None, n, m, batch)
+    ref = orc.batch_matmul(q, 3, x, n, m, batch)
+    for t in range(batch):
+        if t == 3:
+            assert np.all(got[t] == 0.0)
+        else:
+            assert orc.normwise_err(got[t], ref[t]) <= GEMV_TOL, t
+
+
 def test_gemv_linearity_and_determinism_full_size(torch, hk, orc):
     # Mistral gate/up at full size: size-independent properties
     n, m = 14336, 4096
