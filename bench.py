@@ -15,9 +15,12 @@ Also reported, in the same JSON line:
                 read from the committed profile summary);
   cpu_baseline  the CPU restatement of hypno's AVX2 kernel (oracle/) on this
                 host, on a bounded sample (layer 0's seven matrices);
-  secondary     prefill GEMM TFLOP/s at Llama-3.2-3B MLP shapes (M = 512,
-                config 3) and Mistral-7B decode GEMV GB/s with >= 512 MB of
-                rotating weight copies (config 4).
+  secondary     every other BASELINE config, GPU-timed (graph replay):
+                configs[0] the single 2048x2048 GEMV, configs[2] the prefill
+                GEMM at Llama-3.2-3B MLP shapes (M = 512), configs[3] the
+                Mistral-7B decode stream (224 GEMVs, one plan launch) and the
+                M-sweep {1, 8, 64, 512, 2048}, configs[4] the lm_head in Q4_0
+                and FP16 at M = 1 and 128.
 
 Inputs are synthetic: weights N(0, 0.02) from a seeded torch generator,
 quantised on the GPU by the bit-exact Q4_0 quantizer; activations N(0, 1).
@@ -187,67 +190,158 @@ def decode_stream(torch, lib, steps, warmup, value_only=False):
     return res
 
 
-def prefill_gemm(torch, lib, reps=10):
-    """Config 3: M = 512 tokens, Llama-3.2-3B MLP (gate/up 8192x3072, down 3072x8192)."""
-    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    shapes = [(8192, 3072), (8192, 3072), (3072, 8192)]
-    arena, offs = make_q4_arena(torch, lib, shapes, seed=7, stream=st)
-    M = 512
-    gen = torch.Generator(device="cuda").manual_seed(5)
-    out = {}
-    for name, (n, m), (off, nb) in zip(("gate", "up", "down"), shapes, offs):
-        x = torch.randn(M, m, generator=gen, device="cuda")
-        y = torch.empty(M, n, device="cuda")
-        args = (ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(arena.data_ptr() + off), nb,
-                ctypes.c_void_p(x.data_ptr()), n, m, M, st)
-        for _ in range(3):
-            lib.check(lib.q4(*args), "prefill GEMM")
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            lib.q4(*args)
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / reps
-        out[name] = round(2.0 * M * n * m / (ms * 1e-3) / 1e12, 2)
-    return {"workload": "Llama-3.2-3B MLP, M=512, Q4_0 (config 3); includes the fp16 "
-                        "activation pre-pass", "tflops": out,
-            "frac_fp16_peak": {k: round(v / FP16_PEAK_TFLOPS, 4) for k, v in out.items()}}
-
-
-def mistral_gemv(torch, lib, reps=20):
-    """Config 4 at M = 1: Mistral-7B projections, >= 512 MB of distinct copies rotated."""
-    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    res = {}
-    for name, n, m in (("q_o", 4096, 4096), ("k_v", 1024, 4096), ("gate_up", 14336, 4096),
-                       ("down", 4096, 14336)):
-        nb = q4_bytes(n, m)
-        copies = max(2, -(-512 * 2**20 // nb))
-        arena, offs = make_q4_arena(torch, lib, [(n, m)] * copies, seed=n + m, stream=st)
-        x = torch.randn(m, device="cuda")
-        y = torch.empty(n, device="cuda")
-        ptrs = [ctypes.c_void_p(arena.data_ptr() + off) for off, _ in offs]
-        xp, yp = ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr())
-        for p in ptrs[:4]:
-            lib.q4(yp, p, nb, xp, n, m, 1, st)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        total = 0
-        evs = []
+def time_calls_graph(torch, issue, reps, replays=3):
+    """GPU time per iteration of `issue(stream_ptr)` (library calls on one
+    stream): one warm-up call, then `reps` iterations captured in a HIP graph
+    and replayed `replays` times between HIP events, so host-side call
+    overhead does not enter the figure."""
+    gs = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(gs):
+        issue(ctypes.c_void_p(gs.cuda_stream), 0)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=gs):
+        sp = ctypes.c_void_p(gs.cuda_stream)
         for i in range(reps):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            lib.q4(yp, ptrs[i % copies], nb, xp, n, m, 1, st)
-            b.record()
-            evs.append((a, b))
-        torch.cuda.synchronize()
-        durs = sorted(a.elapsed_time(b) for a, b in evs)
-        med = durs[len(durs) // 2]
-        res[name] = round(nb / (med * 1e-3) / 1e9, 1)
-        del arena
-        torch.cuda.empty_cache()
-    return {"workload": "Mistral-7B decode GEMV M=1 (config 4), median event time per launch, "
-                        f">= 512 MB rotating copies", "weight_gbs": res,
-            "frac_hbm_peak": {k: round(v / HBM_PEAK_GBS, 4) for k, v in res.items()}}
+            issue(sp, i)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del g
+    return e0.elapsed_time(e1) / (replays * reps) * 1e3  # us
+
+
+def rotating_q4(torch, lib, n, m, seed, min_bytes=512 * 2**20):
+    """Distinct Q4_0 copies of one n x m matrix, >= min_bytes in total, so that
+    successive calls stream their weights from HBM, not from the 256 MB cache."""
+    nb = q4_bytes(n, m)
+    copies = max(2, -(-min_bytes // nb))
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    arena, offs = make_q4_arena(torch, lib, [(n, m)] * copies, seed=seed, stream=st)
+    return arena, [arena.data_ptr() + off for off, _ in offs], nb
+
+
+def q4_case(torch, lib, n, m, M, seed, reps):
+    """GPU us per hypno_hip_matmul_q4_0_dev call of an M x m . (n x m)^T
+    product (rotating weight copies when the weights are small)."""
+    arena, ptrs, nb = rotating_q4(torch, lib, n, m, seed,
+                                  min_bytes=512 * 2**20 if M <= 64 else 1)
+    x = torch.randn(M, m, device="cuda")
+    y = torch.empty(M, n, device="cuda")
+    xp, yp = ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr())
+
+    def issue(sp, i):
+        rc = lib.q4(yp, ctypes.c_void_p(ptrs[i % len(ptrs)]), nb, xp, n, m, M, sp)
+        if rc:
+            lib.check(rc, "matmul_q4_0")
+
+    us = time_calls_graph(torch, issue, reps)
+    del arena, x, y
+    torch.cuda.empty_cache()
+    return {"us": round(us, 2), "weight_gbs": round(nb / us / 1e3, 1),
+            "tflops": round(2.0 * M * n * m / us / 1e6, 2),
+            "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4),
+            "frac_fp16_peak": round(2.0 * M * n * m / us / 1e6 / FP16_PEAK_TFLOPS, 4)}
+
+
+def prefill_gemm(torch, lib):
+    """M = 512 tokens, Llama-3.2-3B MLP: gate/up 8192 x 3072 and
+    down 3072 x 8192, activations N(0,1) with 1% of channels x20.  Each call =
+    fp16 activation pre-pass + MFMA GEMM."""
+    out = {}
+    for name, n, m in (("gate_up", 8192, 3072), ("down", 3072, 8192)):
+        out[name] = q4_case(torch, lib, n, m, 512, seed=7 + n, reps=20)
+    return {"workload": "configs[2] Llama-3.2-3B MLP, M=512, Q4_0; GPU time per call incl. "
+                        "the fp16 activation pre-pass", "results": out}
+
+
+MISTRAL = [("q_o", 4096, 4096), ("k_v", 1024, 4096), ("gate_up", 14336, 4096),
+           ("down", 4096, 14336)]
+
+
+def mistral_stream(torch, lib, steps=10, warmup=3):
+    """configs[3] at M = 1 as a decode step streams it: the 224 Q4_0 GEMVs of
+    Mistral-7B (32 layers x q, k, v, o, gate, up, down; 3.93 GB) as one plan
+    launch, launched back to back."""
+    import hypno_amd as hk
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    per_layer = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096),
+                 (14336, 4096), (4096, 14336)]
+    shapes = per_layer * 32
+    arena, offs = make_q4_arena(torch, lib, shapes, seed=11, stream=st)
+    xs = {4096: torch.randn(4096, device="cuda"), 14336: torch.randn(14336, device="cuda")}
+    ys = [torch.empty(n, device="cuda") for n, _ in shapes]
+    plan = hk.GemvPlan([(ys[i], arena[o:o + nb], xs[m], None, n, m)
+                        for i, ((n, m), (o, nb)) in enumerate(zip(shapes, offs))])
+    wb = sum(nb for _, nb in offs)
+    ms = time_launches(torch, plan.run, steps, warmup)
+    plan.close()
+    del arena, ys
+    torch.cuda.empty_cache()
+    gbs = wb / (ms * 1e-3) / 1e9
+    return {"workload": "configs[3] M=1: Mistral-7B decode-step weight stream, 224 Q4_0 "
+                        "GEMVs as one plan launch", "weight_bytes": wb, "us": round(ms * 1e3, 1),
+            "weight_gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def mistral_m_sweep(torch, lib):
+    """Mistral-7B projections at M in {1, 8, 64, 512, 2048}."""
+    out = {}
+    for name, n, m in MISTRAL:
+        for M in (1, 8, 64, 512, 2048):
+            out[f"{name}_M{M}"] = q4_case(torch, lib, n, m, M, seed=n + m + M,
+                                          reps=20 if M <= 64 else 4)
+    return {"workload": "configs[3] Mistral-7B q/o, k/v, gate/up, down at M in "
+                        "{1,8,64,512,2048}; GPU time per call (graph replay); M <= 64 "
+                        "rotates >= 512 MB of weight copies", "results": out}
+
+
+def lm_head(torch, lib):
+    """K = 4096, N = 128256, M in {1, 128}, Q4_0 and FP16 weights."""
+    n, m = 128256, 4096
+    out = {}
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    arena, offs = make_q4_arena(torch, lib, [(n, m)], seed=17, stream=st)
+    gen = torch.Generator(device="cuda").manual_seed(18)
+    w16 = torch.randn(n * m, generator=gen, device="cuda").mul_(0.02).half()
+    for M in (1, 128):
+        x = torch.randn(M, m, device="cuda")
+        y = torch.empty(M, n, device="cuda")
+        xp, yp = ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr())
+        for dt, nb in (("q4_0", offs[0][1]), ("f16", w16.numel() * 2)):
+            def issue(sp, i, dt=dt, nb=nb):
+                if dt == "q4_0":
+                    rc = lib.lib.hypno_hip_matmul_q4_0_dev(
+                        yp, ctypes.c_void_p(arena.data_ptr()), nb, xp, None, n, m, M, sp)
+                else:
+                    rc = lib.lib.hypno_hip_matmul_f16_dev(
+                        yp, ctypes.c_void_p(w16.data_ptr()), nb, xp, None, n, m, M, sp)
+                if rc:
+                    lib.check(rc, "lm_head")
+            us = time_calls_graph(torch, issue, reps=5)
+            out[f"{dt}_M{M}"] = {"us": round(us, 1), "weight_gbs": round(nb / us / 1e3, 1),
+                                 "tflops": round(2.0 * M * n * m / us / 1e6, 2),
+                                 "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4),
+                                 "frac_fp16_peak": round(2.0 * M * n * m / us / 1e6 /
+                                                         FP16_PEAK_TFLOPS, 4)}
+        del x, y
+    del arena, w16
+    torch.cuda.empty_cache()
+    return {"workload": "configs[4] lm_head K=4096 N=128256 (N a multiple of 128 but not "
+                        "of 512/1024), M in {1,128}, Q4_0 and FP16 weights", "results": out}
+
+
+def single_gemv(torch, lib):
+    """one 2048 x 2048 Q4_0 GEMV (TinyLlama q_proj), M = 1."""
+    r = q4_case(torch, lib, 2048, 2048, 1, seed=2048, reps=50)
+    r["workload"] = ("configs[0] 2048x2048 Q4_0 GEMV, M=1; GPU time per call, >= 512 MB "
+                     "of rotating weight copies")
+    return r
 
 
 def copy_probe(torch, nbytes=1 << 30, reps=20):
@@ -393,9 +487,13 @@ def main():
         },
     }
     if not args.no_secondary:
-        print("[bench] secondary: prefill GEMM and Mistral GEMV", file=sys.stderr, flush=True)
-        line["secondary"] = {"prefill_gemm": prefill_gemm(torch, lib),
-                             "mistral_gemv": mistral_gemv(torch, lib)}
+        sec = {}
+        for key, fn in (("c0_single_gemv", single_gemv), ("c2_prefill_gemm", prefill_gemm),
+                        ("c3_mistral_stream", mistral_stream), ("c3_m_sweep", mistral_m_sweep),
+                        ("c4_lm_head", lm_head)):
+            print(f"[bench] secondary: {key}", file=sys.stderr, flush=True)
+            sec[key] = fn(torch, lib)
+        line["secondary"] = sec
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(d["sample"], d["x_host"], args.cpu_seconds)
