@@ -435,6 +435,9 @@ hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
           hipSuccess ||
       per_cu < 1)
     per_cu = 1;
+  // A single matrix gets at most two work-groups per CU, so that each one
+  // streams several steps for the one activation staging it pays for.
+  if (njobs == 1 && per_cu > 2) per_cu = 2;
   const int grid = total_steps < num_cus * per_cu ? total_steps : num_cus * per_cu;
   GemvLaunch L;
   L.jobs = d_jobs;
