@@ -155,7 +155,8 @@ int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
     {
       std::lock_guard<std::mutex> g(g_mu);
       DevBuf& b = ds->workspaces[s];
-      e = ensure(b, gemm_workspace_bytes(batch, m), s);
+      e = ensure(b, v3 ? gemm_v3_workspace_bytes(batch, n, m, cus) : gemm_workspace_bytes(batch, m),
+                 s);
       if (e != hipSuccess) return hip_fail(e, "GEMM workspace");
       ws = b.p;
     }

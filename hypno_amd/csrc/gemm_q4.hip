@@ -137,6 +137,8 @@ struct Args {
   int M, N, K;
   int tiles_m, tiles_n;
   int xcd_map;        // 1: blockIdx -> tile mapping groups tiles per XCD
+  int splits;         // K split over blockIdx.y; > 1: fp32 partials to `part`
+  float* part;        // [splits][M][N] partial sums (splits > 1)
 };
 
 __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a) {
@@ -159,7 +161,13 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   if (a.xcd_map) tile = (tile & 7) * (ntiles >> 3) + (tile >> 3);
   const int m0 = (tile % a.tiles_m) * BM;
   const int n0 = (tile / a.tiles_m) * BN;
-  const int steps = a.K / BK;
+  // This work-group's K range: stages [s0, s0 + steps) of gsteps (even
+  // bounds; the ring code runs on local stage numbers, addresses use s0 + s).
+  const int gsteps = a.K / BK;
+  const int z = blockIdx.y;
+  const int s0 = (int)((long long)gsteps * z / a.splits) & ~1;
+  const int s1 = z == a.splits - 1 ? gsteps : (int)((long long)gsteps * (z + 1) / a.splits) & ~1;
+  const int steps = s1 - s0;
   const size_t x_row = (size_t)a.K * 2;
   const size_t w_row = (size_t)(a.K / 32) * 18;
 
@@ -177,17 +185,17 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   // 16 bytes earlier: it then ends exactly at the row's end.
   const int wrow = min(n0 + 16 * wave + (lane >> 2), a.N - 1);
   const uint8_t* wsrc = a.w + (size_t)wrow * w_row + (lane & 3) * 16;
-  auto win_start = [&](int s) -> int {  // window start relative to the row
-    return ((s * 36) & ~15) - (s == steps - 1 ? 16 : 0);
+  auto win_start = [&](int g) -> int {  // window start of global stage g, from the row
+    return ((g * 36) & ~15) - (g == gsteps - 1 ? 16 : 0);
   };
   auto issue = [&](int s) {  // DMA of stage min(s, steps-1) into the ring slots of s
     const int sc = s < steps ? s : steps - 1;
     uint8_t* adst = smem + kOffA + (s % kARing) * kTileBytes + wave * 1024;
-    const uint8_t* asrc = xsrc + (size_t)sc * kRowBytes;
+    const uint8_t* asrc = xsrc + (size_t)(s0 + sc) * kRowBytes;
     dma16(asrc, adst);
     dma16(asrc + 64 * x_row, adst + 8 * 1024);
     uint8_t* rdst = smem + kOffRaw + (s % kRawRing) * kRawBytes + wave * 1024;
-    dma16(wsrc + win_start(sc), rdst);
+    dma16(wsrc + win_start(s0 + sc), rdst);
   };
 
   // --- expansion role: thread -> row er, block eb of the stage, half eh
@@ -210,7 +218,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   auto expand_read = [&](int s) -> RawW {
     // offset of the stage's first byte in the window: 0, 4, 8 or 12; 28 at
     // the last stage
-    const int o = s * 36 - win_start(s);
+    const int o = (s0 + s) * 36 - win_start(s0 + s);
     const uint8_t* p = smem + kOffRaw + (s % kRawRing) * kRawBytes + o + eoff;
     const uint32_t* d = reinterpret_cast<const uint32_t*>(p);
     return RawW{d[0], d[1], d[2]};
@@ -372,24 +380,61 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   }
   __syncthreads();
   if (kgrp == 0) {
+    // split K: this range's sum goes to its partial plane, the bias is added
+    // by the reduction
+    float* dst = a.splits > 1 ? a.part + (size_t)z * a.M * a.N : a.y;
+    const float* bias = a.splits > 1 ? nullptr : a.bias;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const int n = n0 + wn * 64 + 16 * j + lr;
       const bool nok = n < a.N;
-      const float bv = (a.bias && nok) ? a.bias[n] : 0.0f;
+      const float bv = (bias && nok) ? bias[n] : 0.0f;
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const float v = acc[i][j][r] + red[((wig * 64 + (i * 4 + j) * 4 + r) * 64) + lane];
           const int m = m0 + wm * 64 + 16 * i + 4 * lq + r;
-          if (nok && m < a.M) a.y[(size_t)m * a.N + n] = v + bv;
+          if (nok && m < a.M) dst[(size_t)m * a.N + n] = v + bv;
         }
     }
   }
 }
 
+// Y = sum of the K-split partial planes in split order (+ bias): a fixed
+// order, so results do not depend on which work-group finished first.
+__global__ void __launch_bounds__(256)
+split_k_reduce_kernel(float* __restrict__ y, const float* __restrict__ part,
+                      const float* __restrict__ bias, size_t mn, int n, int splits) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= mn) return;
+  float v = part[i];
+  for (int z = 1; z < splits; z++) v += part[(size_t)z * mn + i];
+  y[i] = v + (bias ? bias[i % n] : 0.0f);
+}
+
+// K splits: when the tile grid leaves CUs idle, each tile's K range is cut
+// into `splits` pieces (each at least kMinSplitStages stages) so the grid
+// nearly fills the chip.
+constexpr int kMinSplitStages = 8;
+int pick_splits(size_t tiles, size_t m, int num_cus) {
+  const size_t stages = m / BK;
+  if (tiles * 4 >= (size_t)num_cus * 3) return 1;
+  size_t s = (size_t)num_cus / tiles;
+  if (s > stages / kMinSplitStages) s = stages / kMinSplitStages;
+  return s < 2 ? 1 : (int)s;
+}
+
+size_t round256(size_t v) { return (v + 255) / 256 * 256; }
+
 }  // namespace
+
+size_t gemm_v3_workspace_bytes(size_t batch, size_t n, size_t m, int num_cus) {
+  const size_t tiles = ((n + BN - 1) / BN) * ((batch + BM - 1) / BM);
+  const int splits = pick_splits(tiles, m, num_cus);
+  const size_t xb = round256(gemm_workspace_bytes(batch, m));
+  return splits > 1 ? xb + (size_t)splits * batch * n * 4 : xb;
+}
 
 bool q4_0_gemm_v3_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t batch) {
   if (m == 0 || m % 256 != 0 || n == 0 || batch == 0) return false;
@@ -403,7 +448,6 @@ bool q4_0_gemm_v3_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t 
 hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const float* bias,
                                size_t n, size_t m, size_t batch, void* ws, int num_cus,
                                hipStream_t s) {
-  (void)num_cus;
   hipError_t e = launch_x_f16_permuted(x, batch, m, ws, s);
   if (e != hipSuccess) return e;
   static bool attr_set = false;
@@ -425,7 +469,16 @@ hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const
   a.tiles_n = (int)((n + BN - 1) / BN);
   const int tiles = a.tiles_m * a.tiles_n;
   a.xcd_map = (tiles % 8) == 0 ? 1 : 0;
-  hipLaunchKernelGGL(q4_0_gemm_v3_kernel, dim3(tiles), dim3(kThreads), kLdsBytes, s, a);
+  a.splits = pick_splits((size_t)tiles, m, num_cus);
+  a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) +
+                                    round256(gemm_workspace_bytes(batch, m)));
+  hipLaunchKernelGGL(q4_0_gemm_v3_kernel, dim3(tiles, a.splits), dim3(kThreads), kLdsBytes, s,
+                     a);
+  e = hipGetLastError();
+  if (e != hipSuccess || a.splits == 1) return e;
+  const size_t mn = batch * n;
+  hipLaunchKernelGGL(split_k_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, y,
+                     a.part, bias, mn, (int)n, a.splits);
   return hipGetLastError();
 }
 

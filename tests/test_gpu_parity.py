@@ -372,6 +372,33 @@ def test_gemm_bias_and_tails(torch, hk, orc, m):
     assert orc.rel_l2(y.cpu().numpy().reshape(batch, n), ref) <= GEMM_TOL
 
 
+@pytest.mark.parametrize("batch,n,m", [(128, 1024, 4096), (200, 300, 2048), (512, 1024, 4096)])
+def test_gemm_split_k_deterministic(torch, hk, orc, batch, n, m):
+    """Small tile grids split K over work-groups and add the partial planes in
+    a fixed order: within the GEMM bar, bias included, and bitwise equal from
+    run to run."""
+    q = _q4(orc, n, m, seed=n + m)
+    x = orc.normal_f32(batch + 9, (batch, m))
+    bias = orc.normal_f32(batch + 10, n)
+    from hypno_amd import _lib
+    import ctypes
+    lib = _lib.load()
+    qg, xg, bg = _gpu(torch, q), _gpu(torch, x), _gpu(torch, bias)
+    outs = []
+    for _ in range(2):
+        y = torch.empty(batch * n, dtype=torch.float32, device="cuda")
+        st = lib.hypno_hip_matmul_q4_0_dev(ctypes.c_void_p(y.data_ptr()),
+                                           ctypes.c_void_p(qg.data_ptr()), q.size,
+                                           ctypes.c_void_p(xg.data_ptr()),
+                                           ctypes.c_void_p(bg.data_ptr()), n, m, batch, None)
+        assert st == 0
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy().reshape(batch, n))
+    assert np.array_equal(outs[0], outs[1])
+    ref = _gemm_ref(orc, q, x, n, m) + bias.astype(np.float64)
+    assert orc.rel_l2(outs[0], ref) <= GEMM_TOL
+
+
 # --- FP16 weights (lm_head variant) --------------------------------------------------
 
 def _f16w(orc, n, m, seed):
