@@ -11,6 +11,7 @@ namespace hypno {
 // Native 4 x u32 vector: loads and stores of it are single instructions
 // (HIP's uint4 struct copies lower to memcpy and can keep values in scratch).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 
 // Load through the global address space (global_load_*, counted by vmcnt only;
 // a generic pointer would give flat_load_*, which also holds lgkmcnt).  The

@@ -53,37 +53,45 @@ constexpr int BK = 64;          // two Q4_0 blocks per stage
 constexpr int kThreads = 512;
 constexpr int kPrefetch = 4;    // stages of DMA in flight ahead of the compute
 constexpr int kARing = kPrefetch;       // stage s+1 read while s+2..s+4 land
-constexpr int kRawRing = kPrefetch - 1; // stage s+2 expanded while s+3, s+4 land
 constexpr int kBRing = 2;               // stage s+1 read while s+2 is written
 constexpr int kRowBytes = BK * 2;           // 128 B: one fp16 tile row
 constexpr int kTileBytes = BM * kRowBytes;  // 16 KB
-constexpr int kRawRow = 64;                 // raw W window per row and stage
-constexpr int kRawBytes = BN * kRawRow;     // 8 KB
 constexpr int kScaleBytes = 2 * BN * 4;     // 1 KB
 constexpr int kOffA = 0;
-constexpr int kOffRaw = kOffA + kARing * kTileBytes;
-constexpr int kOffB = kOffRaw + kRawRing * kRawBytes;
+constexpr int kOffB = kOffA + kARing * kTileBytes;
 constexpr int kOffS = kOffB + kBRing * kTileBytes;
-constexpr int kLdsBytes = kOffS + kBRing * kScaleBytes;  // 122 KB (< 160 KB)
+constexpr int kLdsBytes = kOffS + kBRing * kScaleBytes;  // 98 KB (< 160 KB)
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
-static_assert(4 * 64 * 64 * 4 <= kOffRaw, "K-group reduction fits in the A ring");
+static_assert(4 * 64 * 64 * 4 <= kARing * kTileBytes, "K-group reduction fits in the A ring");
 
-// End of stage s: every wave waits until its DMAs of all stages but the
-// newest (s + kPrefetch) have landed -- vmcnt counts this wave's outstanding
-// DMAs, three per stage -- and its LDS writes are done; then the work-group
-// meets at the barrier.  One asm statement with a memory clobber: the
-// compiler neither moves LDS accesses across it nor adds the vmcnt(0) that a
-// fence-based __syncthreads() would (which would drain the prefetch ring).
-static_assert(kPrefetch == 4, "stage_barrier's vmcnt(3) is one stage of DMAs");
+// End of stage s: every wave waits until all but its three newest global
+// reads (the two X DMAs of stage s+4 and the W read of stage s+4) have
+// landed -- vmcnt counts this wave's outstanding reads in issue order, three
+// per stage -- and its LDS writes are done; then the work-group meets at the
+// barrier.  One asm statement with a memory clobber: the compiler neither
+// moves LDS accesses across it nor adds the vmcnt(0) that a fence-based
+// __syncthreads() would (which would drain the prefetch ring).
+static_assert(kPrefetch == 4, "stage_barrier's vmcnt(3) is one stage of reads");
 __device__ __forceinline__ void stage_barrier() {
   asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
-// The same, split around LDS reads that need only this wave's own DMAs:
-// stage_wait() before them, then barrier_only().
-__device__ __forceinline__ void stage_wait() {
-  asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)" ::: "memory");
+// The same, for a stage whose wait also covers the W words `rw` read by
+// global_load_w() one stage earlier: rw passes through the statement, so
+// nothing reads those registers before it.
+__device__ __forceinline__ void stage_barrier(u32x3& rw) {
+  asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" : "+v"(rw) : : "memory");
 }
-__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
+// 12-byte global read into registers, issued from asm so that the compiler
+// adds no wait of its own for the result (its load-counter model treats the
+// LDS DMAs of the same loop as flat accesses and would wait for all reads,
+// draining the X prefetch).  The caller orders every use of the result
+// after a wait that covers it (stage_barrier(rw) or a vmcnt(0) barrier).
+__device__ __forceinline__ u32x3 global_load_w(const uint8_t* p) {
+  u32x3 v;
+  asm volatile("global_load_dwordx3 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
 
 // Byte offset of 16-byte chunk c (0..7) of tile row r.
 __device__ __forceinline__ uint32_t tile_off(int r, int c) {
@@ -177,51 +185,31 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   const int xr = 8 * wave + (lane >> 3);
   const int xc = (lane & 7) ^ ((xr >> 1) & 7);
   const uint8_t* xsrc = a.xh + (size_t)(m0 + xr) * x_row + xc * 16;
-  // --- W DMA: wave w fills rows 16w .. 16w+15 (1 KB): lane -> row
-  // 16w + (lane >> 2) (rows past N read row N-1), 16-byte piece lane & 3 of
-  // the row's 64-byte window at the 16-byte boundary at or below the stage's
-  // 36 bytes.  At the last stage that window would run 16 bytes past the
-  // row (and past the end of W for row N-1), so there every window starts
-  // 16 bytes earlier: it then ends exactly at the row's end.
-  const int wrow = min(n0 + 16 * wave + (lane >> 2), a.N - 1);
-  const uint8_t* wsrc = a.w + (size_t)wrow * w_row + (lane & 3) * 16;
-  auto win_start = [&](int g) -> int {  // window start of global stage g, from the row
-    return ((g * 36) & ~15) - (g == gsteps - 1 ? 16 : 0);
-  };
-  auto issue = [&](int s) {  // DMA of stage min(s, steps-1) into the ring slots of s
+  auto issue = [&](int s) {  // X DMA of stage min(s, steps-1) into the ring slot of s
     const int sc = s < steps ? s : steps - 1;
     uint8_t* adst = smem + kOffA + (s % kARing) * kTileBytes + wave * 1024;
     const uint8_t* asrc = xsrc + (size_t)(s0 + sc) * kRowBytes;
     dma16(asrc, adst);
     dma16(asrc + 64 * x_row, adst + 8 * 1024);
-    uint8_t* rdst = smem + kOffRaw + (s % kRawRing) * kRawBytes + wave * 1024;
-    dma16(wsrc + win_start(s0 + sc), rdst);
   };
 
-  // --- expansion role: thread -> row er, block eb of the stage, half eh
+  // --- expansion role: thread -> row er, block eb of the stage, half eh.
+  // Its 12 bytes of a stage are read straight into registers: for eb = 0 the
+  // block's scale and first 8 nibble bytes, or the last 8; for eb = 1 the
+  // same 2 bytes later (the block starts 18 bytes into the stage's 36), so
+  // the dword-aligned read starts at 16 + 8 eh and ends at most at the row's
+  // end.
   const int er = t >> 2, eb = (t >> 1) & 1, eh = t & 1;
   const bool evalid = n0 + er < a.N;
   const uint32_t esel = eb ? 0x07060504u : 0x05040302u;  // block at byte 0 / 2 mod 4
-  // byte of the row's window where this thread's 12 bytes start, minus the
-  // stage's window offset (a multiple of 4); 18 * eb + 8 * eh = 2 mod 4 for
-  // eb = 1, so the dword-aligned start is 18 * eb + 8 * eh - 2 * eb
-  const uint32_t eoff = er * kRawRow + 16 * eb + 8 * eh;
+  const uint8_t* erow = a.w + (size_t)min(n0 + er, a.N - 1) * w_row + 16 * eb + 8 * eh;
   const uint32_t boff0 = tile_off(er, 4 * eb + 2 * eh);
   const uint32_t boff1 = tile_off(er, 4 * eb + 2 * eh + 1);
   const uint32_t soff = (((eb * 2 + (er >> 6)) * 16 + (er & 15)) * 4 + ((er & 63) >> 4)) * 4;
-
-  // Expansion in two parts: the raw reads go out first in a stage, the
-  // unpack (VALU) is interleaved with that stage's MFMAs, the writes close it.
-  struct RawW {
-    uint32_t d0, d1, d2;
-  };
-  auto expand_read = [&](int s) -> RawW {
-    // offset of the stage's first byte in the window: 0, 4, 8 or 12; 28 at
-    // the last stage
-    const int o = (s0 + s) * 36 - win_start(s0 + s);
-    const uint8_t* p = smem + kOffRaw + (s % kRawRing) * kRawBytes + o + eoff;
-    const uint32_t* d = reinterpret_cast<const uint32_t*>(p);
-    return RawW{d[0], d[1], d[2]};
+  using RawW = u32x3;
+  auto raw_load = [&](int s) -> RawW {  // stage min(s, steps-1) of this range
+    const int g = s0 + (s < steps ? s : steps - 1);
+    return global_load_w(erow + (size_t)g * 36);
   };
   struct Expanded {
     u32x4 lo, hi;
@@ -229,9 +217,9 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   };
   auto expand_unpack = [&](const RawW& r) -> Expanded {
     Expanded e;
-    e.lo = unpack8(__builtin_amdgcn_perm(r.d1, r.d0, esel));
-    e.hi = unpack8(__builtin_amdgcn_perm(r.d2, r.d1, esel));
-    const uint32_t dbits = (r.d0 >> (eb ? 16 : 0)) & 0xFFFFu;
+    e.lo = unpack8(__builtin_amdgcn_perm(r.y, r.x, esel));
+    e.hi = unpack8(__builtin_amdgcn_perm(r.z, r.y, esel));
+    const uint32_t dbits = (r.x >> (eb ? 16 : 0)) & 0xFFFFu;
     e.scale = evalid ? f16_bits_to_f32(dbits) : 0.0f;
     return e;
   };
@@ -242,7 +230,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
     if (eh == 0)
       *reinterpret_cast<float*>(smem + kOffS + (s % kBRing) * kScaleBytes + soff) = e.scale;
   };
-  auto expand = [&](int s) { expand_write(s, expand_unpack(expand_read(s))); };
+  auto expand = [&](int s, const RawW& r) { expand_write(s, expand_unpack(r)); };
 
   // MFMA operands of this wave's block (kb = kgrp) of one stage: one
   // register set for A and one for B, each operand reloaded in place for the
@@ -281,13 +269,13 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   // A operand i is reloaded for stage `nx` right after MFMA 4i+3 and B
   // operand j right after MFMA 12+j, from one base address per tile that
   // also passes through the statements (which orders the loads); the
-  // unpacked weights of stage `xs` (raw words `rw`) go to LDS early.
+  // unpacked weights of stage `xs` (W words `rw`) go to LDS early.
   constexpr int kLag = 3;
   auto mma = [&](half8 (&fa)[4], half8 (&fb)[4], const floatx4& sc, int nx, const RawW& rw,
                  int xs) {
     floatx4 part[16];
-    uint32_t abase = a_addr(nx < 0 ? 0 : nx, 0);
-    uint32_t bbase = b_addr(nx < 0 ? 0 : nx, 0);
+    uint32_t abase = a_addr(nx, 0);
+    uint32_t bbase = b_addr(nx, 0);
 #pragma unroll
     for (int q = 0; q < 16 + kLag; q++) {
       const int u = q - kLag;
@@ -303,33 +291,34 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
                        : "v"(part[q]));
         else
           asm volatile("" : "+v"(fa[i1]), "+v"(abase), "+v"(bbase) : "v"(part[q]));
-        if (nx >= 0) {
-          if ((q & 3) == 3)
-            fa[q >> 2] = *reinterpret_cast<const half8*>(smem + abase + (q >> 2) * 16 * kRowBytes);
-          if (q >= 12)
-            fb[q & 3] = *reinterpret_cast<const half8*>(smem + bbase + (q & 3) * 16 * kRowBytes);
-        }
+        if ((q & 3) == 3)
+          fa[q >> 2] = *reinterpret_cast<const half8*>(smem + abase + (q >> 2) * 16 * kRowBytes);
+        if (q >= 12)
+          fb[q & 3] = *reinterpret_cast<const half8*>(smem + bbase + (q & 3) * 16 * kRowBytes);
       }
       if (u >= 0) {
 #pragma unroll
         for (int r = 0; r < 4; r++)
           acc[u >> 2][u & 3][r] = fmaf(sc[u & 3], part[u][r], acc[u >> 2][u & 3][r]);
       }
-      if (q == 2 && xs >= 0) expand_write(xs, expand_unpack(rw));
+      if (q == 2) expand_write(xs, expand_unpack(rw));
       if (q < 16) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
     }
   };
 
-  // Prologue: DMA of stages 0..2 (the raw ring holds three stages), B tiles
-  // of stages 0 and 1, operands of stage 0, then stage 3's DMA (its raw
-  // bytes reuse stage 0's slot, free once stage 0 is expanded).
+  // Prologue: X DMA of stages 0..3 and W reads of stages 0..3, all landed;
+  // B tiles of stages 0 and 1; operands of stage 0.
   issue(0);
   issue(1);
   issue(2);
-  __syncthreads();  // all of it landed (vmcnt(0))
-  expand(0);
-  expand(1);
+  issue(3);
+  RawW r0 = raw_load(0), r1 = raw_load(1);
+  RawW rwa = raw_load(2), rwb = raw_load(3);
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier"  // all of it landed
+               : "+v"(r0), "+v"(r1), "+v"(rwa), "+v"(rwb) : : "memory");
+  expand(0, r0);
+  expand(1, r1);
   stage_barrier();
   half8 fa[4], fb[4];
 #pragma unroll
@@ -338,34 +327,37 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
     fb[i] = *reinterpret_cast<const half8*>(smem + b_addr(0, i));
   }
   floatx4 sc0 = read_sc(0), sc1;
-  issue(3);
   stage_barrier();
 
-  // Stage s (operands of s and raw words of s+2 already in registers): DMA
-  // of stage s+4; LDS read of stage s+1's scales; MFMAs of stage s with the
-  // reloads of stage s+1's operands and the unpack/writes of stage s+2's B
-  // tile woven in; then wait for stage s+3's DMAs (stage s+2's X, s+3's W),
-  // read stage s+3's raw words and barrier.  Unrolled by two so the scale
-  // double buffer has static names (steps is even).
-  // A wave expands exactly the W rows its own DMAs fetched, so the raw reads
-  // for the next stage need only this wave's DMA wait, not the barrier:
-  // they are issued between the two and are in flight across the barrier.
-  RawW rw = expand_read(2);
+  // Stage s (operands of s and W words of s+2 already in registers): LDS
+  // read of stage s+1's scales; MFMAs of stage s with the reloads of stage
+  // s+1's operands and the unpack/writes of stage s+2's B tile woven in; X
+  // DMA of stage s+4 and W read of stage s+4 (into the register slot just
+  // used); then wait for everything but stage s+4's reads, and barrier.
+  // Unrolled by two so the register double buffers have static names (steps
+  // is even).
+  // Past the end (the last two stages) the reloads and expansions run
+  // anyway, on stale data into slots no later stage reads: the loop body
+  // has no branches, so the scheduler keeps the reads where they are issued.
+  // The stage's global reads are issued after its MFMAs (a scheduling
+  // barrier keeps them there).
   for (int s = 0; s < steps; s += 2) {
-    issue(s + kPrefetch);
     sc1 = read_sc(s + 1);
-    mma(fa, fb, sc0, s + 1, rw, s + 2 < steps ? s + 2 : -1);
-    stage_wait();
-    rw = expand_read(min(s + 3, steps - 1));
-    barrier_only();
+    mma(fa, fb, sc0, s + 1, rwa, s + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(s + kPrefetch);
+    rwa = raw_load(s + 4);
+    stage_barrier(rwb);  // covers rwb, read one stage earlier
+    sc0 = read_sc(s + 2);
+    mma(fa, fb, sc1, s + 2, rwb, s + 3);
+    __builtin_amdgcn_sched_barrier(0);
     issue(s + 1 + kPrefetch);
-    if (s + 2 < steps) sc0 = read_sc(s + 2);
-    mma(fa, fb, sc1, s + 2 < steps ? s + 2 : -1, rw, s + 3 < steps ? s + 3 : -1);
-    stage_wait();
-    rw = expand_read(min(s + 4, steps - 1));
-    barrier_only();
+    rwb = raw_load(s + 5);
+    stage_barrier(rwa);
   }
-  __syncthreads();  // trailing DMAs (re-loads of the last stage) have landed
+  // The trailing reads (re-loads of the last stage) land before their
+  // registers and LDS slots are reused.
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" : "+v"(rwa), "+v"(rwb) : : "memory");
 
   // K-group 1 -> LDS -> K-group 0 adds (fixed order) and stores.
   float* red = reinterpret_cast<float*>(smem + kOffA);
