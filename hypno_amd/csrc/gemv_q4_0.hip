@@ -435,10 +435,17 @@ hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
           hipSuccess ||
       per_cu < 1)
     per_cu = 1;
-  // A single matrix gets at most two work-groups per CU, so that each one
-  // streams several steps for the one activation staging it pays for.
-  if (njobs == 1 && per_cu > 2) per_cu = 2;
-  const int grid = total_steps < num_cus * per_cu ? total_steps : num_cus * per_cu;
+  int grid = total_steps < num_cus * per_cu ? total_steps : num_cus * per_cu;
+  // A single matrix: every work-group stages all of x (4K bytes) before its
+  // first step, so each one should stream at least about twice that in
+  // weights (14 rows x K/32 x 18 B >= 8K B): about n/14 work-groups, rounded
+  // to a whole number per CU (a partial round leaves most CUs idle while a
+  // few run a second work-group), at least one per CU.
+  if (njobs == 1) {
+    const int per = (job0.n / 14 + num_cus / 2) / num_cus;
+    const int cap = (per > 1 ? per : 1) * num_cus;
+    if (grid > cap) grid = cap;
+  }
   GemvLaunch L;
   L.jobs = d_jobs;
   L.job0 = job0;
