@@ -141,7 +141,7 @@ int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
     {
       std::lock_guard<std::mutex> g(g_mu);
       DevBuf& b = ds->workspaces[s];
-      e = ensure(b, skinny_workspace_bytes(batch, m), s);
+      e = ensure(b, skinny_workspace_bytes(batch, n, m, cus), s);
       if (e != hipSuccess) return hip_fail(e, "skinny workspace");
       ws = b.p;
     }

@@ -60,6 +60,40 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
   return (float)h;
 }
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// (a & b) | c in one v_and_or_b32 (the compiler emits two ops when b and c
+// are both literals).  VOP3 reads at most one SGPR here, so the mask b sits
+// in a VGPR and c in an SGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(c));
+  return r;
+}
+
+// Eight nibbles (byte i of q = e[2i] | e[2i+1] << 4) -> eight exact fp16
+// values e - 8 in slot order e0,e4,e1,e5,e2,e6,e3,e7.  0x6400 | n is the fp16
+// value 1024 + n and 0x6400 | n << 4 is 1024 + 16n; one packed fp16 add or
+// fma maps either to n - 8 exactly.
+__device__ __forceinline__ u32x4 unpack8(uint32_t q) {
+  const half2v lo_off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+  const half2v hi_mul = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const half2v hi_off = {(_Float16)-72.0f, (_Float16)-72.0f};
+  const uint32_t q8 = q >> 8;
+  const uint32_t p0 = and_or(q, 0x000F000Fu, 0x64006400u);   // e0, e4
+  const uint32_t p1 = and_or(q, 0x00F000F0u, 0x64006400u);   // e1, e5 (x16)
+  const uint32_t p2 = and_or(q8, 0x000F000Fu, 0x64006400u);  // e2, e6
+  const uint32_t p3 = and_or(q8, 0x00F000F0u, 0x64006400u);  // e3, e7 (x16)
+  u32x4 r;
+  r[0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, p0) + lo_off);
+  r[1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
+                                          __builtin_bit_cast(half2v, p1), hi_mul, hi_off));
+  r[2] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, p2) + lo_off);
+  r[3] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
+                                          __builtin_bit_cast(half2v, p3), hi_mul, hi_off));
+  return r;
+}
+
 // Wave-wide sum (wave64) with xor butterflies; every lane gets the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -174,7 +208,7 @@ hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const
 // A few tokens (2 <= batch <= 64): weight-streaming MFMA kernel (skinny_q4.hip).
 bool q4_0_skinny_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t batch,
                     int num_cus);
-size_t skinny_workspace_bytes(size_t batch, size_t m);
+size_t skinny_workspace_bytes(size_t batch, size_t n, size_t m, int num_cus);
 hipError_t launch_q4_0_skinny(float* y, const uint8_t* w, const float* x, const float* bias,
                               size_t n, size_t m, size_t batch, void* workspace, int num_cus,
                               hipStream_t s);

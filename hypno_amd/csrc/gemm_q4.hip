@@ -44,7 +44,6 @@ namespace hypno {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128;
@@ -96,38 +95,6 @@ __device__ __forceinline__ u32x3 global_load_w(const uint8_t* p) {
 // Byte offset of 16-byte chunk c (0..7) of tile row r.
 __device__ __forceinline__ uint32_t tile_off(int r, int c) {
   return (uint32_t)(r * kRowBytes + ((c ^ ((r >> 1) & 7)) << 4));
-}
-
-// (a & b) | c in one v_and_or_b32 (the compiler emits two ops when b and c
-// are both literals).  VOP3 reads at most one SGPR here, so the mask b sits
-// in a VGPR and c in an SGPR.
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t b, uint32_t c) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(c));
-  return r;
-}
-
-// Eight nibbles (byte i of q = e[2i] | e[2i+1] << 4) -> eight exact fp16
-// values e - 8 in slot order e0,e4,e1,e5,e2,e6,e3,e7.  0x6400 | n is the fp16
-// value 1024 + n and 0x6400 | n << 4 is 1024 + 16n; one packed fp16 add or
-// fma maps either to n - 8 exactly.
-__device__ __forceinline__ u32x4 unpack8(uint32_t q) {
-  const half2v lo_off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-  const half2v hi_mul = {(_Float16)0.0625f, (_Float16)0.0625f};
-  const half2v hi_off = {(_Float16)-72.0f, (_Float16)-72.0f};
-  const uint32_t q8 = q >> 8;
-  const uint32_t p0 = and_or(q, 0x000F000Fu, 0x64006400u);   // e0, e4
-  const uint32_t p1 = and_or(q, 0x00F000F0u, 0x64006400u);   // e1, e5 (x16)
-  const uint32_t p2 = and_or(q8, 0x000F000Fu, 0x64006400u);  // e2, e6
-  const uint32_t p3 = and_or(q8, 0x00F000F0u, 0x64006400u);  // e3, e7 (x16)
-  u32x4 r;
-  r[0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, p0) + lo_off);
-  r[1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
-                                          __builtin_bit_cast(half2v, p1), hi_mul, hi_off));
-  r[2] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, p2) + lo_off);
-  r[3] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
-                                          __builtin_bit_cast(half2v, p3), hi_mul, hi_off));
-  return r;
 }
 
 // One wave-wide 16-byte-per-lane DMA: lane i's 16 bytes at `src` land at

@@ -1,29 +1,34 @@
 // Q4_0 matmul for a few tokens (2 <= M <= 64): Y[M][N] = X[M][K] . W[N][K]^T.
 //
-// This regime is bound by the weight stream (3.6 M flop per weight byte at
-// most 228 flop/B, below the ~310 flop/B ridge), so the kernel streams every
-// Q4_0 block of W exactly once and does the arithmetic on the matrix cores:
+// This regime is bound by the weight stream (2 M flop per weight byte, at
+// most 228 flop/B, below the ~310 flop/B ridge), so the kernel reads every
+// Q4_0 block of W exactly once, in coalesced 16-byte pieces of contiguous
+// row segments, and does the arithmetic on the matrix cores:
 //
-//  * A work-group owns 16 rows of W (one MFMA column tile); its W waves split
-//    K into W equal ranges and their fp32 partial sums are added through LDS
-//    in wave order at the end (deterministic, no atomics).
-//  * Each lane loads the 4 nibble bytes it feeds to v_mfma_f32_16x16x32_f16
-//    (row lane & 15, nibble dword lane >> 4 of the block) plus the block's
-//    fp16 scale straight from global memory, two blocks at a time, a few
-//    block pairs ahead in registers.  The nibbles become exact fp16
-//    (nib - 8) in registers; the block's partial is scaled in fp32.
+//  * A work-group owns 64 rows of W (16 per wave, one MFMA column tile each)
+//    and a range of K; K streams through LDS in stages of 256 (8 blocks):
+//    DMA (global_load_lds) of the stage's activation rows and W row segments
+//    into a ring of LDS slots, one barrier per stage.
+//  * Lane (n, g) of a wave takes nibble quarter g of row n's block from LDS
+//    (4 bytes), turns it into exact fp16 (nib - 8) in registers and feeds
+//    v_mfma_f32_16x16x32_f16; the block's partial is scaled in fp32.
+//  * Small tile grids split K over blockIdx.y; the fp32 partials are added in
+//    split order by a second kernel (deterministic, no atomics).
 //  * Activations come from a pre-pass as MFMA A-operand rows (fp16, columns
 //    permuted per group of 8 to the unpack order):
-//      - M <= 16 ("split"): token t is scaled by a power of two s_t so that
-//        max|x_t| s_t lies in [2^14, 2^15), and stored as hi = fp16(x s_t)
-//        in row t and lo = fp16(x s_t - hi) in row Mh + t.  hi + lo equals
-//        x s_t to about 2^-22 relative, the products with the exact integer
-//        weights are exact in fp32, and y_t = (acc_hi + acc_lo) / s_t: an
-//        fp32-accurate result, as the GEMV path gives.
+//      - M <= 16 ("split"): each stage (256 K) of token t is scaled by a
+//        power of two s so that its max |x| s lies in [2^14, 2^15), and
+//        stored as hi = fp16(x s) in row t and lo = fp16(x s - hi) in row
+//        Mh + t.  hi + lo equals x s to about 2^-22 relative, the products
+//        with the exact integer weights are exact in fp32, and every stage
+//        adds (acc_hi + acc_lo) / s to y_t: an fp32-accurate result, as the
+//        GEMV path gives.  (Per-stage scales keep the pre-pass one pass over
+//        X with a work-group per stage.)
 //      - 16 < M <= 64: one fp16 row per token (the prefill GEMM's rounding).
 //
-// Requirements (q4_0_skinny_ok): K % (64 * waves) == 0, w 4-byte aligned,
-// w holds N whole rows.
+// Requirements (q4_0_skinny_ok): K % 256 == 0, w 16-byte aligned (row
+// segments of a stage are then 16-byte aligned), W and X under 4 GB, w
+// holds N whole rows.
 #include "common.hpp"
 
 namespace hypno {
@@ -31,255 +36,315 @@ namespace hypno {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
-
-// Eight nibbles (byte i of q = e[2i] | e[2i+1] << 4) -> eight exact fp16
-// values e - 8 in slot order e0,e4,e1,e5,e2,e6,e3,e7 (0x6400 | n = 1024 + n,
-// 0x6400 | n << 4 = 1024 + 16 n).
-__device__ __forceinline__ half8 unpack8h(uint32_t q) {
-  const half2v lo_off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-  const half2v hi_mul = {(_Float16)0.0625f, (_Float16)0.0625f};
-  const half2v hi_off = {(_Float16)-72.0f, (_Float16)-72.0f};
-  const uint32_t q8 = q >> 8;
-  u32x4 r;
-  r[0] = __builtin_bit_cast(uint32_t,
-                            __builtin_bit_cast(half2v, (q & 0x000F000Fu) | 0x64006400u) + lo_off);
-  r[1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
-      __builtin_bit_cast(half2v, (q & 0x00F000F0u) | 0x64006400u), hi_mul, hi_off));
-  r[2] = __builtin_bit_cast(uint32_t,
-                            __builtin_bit_cast(half2v, (q8 & 0x000F000Fu) | 0x64006400u) + lo_off);
-  r[3] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
-      __builtin_bit_cast(half2v, (q8 & 0x00F000F0u) | 0x64006400u), hi_mul, hi_off));
-  return __builtin_bit_cast(half8, r);
-}
 
 __device__ __forceinline__ uint32_t pack2h(float a, float b) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) |
          ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
 }
 
-// Pre-pass: X fp32 [M][K] -> A rows fp16 [rows][K] (+ 1/s_t per token).
-// One work-group per hi row r < Mh: token r's hi row (and lo row Mh + r when
-// split), or zero rows for r >= M.
+// Pre-pass: X fp32 [M][K] -> A rows fp16 [rows][K], in stages of 256 K
+// (the main kernel's stage), plus 1/s per token and stage when split.
+// 32 lanes per (row, stage): lane i converts K elements 8i .. 8i+7 of the
+// stage.  Grid: (stages / 8 rounded up, hi rows); rows r >= M are zero.
 __global__ void __launch_bounds__(256)
 x_skinny_kernel(uint8_t* __restrict__ xa, float* __restrict__ inv_s, const float* __restrict__ x,
                 int M, int K, int Mh, int split) {
-  __shared__ float red[4];
-  const int r = blockIdx.x;
+  const int r = blockIdx.y;
   const int t = threadIdx.x;
+  const int c = blockIdx.x * 8 + (t >> 5);  // stage
+  const int gi = t & 31;
+  const int stages = K / 256;
+  if (c >= stages) return;  // whole 32-lane groups
+  const size_t g = (size_t)c * 32 + gi;     // group of 8 along the row
   u32x4* hi_row = reinterpret_cast<u32x4*>(xa + (size_t)r * K * 2);
   u32x4* lo_row = reinterpret_cast<u32x4*>(xa + (size_t)(Mh + r) * K * 2);
-  const int groups = K / 8;
   if (r >= M) {
-    for (int g = t; g < groups; g += 256) {
-      hi_row[g] = u32x4{0u, 0u, 0u, 0u};
-      if (split) lo_row[g] = u32x4{0u, 0u, 0u, 0u};
+    hi_row[g] = u32x4{0u, 0u, 0u, 0u};
+    if (split) {
+      lo_row[g] = u32x4{0u, 0u, 0u, 0u};
+      if (gi == 0) inv_s[(size_t)c * Mh + r] = 1.0f;
     }
     return;
   }
-  const float* xr = x + (size_t)r * K;
-  float s = 1.0f;
+  const float* xr = x + (size_t)r * K + 8 * g;
+  const float4 a0 = load_global<float4>(xr);
+  const float4 a1 = load_global<float4>(xr + 4);
+  float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
   if (split) {
-    uint32_t mb = 0;  // largest |x| by bit pattern (NaN/inf compare above finite)
-    for (int i = t; i < K; i += 256) mb = max(mb, __float_as_uint(xr[i]) & 0x7FFFFFFFu);
+    uint32_t mb = 0;  // largest |x| of the stage by bit pattern (NaN/inf above finite)
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, o, 64));
-    if ((t & 63) == 0) red[t >> 6] = __uint_as_float(mb);
-    __syncthreads();
-    const float amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int k = 0; k < 8; k++) mb = max(mb, __float_as_uint(v[k]) & 0x7FFFFFFFu);
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, o, 64));
+    const float amax = __uint_as_float(mb);
     // s = 2^(15 - e) with amax < 2^e, so amax * s < 2^15; zero, inf and NaN
-    // rows keep s = 1 (their products propagate as the reference's would)
+    // stages keep s = 1 (their products propagate as the reference's would)
+    float s = 1.0f;
     if (amax > 0.0f && amax < __builtin_inff())
       s = ldexpf(1.0f, min(15 - __builtin_amdgcn_frexp_expf(amax), 126));
-    if (t == 0) inv_s[r] = 1.0f / s;
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] *= s;
+    if (gi == 0) inv_s[(size_t)c * Mh + r] = 1.0f / s;
   }
   constexpr int perm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
-  for (int g = t; g < groups; g += 256) {
-    const float4 a0 = load_global<float4>(xr + 8 * g);
-    const float4 a1 = load_global<float4>(xr + 8 * g + 4);
-    const float v[8] = {a0.x * s, a0.y * s, a0.z * s, a0.w * s,
-                        a1.x * s, a1.y * s, a1.z * s, a1.w * s};
-    u32x4 h, l;
+  u32x4 h, l;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const float p = v[perm[2 * j]], q = v[perm[2 * j + 1]];
-      h[j] = pack2h(p, q);
-      if (split) {
-        const float ph = (float)(_Float16)p, qh = (float)(_Float16)q;
-        l[j] = pack2h(p - ph, q - qh);
-      }
-    }
-    hi_row[g] = h;
-    if (split) lo_row[g] = l;
+  for (int j = 0; j < 4; j++) {
+    const float p = v[perm[2 * j]], q = v[perm[2 * j + 1]];
+    h[j] = pack2h(p, q);
+    const float ph = (float)(_Float16)p, qh = (float)(_Float16)q;
+    l[j] = pack2h(p - ph, q - qh);
   }
+  hi_row[g] = h;
+  if (split) lo_row[g] = l;
+}
+
+// Stage geometry.  A stage is 256 K (8 Q4_0 blocks) of every row and token:
+// a row's 144 bytes of a stage start 16-byte aligned (rows are K/32*18 =
+// multiples of 144 bytes when K % 256 == 0), so they move as nine 16-byte
+// pieces.
+constexpr int kSkWaves = 4;                    // waves per work-group, 16 W rows each
+constexpr int kSkRowBytes = 144;               // W bytes of one row and stage
+constexpr int kSkRowPieces = kSkRowBytes / 16;  // 9
+constexpr int kSkWDma = (16 * kSkRowPieces + 63) / 64;  // 3 DMAs per wave and stage
+constexpr int kSkWBytes = 1024 * kSkWDma;      // LDS per wave and stage (W)
+constexpr int kSkXRowBytes = 512;              // fp16 A-row bytes of one stage
+constexpr int kSkStageK = 256;
+
+template <int MF>
+struct SkGeom {
+  static constexpr int kRows = 16 * MF;                      // A rows
+  static constexpr int kXBytes = kRows * kSkXRowBytes;       // X chunk per stage
+  static constexpr int kXDma = kXBytes / 1024 / kSkWaves;    // X DMAs per wave and stage
+  static constexpr int kSlot = kXBytes + kSkWaves * kSkWBytes;
+  static constexpr int kRing = MF == 4 ? 3 : 4;              // stages in LDS
+  static constexpr int kLds = kRing * kSlot;                 // 80 / 112 / 132 KB
+  static constexpr int kReads = kXDma + kSkWDma;             // DMAs per wave and stage
+  static_assert(kLds <= 160 * 1024, "LDS budget");
+  static_assert((kRing - 2) * kReads <= 63, "vmcnt range");
+};
+
+// Wait until at most N of this wave's global reads are outstanding and its
+// LDS accesses are done, then meet the work-group.  (One asm statement with a
+// memory clobber: the compiler adds no wait of its own, and no LDS access
+// moves across it.)
+template <int N>
+__device__ __forceinline__ void wait_reads_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
+}
+
+// One wave-wide DMA of 16 bytes per lane: lane i's 16 bytes at `src` land at
+// lds_wave_base + 16 i.
+__device__ __forceinline__ void dma16(const void* src, uint8_t* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_wave_base,
+                                   16, 0, 0);
 }
 
 struct SkinnyArgs {
   float* y;
+  float* part;        // [splits][M][N] partial sums when splits > 1
   const uint8_t* w;
   const uint8_t* xa;
   const float* inv_s;
   const float* bias;
   int M, N, K;
-  int Mh;     // row offset of the lo rows (split), else 0
-  int split;
+  int split;          // hi/lo rows
+  int splits;         // K ranges over blockIdx.y
 };
 
-// One block pair (2p, 2p+1) of one 16-row tile, as loaded by this lane.
-template <int MF>
-struct Pair {
-  uint32_t e0, e1, es;  // even block: 8 bytes around the nibble dword, scale dword
-  uint32_t on, os;      // odd block: nibble dword, scale dword
-  u32x4 xe[MF], xo[MF]; // A operands of the two blocks
-};
-
-template <int MF, int W>
-__global__ void __launch_bounds__(64 * W) q4_0_skinny_kernel(const SkinnyArgs a) {
+// A work-group owns 64 rows of W (wave w: rows 16w..16w+15, one MFMA column
+// tile) and a range of whole stages of K; stages stream through a ring of
+// LDS slots:
+//  * X: the stage's 16 MF A rows (512 bytes each), DMA'd by all waves, 16-byte
+//    pieces XOR-swizzled by row (piece c of row r at c ^ (r & 15)) so the
+//    A-operand reads of 16 rows hit 16 different bank groups;
+//  * W: each wave DMAs its own 16 rows x 144 bytes, row after row (row
+//    stride 144 bytes = 36 dwords: 16 rows land in 16 different bank groups),
+//    as 16-byte pieces of contiguous row segments (coalesced reads).
+// One barrier per stage, after the wait for that stage's DMAs.  The MFMA B
+// operand of lane (n, g) for a block is its quarter g (4 nibble bytes) of
+// row n; it becomes exact fp16 (nib - 8) in registers, and the block's
+// partial is scaled in fp32.
+template <int MF, bool SPLIT>
+__global__ void __launch_bounds__(64 * kSkWaves) q4_0_skinny_kernel(const SkinnyArgs a) {
+  using G = SkGeom<MF>;
   extern __shared__ __align__(16) uint8_t smem[];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int lr = lane & 15, lq = lane >> 4;
-  const int K = a.K;
-  const int nblk = K / 32 / W;  // blocks per wave (even)
-  const int n = blockIdx.x * 16 + lr;
-  const bool nvalid = n < a.N;
-  const size_t w_row = (size_t)(K / 32) * 18;
-  const uint8_t* wr = a.w + (size_t)(nvalid ? n : a.N - 1) * w_row + (size_t)wave * nblk * 18;
-  const size_t x_row = (size_t)K * 2;
-  const uint8_t* xr = a.xa + (size_t)lr * x_row + ((size_t)wave * nblk * 32 + 8 * lq) * 2;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n16 = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16 * kSkWaves + 16 * wave;  // this wave's first W row
+  const int gsteps = a.K / kSkStageK;
+  const int z = blockIdx.y;
+  const int s0 = (int)((long long)gsteps * z / a.splits);
+  const int steps = (int)((long long)gsteps * (z + 1) / a.splits) - s0;
+  const size_t w_row = (size_t)(a.K / 32) * 18;
+  const size_t x_row = (size_t)a.K * 2;
 
-  auto load = [&](int p) -> Pair<MF> {
-    Pair<MF> r;
-    const uint8_t* b = wr + (size_t)p * 36;  // even block start (4-byte aligned)
-    r.e0 = load_global<uint32_t>(b + 4 * lq);
-    r.e1 = load_global<uint32_t>(b + 4 * lq + 4);
-    r.es = load_global<uint32_t>(b);
-    r.on = load_global<uint32_t>(b + 20 + 4 * lq);
-    r.os = load_global<uint32_t>(b + 16);
-    const uint8_t* xp = xr + (size_t)p * 128;
+  // W DMA i, lane -> piece p = 64 i + lane of the wave's 16 x 9 pieces: row
+  // p / 9, piece p % 9 (lanes past 144 are idle).  Rows past N re-read row
+  // N - 1 (their outputs are not stored).
+  uint32_t woff[kSkWDma];
 #pragma unroll
-    for (int m = 0; m < MF; m++) {
-      r.xe[m] = load_global<u32x4>(xp + (size_t)m * 16 * x_row);
-      r.xo[m] = load_global<u32x4>(xp + (size_t)m * 16 * x_row + 64);
-    }
-    return r;
+  for (int i = 0; i < kSkWDma; i++) {
+    const int p = 64 * i + lane;
+    const int rr = p < 16 * kSkRowPieces ? p / kSkRowPieces : 0;
+    const int row = min(n0 + rr, a.N - 1);
+    woff[i] = (uint32_t)((size_t)row * w_row + 16 * (p % kSkRowPieces));
+  }
+  // The last W DMA has 16 W lanes; with SPLIT, the next Mh / 4 lanes bring the
+  // stage's 1/s of the hi rows (Mh floats) to byte 2304 of the wave's W area.
+  constexpr int kWLast = 16 * kSkRowPieces - 64 * (kSkWDma - 1);
+  constexpr int kMh = MF == 1 ? 8 : 16;
+  constexpr int kInvOff = 16 * kSkRowPieces * 16;  // 2304
+  const int w_active = kWLast + (SPLIT ? kMh / 4 : 0);
+  const bool inv_lane = SPLIT && lane >= kWLast;
+  // X DMA i of this wave covers pieces p = 64 (wave * kXDma + i) + lane of the
+  // chunk: row p / 32, slot p % 32 holding logical piece (p % 32) ^ (row & 15).
+  uint32_t xoff[G::kXDma];
+#pragma unroll
+  for (int i = 0; i < G::kXDma; i++) {
+    const int p = 64 * (wave * G::kXDma + i) + lane;
+    const int r = p >> 5;
+    xoff[i] = (uint32_t)((size_t)r * x_row + 16 * ((p & 31) ^ (r & 15)));
+  }
+  // Stage s (clamped to the last one: the trailing requests re-read it into
+  // slots no later stage reads) into ring slot s % kRing.
+  auto issue = [&](int s) {
+    const int gs = s0 + (s < steps ? s : steps - 1);
+    uint8_t* slot = smem + (s % G::kRing) * G::kSlot;
+    const uint8_t* xsrc = a.xa + (size_t)gs * kSkXRowBytes;
+#pragma unroll
+    for (int i = 0; i < G::kXDma; i++) dma16(xsrc + xoff[i], slot + (wave * G::kXDma + i) * 1024);
+    const uint8_t* wsrc = a.w + (size_t)gs * kSkRowBytes;
+    uint8_t* wdst = slot + G::kXBytes + wave * kSkWBytes;
+#pragma unroll
+    for (int i = 0; i < kSkWDma - 1; i++) dma16(wsrc + woff[i], wdst + i * 1024);
+    const uint8_t* last = wsrc + woff[kSkWDma - 1];
+    if (inv_lane)
+      last = reinterpret_cast<const uint8_t*>(a.inv_s + (size_t)gs * kMh + 4 * (lane - kWLast));
+    if (lane < w_active) dma16(last, wdst + (kSkWDma - 1) * 1024);
   };
 
   floatx4 acc[MF];
 #pragma unroll
-  for (int m = 0; m < MF; m++) acc[m] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-  // `live` is false for the padding pairs past the end (their scales are
-  // zeroed, so they add nothing).
-  auto compute = [&](const Pair<MF>& r, bool live) {
-    const half8 be = unpack8h(__builtin_amdgcn_perm(r.e1, r.e0, 0x05040302u));
-    const half8 bo = unpack8h(r.on);
-    const bool v = nvalid && live;
-    const float se = v ? f16_bits_to_f32(r.es & 0xFFFFu) : 0.0f;
-    const float so = v ? f16_bits_to_f32(r.os >> 16) : 0.0f;
+  for (int f = 0; f < MF; f++) acc[f] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  // All LDS operands of a stage are read first (one wait), then the four
+  // block pairs are unpacked and multiplied.
+  auto compute = [&](int slot_i) {
+    floatx4 st_[MF];
 #pragma unroll
-    for (int m = 0; m < MF; m++) {
-      const floatx4 pe = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-          __builtin_bit_cast(half8, r.xe[m]), be, floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-      const floatx4 po = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-          __builtin_bit_cast(half8, r.xo[m]), bo, floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    for (int f = 0; f < MF; f++) st_[f] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    floatx4(&st)[MF] = SPLIT ? st_ : acc;  // stage sums (SPLIT) or the totals
+    const uint8_t* xs = smem + slot_i * G::kSlot;
+    const uint32_t* wr = reinterpret_cast<const uint32_t*>(xs + G::kXBytes + wave * kSkWBytes +
+                                                           n16 * kSkRowBytes);
+    // blocks 2 jp (byte 36 jp of the row) and 2 jp + 1 (byte 36 jp + 18)
+    uint32_t qe0[4], qe1[4], qo[4], se_bits[4], so_bits[4];
 #pragma unroll
-      for (int i = 0; i < 4; i++) acc[m][i] = fmaf(so, po[i], fmaf(se, pe[i], acc[m][i]));
+    for (int jp = 0; jp < 4; jp++) {
+      const uint32_t* q = wr + 9 * jp;
+      qe0[jp] = q[g];
+      qe1[jp] = q[g + 1];
+      qo[jp] = q[5 + g];
+      se_bits[jp] = q[0];
+      so_bits[jp] = q[4];
+    }
+    half8 xe[MF][4], xo[MF][4];
+#pragma unroll
+    for (int f = 0; f < MF; f++) {
+      const uint8_t* xr = xs + (16 * f + n16) * kSkXRowBytes;  // A row of this lane
+#pragma unroll
+      for (int jp = 0; jp < 4; jp++) {
+        xe[f][jp] = *reinterpret_cast<const half8*>(xr + (((8 * jp + g) ^ n16) << 4));
+        xo[f][jp] = *reinterpret_cast<const half8*>(xr + (((8 * jp + 4 + g) ^ n16) << 4));
+      }
+    }
+#pragma unroll
+    for (int jp = 0; jp < 4; jp++) {
+      const half8 be = __builtin_bit_cast(
+          half8, unpack8(__builtin_amdgcn_perm(qe1[jp], qe0[jp], 0x05040302u)));
+      const half8 bo = __builtin_bit_cast(half8, unpack8(qo[jp]));
+      const float se = f16_bits_to_f32(se_bits[jp] & 0xFFFFu);
+      const float so = f16_bits_to_f32(so_bits[jp] >> 16);
+#pragma unroll
+      for (int f = 0; f < MF; f++) {
+        const floatx4 pe = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            xe[f][jp], be, floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        const floatx4 po = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            xo[f][jp], bo, floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) st[f][i] = fmaf(so, po[i], fmaf(se, pe[i], st[f][i]));
+      }
+    }
+    // SPLIT: this lane's tokens (4 g + i, hi and lo alike; g mod 2 when the hi
+    // and lo rows share one frag) were scaled by s of this stage.
+    if (SPLIT) {
+      const floatx4 inv = *reinterpret_cast<const floatx4*>(
+          xs + G::kXBytes + wave * kSkWBytes + kInvOff + 16 * (MF == 1 ? (g & 1) : g));
+#pragma unroll
+      for (int f = 0; f < MF; f++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[f][i] = fmaf(st[f][i], inv[i], acc[f][i]);
     }
   };
 
-  // Ring of four pairs with static slot names and no early exit (an exit
-  // lets the compiler sink each load down to its use, which serialises the
-  // stream): while pair p is computed, pairs p+1..p+3 are in flight and pair
-  // p+4 is requested into the slot just freed.  The pair count is padded to
-  // a multiple of four; requests past the end re-read pair 0 (in bounds).
-  const int np = nblk / 2;
-  auto nxt = [&](int p) { return p < np ? p : 0; };
-  Pair<MF> ra = load(0);
-  __builtin_amdgcn_sched_barrier(0);
-  Pair<MF> rb = load(nxt(1));
-  __builtin_amdgcn_sched_barrier(0);
-  Pair<MF> rc = load(nxt(2));
-  __builtin_amdgcn_sched_barrier(0);
-  Pair<MF> rd = load(nxt(3));
-  __builtin_amdgcn_sched_barrier(0);
-  // Scheduling barriers keep each request after the compute before it (the
-  // scheduler would otherwise hoist requests, and the in-order load counter
-  // would then make each compute wait for younger requests too).
-  for (int p = 0; p < np; p += 4) {
-    compute(ra, true);
-    __builtin_amdgcn_sched_barrier(0);
-    ra = load(nxt(p + 4));
-    __builtin_amdgcn_sched_barrier(0);
-    compute(rb, p + 1 < np);
-    __builtin_amdgcn_sched_barrier(0);
-    rb = load(nxt(p + 5));
-    __builtin_amdgcn_sched_barrier(0);
-    compute(rc, p + 2 < np);
-    __builtin_amdgcn_sched_barrier(0);
-    rc = load(nxt(p + 6));
-    __builtin_amdgcn_sched_barrier(0);
-    compute(rd, p + 3 < np);
-    __builtin_amdgcn_sched_barrier(0);
-    rd = load(nxt(p + 7));
-    __builtin_amdgcn_sched_barrier(0);
+  for (int s = 0; s < G::kRing - 1; s++) issue(s);
+  for (int s = 0; s < steps; s++) {
+    wait_reads_barrier<(G::kRing - 2) * G::kReads>();  // stage s landed, slot of s-1 free
+    issue(s + G::kRing - 1);
+    compute(s % G::kRing);
   }
+  asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // trailing DMAs landed
 
-  // Wave partials -> LDS; wave 0 adds them in wave order and stores.
-  float* red = reinterpret_cast<float*>(smem);
-  if (wave > 0) {
-#pragma unroll
-    for (int m = 0; m < MF; m++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) red[(((wave - 1) * MF + m) * 4 + i) * 64 + lane] = acc[m][i];
-  }
-  __syncthreads();
-  if (wave != 0) return;
-  for (int v = 1; v < W; v++)
-#pragma unroll
-    for (int m = 0; m < MF; m++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) acc[m][i] += red[(((v - 1) * MF + m) * 4 + i) * 64 + lane];
-  // lane holds A rows 16m + 4*lq + i of column n
-  const float bv = (a.bias && nvalid) ? a.bias[n] : 0.0f;
-  if (a.split) {
-    if (MF == 1) {  // hi rows 0..7 in lanes lq 0-1, lo rows 8..15 in lanes lq 2-3
+  // lane holds A rows 16 f + 4 g + i of W row n
+  const int n = n0 + n16;
+  const bool nvalid = n < a.N;
+  float* out = a.splits > 1 ? a.part + (size_t)z * a.M * a.N : a.y;
+  const float bv = (a.splits == 1 && a.bias && nvalid) ? a.bias[n] : 0.0f;
+  if (SPLIT) {
+    if (MF == 1) {  // hi rows 0..7 in lanes g 0-1, lo rows 8..15 in lanes g 2-3
 #pragma unroll
       for (int i = 0; i < 4; i++) acc[0][i] += __shfl_down(acc[0][i], 32, 64);
-      if (lq < 2 && nvalid) {
+      if (g < 2 && nvalid) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const int tkn = 4 * lq + i;
-          if (tkn < a.M) a.y[(size_t)tkn * a.N + n] = acc[0][i] * a.inv_s[tkn] + bv;
+          const int tkn = 4 * g + i;
+          if (tkn < a.M) out[(size_t)tkn * a.N + n] = acc[0][i] + bv;
         }
       }
     } else {  // hi frags 0 .. MF/2-1, lo frags MF/2 .. MF-1
 #pragma unroll
-      for (int m = 0; m < MF / 2; m++)
+      for (int f = 0; f < MF / 2; f++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const int tkn = 16 * m + 4 * lq + i;
+          const int tkn = 16 * f + 4 * g + i;
           if (nvalid && tkn < a.M)
-            a.y[(size_t)tkn * a.N + n] = (acc[m][i] + acc[m + MF / 2][i]) * a.inv_s[tkn] + bv;
+            out[(size_t)tkn * a.N + n] = (acc[f][i] + acc[f + MF / 2][i]) + bv;
         }
     }
   } else {
 #pragma unroll
-    for (int m = 0; m < MF; m++)
+    for (int f = 0; f < MF; f++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const int tkn = 16 * m + 4 * lq + i;
-        if (nvalid && tkn < a.M) a.y[(size_t)tkn * a.N + n] = acc[m][i] + bv;
+        const int tkn = 16 * f + 4 * g + i;
+        if (nvalid && tkn < a.M) out[(size_t)tkn * a.N + n] = acc[f][i] + bv;
       }
   }
 }
 
-// Waves per work-group (K split): enough waves overall to cover the chip.
-int skinny_waves(size_t n, size_t m, int num_cus) {
-  const size_t tiles = (n + 15) / 16;
-  int w = 2;
-  while (w < 8 && tiles * (size_t)w < (size_t)num_cus * 8 && m % (64 * (size_t)w * 2) == 0) w *= 2;
-  return m % (64 * (size_t)w) == 0 ? w : 0;
+// y = sum of the split partials in split order (+ bias): deterministic.
+__global__ void __launch_bounds__(256)
+skinny_reduce_kernel(float* __restrict__ y, const float* __restrict__ part,
+                     const float* __restrict__ bias, int M, int N, int splits) {
+  const size_t mn = (size_t)M * N;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= mn) return;
+  float v = 0.0f;
+  for (int z = 0; z < splits; z++) v += part[(size_t)z * mn + i];
+  if (bias) v += bias[i % N];
+  y[i] = v;
 }
 
 struct SkinnyShape {
@@ -304,36 +369,55 @@ SkinnyShape skinny_shape(size_t batch) {
   return s;
 }
 
-template <int MF>
-hipError_t launch_mf(int w, const SkinnyArgs& a, int grid, hipStream_t s) {
-  const size_t lds = (size_t)(w - 1) * MF * 4 * 64 * 4;
-  switch (w) {
-    case 2:
-      hipLaunchKernelGGL((q4_0_skinny_kernel<MF, 2>), dim3(grid), dim3(128), lds, s, a);
-      break;
-    case 4:
-      hipLaunchKernelGGL((q4_0_skinny_kernel<MF, 4>), dim3(grid), dim3(256), lds, s, a);
-      break;
-    default:
-      hipLaunchKernelGGL((q4_0_skinny_kernel<MF, 8>), dim3(grid), dim3(512), lds, s, a);
-      break;
+// K ranges per row tile: about `target` resident work-groups in all (two per
+// CU when a work-group's LDS allows it), at most one range per stage.
+int skinny_splits(size_t n, size_t m, size_t batch, int num_cus) {
+  const SkinnyShape sh = skinny_shape(batch);
+  const size_t tiles = (n + 63) / 64;
+  const size_t per_cu = sh.mf == 1 ? 2 : 1;
+  const size_t target = (size_t)num_cus * per_cu;
+  size_t sp = (target + tiles / 2) / tiles;
+  const size_t gsteps = m / kSkStageK;
+  if (sp < 1) sp = 1;
+  if (sp > gsteps) sp = gsteps;
+  return (int)sp;
+}
+
+template <int MF, bool SPLIT>
+hipError_t launch_mf(const SkinnyArgs& a, dim3 grid, hipStream_t s) {
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(q4_0_skinny_kernel<MF, SPLIT>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       SkGeom<MF>::kLds);
+    if (e != hipSuccess) return e;
+    attr = true;
   }
+  hipLaunchKernelGGL((q4_0_skinny_kernel<MF, SPLIT>), grid, dim3(64 * kSkWaves), SkGeom<MF>::kLds,
+                     s, a);
   return hipGetLastError();
 }
 
 }  // namespace
 
 bool q4_0_skinny_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t batch, int num_cus) {
+  (void)num_cus;
   if (batch < 2 || batch > 64 || n == 0 || m == 0) return false;
-  if (((uintptr_t)w & 3) != 0) return false;
+  if (m % kSkStageK != 0 || ((uintptr_t)w & 15) != 0) return false;
+  // 32-bit piece offsets within W and X
+  if (n * (m / kBlockElems) * kBlockBytes > 0xFFFFFFFFull || 64 * m * 2 > 0xFFFFFFFFull) return false;
   if (n > (size_t)0x7FFFFFFF || m > (size_t)0x7FFFFFF) return false;
-  if (skinny_waves(n, m, num_cus) == 0) return false;
   return w_len / kBlockBytes >= n * (m / kBlockElems);
 }
 
-size_t skinny_workspace_bytes(size_t batch, size_t m) {
+static size_t round256(size_t v) { return (v + 255) / 256 * 256; }
+
+size_t skinny_workspace_bytes(size_t batch, size_t n, size_t m, int num_cus) {
   const SkinnyShape sh = skinny_shape(batch);
-  return (size_t)sh.rows * m * 2 + 64 * 4;
+  const int sp = skinny_splits(n, m, batch, num_cus);
+  size_t b = round256((size_t)sh.rows * m * 2) + round256(m / kSkStageK * 16 * 4);
+  if (sp > 1) b += (size_t)sp * batch * n * 4;
+  return b;
 }
 
 hipError_t launch_q4_0_skinny(float* y, const uint8_t* w, const float* x, const float* bias,
@@ -341,14 +425,19 @@ hipError_t launch_q4_0_skinny(float* y, const uint8_t* w, const float* x, const 
                               hipStream_t s) {
   const SkinnyShape sh = skinny_shape(batch);
   uint8_t* xa = static_cast<uint8_t*>(ws);
-  float* inv_s = reinterpret_cast<float*>(xa + (size_t)sh.rows * m * 2);
+  float* inv_s = reinterpret_cast<float*>(xa + round256((size_t)sh.rows * m * 2));
+  float* part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(inv_s) +
+                                         round256(m / kSkStageK * 16 * 4));
   const int hi_rows = sh.split ? sh.mh : sh.rows;
-  hipLaunchKernelGGL(x_skinny_kernel, dim3(hi_rows), dim3(256), 0, s, xa, inv_s, x, (int)batch,
-                     (int)m, sh.mh, sh.split);
+  const int stages = (int)(m / kSkStageK);
+  hipLaunchKernelGGL(x_skinny_kernel, dim3((unsigned)((stages + 7) / 8), (unsigned)hi_rows),
+                     dim3(256), 0, s, xa, inv_s, x, (int)batch, (int)m, sh.mh, sh.split);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  const int sp = skinny_splits(n, m, batch, num_cus);
   SkinnyArgs a;
   a.y = y;
+  a.part = part;
   a.w = w;
   a.xa = xa;
   a.inv_s = inv_s;
@@ -356,15 +445,20 @@ hipError_t launch_q4_0_skinny(float* y, const uint8_t* w, const float* x, const 
   a.M = (int)batch;
   a.N = (int)n;
   a.K = (int)m;
-  a.Mh = sh.mh;
   a.split = sh.split;
-  const int grid = (int)((n + 15) / 16);
-  const int wv = skinny_waves(n, m, num_cus);
-  switch (sh.mf) {
-    case 1: return launch_mf<1>(wv, a, grid, s);
-    case 2: return launch_mf<2>(wv, a, grid, s);
-    default: return launch_mf<4>(wv, a, grid, s);
-  }
+  a.splits = sp;
+  const dim3 grid((unsigned)((n + 63) / 64), (unsigned)sp);
+  if (sh.mf == 1)
+    e = launch_mf<1, true>(a, grid, s);
+  else if (sh.mf == 2)
+    e = sh.split ? launch_mf<2, true>(a, grid, s) : launch_mf<2, false>(a, grid, s);
+  else
+    e = launch_mf<4, false>(a, grid, s);
+  if (e != hipSuccess || sp == 1) return e;
+  const size_t mn = batch * n;
+  hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, y,
+                     part, bias, (int)batch, (int)n, sp);
+  return hipGetLastError();
 }
 
 }  // namespace hypno
