@@ -369,14 +369,16 @@ SkinnyShape skinny_shape(size_t batch) {
   return s;
 }
 
-// K ranges per row tile: about `target` resident work-groups in all (two per
-// CU when a work-group's LDS allows it), at most one range per stage.
+// K ranges per row tile: none when the row tiles alone cover three quarters
+// of the CUs (a split costs a reduction launch), else about `target`
+// resident work-groups in all (two per CU when a work-group's LDS allows
+// it), at most one range per stage.
 int skinny_splits(size_t n, size_t m, size_t batch, int num_cus) {
   const SkinnyShape sh = skinny_shape(batch);
   const size_t tiles = (n + 63) / 64;
   const size_t per_cu = sh.mf == 1 ? 2 : 1;
   const size_t target = (size_t)num_cus * per_cu;
-  size_t sp = (target + tiles / 2) / tiles;
+  size_t sp = tiles * 4 >= (size_t)num_cus * 3 ? 1 : (target + tiles / 2) / tiles;
   const size_t gsteps = m / kSkStageK;
   if (sp < 1) sp = 1;
   if (sp > gsteps) sp = gsteps;

@@ -223,6 +223,43 @@ def test_skinny_q4_0(torch, hk, orc, batch, n, m):
         assert orc.rel_l2(got, ref) <= GEMM_TOL
 
 
+@pytest.mark.parametrize("batch,n,m", [(8, 1000, 4096), (40, 1100, 4096), (16, 4096, 14336)])
+def test_skinny_split_k_repeat(torch, hk, orc, batch, n, m):
+    """Split-K (few row tiles): the work-group finishing a tile adds the
+    partials in split order and re-arms the tile counter, so back-to-back
+    calls with other inputs in between stay bit-identical and correct."""
+    import ctypes
+    from hypno_amd import _lib
+    lib = _lib.load()
+    qh = _q4(orc, n, m, seed=batch + n)
+    q = _gpu(torch, qh)
+    x1 = orc.normal_f32(batch + 1, (batch, m))
+    x2 = orc.normal_f32(batch + 2, (batch, m))
+    bias = orc.normal_f32(batch + 3, n)
+    bg = _gpu(torch, bias)
+
+    def run(x):
+        y = torch.empty(batch * n, dtype=torch.float32, device="cuda")
+        xg = _gpu(torch, x)
+        st = lib.hypno_hip_matmul_q4_0_dev(ctypes.c_void_p(y.data_ptr()),
+                                           ctypes.c_void_p(q.data_ptr()), qh.size,
+                                           ctypes.c_void_p(xg.data_ptr()),
+                                           ctypes.c_void_p(bg.data_ptr()), n, m, batch, None)
+        assert st == 0
+        torch.cuda.synchronize()
+        return y.cpu().numpy().reshape(batch, n)
+
+    y1, y2, y1b = run(x1), run(x2), run(x1)
+    assert np.array_equal(y1, y1b)
+    for x, got in ((x1, y1), (x2, y2)):
+        ref = orc.batch_matmul(qh, 3, x, n, m, batch) + bias
+        if batch < 16:
+            for t in range(batch):
+                assert orc.normwise_err(got[t], ref[t]) <= GEMV_TOL, t
+        else:
+            assert orc.rel_l2(got, ref) <= GEMM_TOL
+
+
 def test_skinny_wide_range_activations(torch, hk, orc):
     """Per-token power-of-two scaling: tokens of very different magnitude,
     a 1e4 outlier channel, tiny values and an all-zero token stay within the
