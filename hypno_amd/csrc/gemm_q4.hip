@@ -15,24 +15,30 @@
 //    each wave a 64 x 64 sub-tile (4 x 4 MFMA tiles).  At the end K-group 1
 //    hands its accumulators to K-group 0 through LDS (fixed-order sum:
 //    deterministic, no atomics, no zeroed output).
-//  * All global reads are LDS DMA (global_load_lds_dwordx4), issued
-//    kPrefetch stages ahead into LDS rings: no staging registers, and every
-//    wave issues exactly three DMA instructions per stage, so one
-//    s_waitcnt vmcnt(3) per stage waits for precisely the data the next
-//    stage needs.
-//      - X: a pre-pass rounds X to fp16 once, permuting each group of 8
+//  * Global reads run kPrefetch = 4 stages ahead, three VMEM instructions
+//    per wave and stage, so one s_waitcnt vmcnt(3) per stage waits for
+//    precisely the data the next stage needs:
+//      - X: two LDS DMAs (global_load_lds_dwordx4) per wave into a 4-slot
+//        ring.  A pre-pass rounds X to fp16 once, permuting each group of 8
 //        columns into the order the nibble unpack emits weights.  Each
 //        stage's 128 x 64 tile lands with 16-byte chunk c of row r in slot
 //        c ^ ((r >> 1) & 7) (conflict-free MFMA operand reads).
-//      - W: each row's 36 bytes of the stage arrive as a 64-byte window
-//        starting at the 16-byte boundary at or below them.
-//  * Two stages ahead, every thread expands a quarter of a row's stage (one
-//    half block) from the raw window into an fp16 (nib - 8) tile with one
-//    and-or op and one packed fp16 op per pair of weights, plus the block
-//    scale as fp32.  The expansion is shared by all 128 rows of X.
-//  * While a stage's MFMAs run from registers, the operands of the next
-//    stage are already being read from LDS into a second register set, so
-//    LDS latency hides behind the matrix work.  One barrier per stage.
+//      - W: one 12-byte register read per thread (global_load_dwordx3 from
+//        asm, so the compiler adds no waits of its own): a quarter of one
+//        row's 36 stage bytes -- a block's scale and 8 nibble bytes, or the
+//        other 8 -- in a two-deep register double buffer.
+//  * Two stages ahead, every thread unpacks its 16 nibbles into exact fp16
+//    (nib - 8) with one and-or op and one packed fp16 op per pair of weights
+//    and writes them, with the block scale as fp32, to a 2-slot B ring in
+//    LDS.  The expansion is shared by all 128 rows of X.
+//  * Each MFMA operand register is reloaded from LDS for the next stage
+//    right after its last MFMA of this stage, so LDS latency hides behind
+//    the matrix work.  One barrier per stage.
+//  * Tile grids under 3/4 of the CUs split K over blockIdx.y into fp32
+//    partial planes that split_k_reduce_kernel adds in split order (+ bias).
+//  * Work-groups go round-robin over the 8 XCDs; the tile order gives each
+//    XCD a contiguous range of tiles, so the M-tiles sharing a W tile share
+//    an L2.
 //
 // Requirements (q4_0_gemm_v3_ok): K % 256 == 0 (rows of W start on 16-byte
 // boundaries), w 16-byte aligned, w holds N whole rows.  Rows past N read

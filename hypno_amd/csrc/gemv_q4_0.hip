@@ -75,9 +75,11 @@ hipError_t launch_q4_0_generic(float* y, const uint8_t* w, size_t w_len, const f
 // span, so the loads coalesce), and keeps the next three steps in flight in
 // a register ring that runs across job boundaries.  A lane-dependent byte
 // permute realigns the nibble dwords (a block starts at byte 0 or 2 of its
-// window), the nibbles are converted in registers (v_cvt_f32_ubyte*), sum(nib
-// * x) accumulates in fp32, and the block's scale is applied as
-// d * (sum - 8 * sum(x)).  Each step, DPP row shifts add the partials of
+// window); nib ^ 8 read as a signed i4 is nib - 8, and v_dot8_i32_i4
+// multiplies eight of them with eight i4 digits of the block's activations
+// (the limbs below) into an exact int32 sum; the limb sums combine into one
+// fp32 value that the block scale d and the block's exponent scale.  Each
+// step, DPP row shifts add the partials of
 // aligned 8-lane groups (a row is B/8 whole groups), and the group sums of S
 // steps are parked in LDS; after one barrier one thread per row adds its
 // groups in a fixed order (deterministic) and writes y.  Activations are
