@@ -310,6 +310,10 @@ hipError_t launch_x_f16_permuted(const float* x, size_t batch, size_t m, void* w
   return launch_x_prepass(x, batch, m, ws, true, nullptr, 0, s);
 }
 
+hipError_t launch_x_f16_plain(const float* x, size_t batch, size_t m, void* ws, hipStream_t s) {
+  return launch_x_prepass(x, batch, m, ws, false, nullptr, 0, s);
+}
+
 template <bool kQ4>
 static hipError_t launch_gemm(float* y, const uint8_t* w, const float* x, const float* bias,
                               size_t n, size_t m, size_t batch, void* ws, int num_cus,

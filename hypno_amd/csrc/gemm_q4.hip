@@ -378,6 +378,142 @@ split_k_reduce_kernel(float* __restrict__ y, const float* __restrict__ part,
   y[i] = v + (bias ? bias[i % n] : 0.0f);
 }
 
+// ---------------------------------------------------------------------------
+// FP16 weights: Y[M][N] = X[M][K] . W[N][K]^T with W fp16 (kernels.rs:571-586
+// per token).  No per-block scale, so the MFMAs accumulate straight into
+// their accumulators; at the BASELINE sizes (lm_head, M = 128: 2 bytes per
+// weight against 256 flop) the kernel is bound by the weight stream, so it
+// keeps many bytes in flight: a 128 x 64 NW tile per work-group of 2 NW
+// waves (64 x 64 each), stages of 64 K, and an LDS ring fed by DMA, W
+// non-temporal (read once), X cached (shared by all N tiles).  Both tiles use
+// the layout of the Q4_0 kernel's X tile (chunk c of row r in slot
+// c ^ ((r >> 1) & 7)), so the operand reads of 16 rows hit 16 bank groups.
+// Geometry: NW waves along N (BN = 64 NW), two along M (128 rows).
+template <int NW>
+struct F16Geom {
+  static constexpr int kWaves = 2 * NW;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kBN = 64 * NW;
+  static constexpr int kXBytes = kTileBytes;            // 128 rows x 128 bytes
+  static constexpr int kWBytes = kBN * kRowBytes;
+  static constexpr int kSlot = kXBytes + kWBytes;
+  static constexpr int kRing = NW == 2 ? 4 : 3;
+  static constexpr int kLds = kRing * kSlot;           // 128 KB / 144 KB
+  static constexpr int kXDma = kXBytes / 1024 / kWaves;  // per wave and stage
+  static constexpr int kWDma = kWBytes / 1024 / kWaves;
+  static_assert(kLds <= 160 * 1024, "LDS budget");
+};
+constexpr int kF16NW = 4;  // 128 x 256 tiles
+
+struct F16Args {
+  float* y;
+  const uint8_t* w;   // fp16 [N][K]
+  const uint8_t* xh;  // fp16 [Mp][K]
+  const float* bias;
+  int M, N, K;
+  int tiles_m, tiles_n;
+  int xcd_map;
+  int splits;
+  float* part;
+};
+
+__device__ __forceinline__ void dma16_nt(const void* src, uint8_t* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_wave_base,
+                                   16, 0, 2);
+}
+
+template <int NW>
+__global__ void __launch_bounds__(F16Geom<NW>::kThreads, 1) f16_gemm_v2_kernel(const F16Args a) {
+  using G = F16Geom<NW>;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = wave / NW, wn = wave % NW;
+  const int lr = lane & 15, lq = lane >> 4;
+
+  int tile = blockIdx.x;
+  const int ntiles = a.tiles_m * a.tiles_n;
+  if (a.xcd_map) tile = (tile & 7) * (ntiles >> 3) + (tile >> 3);
+  const int m0 = (tile % a.tiles_m) * BM;
+  const int n0 = (tile / a.tiles_m) * G::kBN;
+  const int gsteps = a.K / BK;
+  const int z = blockIdx.y;
+  const int s0 = (int)((long long)gsteps * z / a.splits);
+  const int steps = (int)((long long)gsteps * (z + 1) / a.splits) - s0;
+  const size_t row_bytes = (size_t)a.K * 2;
+
+  // DMA i of a tile fills rows 8 (kWaves i + wave) .. + 7: lane -> row
+  // 8 (kWaves i + wave) + (lane >> 3), slot lane & 7 holding logical chunk
+  // (lane & 7) ^ ((row >> 1) & 7) ((row >> 1) & 7 does not depend on i).
+  const int dr = 8 * wave + (lane >> 3);
+  const int dc = (lane & 7) ^ ((dr >> 1) & 7);
+  const uint8_t* xsrc = a.xh + (size_t)(m0 + dr) * row_bytes + dc * 16;
+  const uint8_t* wsrc[G::kWDma];
+#pragma unroll
+  for (int i = 0; i < G::kWDma; i++)
+    wsrc[i] = a.w + (size_t)min(n0 + 8 * G::kWaves * i + dr, a.N - 1) * row_bytes + dc * 16;
+  auto issue = [&](int s) {  // stage min(s, steps - 1) into ring slot s % kRing
+    const int sc = s < steps ? s : steps - 1;
+    const size_t koff = (size_t)(s0 + sc) * kRowBytes;
+    uint8_t* slot = smem + (s % G::kRing) * G::kSlot + wave * 1024;
+#pragma unroll
+    for (int i = 0; i < G::kXDma; i++)
+      dma16(xsrc + (size_t)8 * G::kWaves * i * row_bytes + koff, slot + i * 1024 * G::kWaves);
+#pragma unroll
+    for (int i = 0; i < G::kWDma; i++)
+      dma16_nt(wsrc[i] + koff, slot + G::kXBytes + i * 1024 * G::kWaves);
+  };
+
+  floatx4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int s = 0; s < G::kRing - 1; s++) issue(s);
+  for (int s = 0; s < steps; s++) {
+    // stage s landed (all but the newest kRing - 2 stages), everyone done
+    // with stage s - 1, whose slot the next request reuses
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier"
+                 : : "n"((G::kXDma + G::kWDma) * (G::kRing - 2)) : "memory");
+    issue(s + G::kRing - 1);
+    const uint8_t* xt = smem + (s % G::kRing) * G::kSlot;
+    const uint8_t* wt = xt + G::kXBytes;
+#pragma unroll
+    for (int kh = 0; kh < 2; kh++) {
+      half8 fa[4], fb[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        fa[i] = *reinterpret_cast<const half8*>(xt + tile_off(wm * 64 + 16 * i + lr, 4 * kh + lq));
+        fb[i] = *reinterpret_cast<const half8*>(wt + tile_off(wn * 64 + 16 * i + lr, 4 * kh + lq));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // trailing re-loads landed
+
+  // acc[i][j][r]: row m0 + wm 64 + 16 i + 4 lq + r, column n0 + wn 64 + 16 j + lr
+  float* out = a.splits > 1 ? a.part + (size_t)z * a.M * a.N : a.y;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int n = n0 + wn * 64 + 16 * j + lr;
+    if (n >= a.N) continue;
+    const float bv = (a.splits == 1 && a.bias) ? a.bias[n] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int m = m0 + wm * 64 + 16 * i + 4 * lq + r;
+        if (m < a.M) out[(size_t)m * a.N + n] = acc[i][j][r] + bv;
+      }
+  }
+}
+
 // K splits: when the tile grid leaves CUs idle, each tile's K range is cut
 // into `splits` pieces (each at least kMinSplitStages stages) so the grid
 // nearly fills the chip.
@@ -408,6 +544,60 @@ bool q4_0_gemm_v3_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t 
   const size_t tiles = ((n + BN - 1) / BN) * ((batch + BM - 1) / BM);
   if (tiles > (size_t)0x7FFFFFFF) return false;
   return w_len / kBlockBytes >= n * (m / kBlockElems);
+}
+
+size_t f16_gemm_v2_workspace_bytes(size_t batch, size_t n, size_t m, int num_cus) {
+  const size_t tiles = ((n + F16Geom<kF16NW>::kBN - 1) / F16Geom<kF16NW>::kBN) *
+                       ((batch + BM - 1) / BM);
+  const int splits = pick_splits(tiles, m, num_cus);
+  const size_t xb = round256(gemm_workspace_bytes(batch, m));
+  return splits > 1 ? xb + (size_t)splits * batch * n * 4 : xb;
+}
+
+bool f16_gemm_v2_ok(const uint8_t* w, size_t n, size_t m, size_t batch) {
+  if (m == 0 || m % BK != 0 || n == 0 || batch == 0) return false;
+  if (((uintptr_t)w & 15) != 0) return false;
+  if (n > (size_t)0x7FFFFFFF || m > (size_t)0x7FFFFFF || batch > (size_t)0x7FFFFFFF) return false;
+  const size_t tiles = ((n + BN - 1) / BN) * ((batch + BM - 1) / BM);
+  return tiles <= (size_t)0x7FFFFFFF;
+}
+
+hipError_t launch_f16_gemm_v2(float* y, const uint8_t* w, const float* x, const float* bias,
+                              size_t n, size_t m, size_t batch, void* ws, int num_cus,
+                              hipStream_t s) {
+  using G = F16Geom<kF16NW>;
+  hipError_t e = launch_x_f16_plain(x, batch, m, ws, s);
+  if (e != hipSuccess) return e;
+  static bool attr_set = false;
+  if (!attr_set) {
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(f16_gemm_v2_kernel<kF16NW>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, G::kLds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  F16Args a;
+  a.y = y;
+  a.w = w;
+  a.xh = static_cast<const uint8_t*>(ws);
+  a.bias = bias;
+  a.M = (int)batch;
+  a.N = (int)n;
+  a.K = (int)m;
+  a.tiles_m = (int)((batch + BM - 1) / BM);
+  a.tiles_n = (int)((n + G::kBN - 1) / G::kBN);
+  const int tiles = a.tiles_m * a.tiles_n;
+  a.xcd_map = (tiles % 8) == 0 ? 1 : 0;
+  a.splits = pick_splits((size_t)tiles, m, num_cus);
+  a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) +
+                                    round256(gemm_workspace_bytes(batch, m)));
+  hipLaunchKernelGGL(f16_gemm_v2_kernel<kF16NW>, dim3(tiles, a.splits), dim3(G::kThreads), G::kLds,
+                     s, a);
+  e = hipGetLastError();
+  if (e != hipSuccess || a.splits == 1) return e;
+  const size_t mn = batch * n;
+  hipLaunchKernelGGL(split_k_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, y,
+                     a.part, bias, mn, (int)n, a.splits);
+  return hipGetLastError();
 }
 
 hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const float* bias,

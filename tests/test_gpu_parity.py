@@ -467,6 +467,35 @@ def test_gemm_f16(torch, hk, orc, batch, n, m):
     assert orc.rel_l2(y.cpu().numpy().reshape(batch, n), ref) <= GEMM_TOL
 
 
+@pytest.mark.parametrize("batch,n,m", [(200, 1000, 1024), (130, 3000, 2048), (40, 513, 320)])
+def test_gemm_f16_bias_tails_and_repeat(torch, hk, orc, batch, n, m):
+    """FP16 GEMM with bias through the C ABI: M and N tails, K split across
+    work-groups (partials added in split order), and bit-identical repeats."""
+    import ctypes
+    from hypno_amd import _lib
+    lib = _lib.load()
+    w = _f16w(orc, n, m, seed=n + 3)
+    wb = _gpu(torch, w.view(np.uint8).ravel())
+    x = _gpu(torch, orc.normal_f32(9, (batch, m)))
+    bias = orc.normal_f32(10, n)
+    bg = _gpu(torch, bias)
+
+    def run():
+        y = torch.empty(batch * n, dtype=torch.float32, device="cuda")
+        st = lib.hypno_hip_matmul_f16_dev(ctypes.c_void_p(y.data_ptr()),
+                                          ctypes.c_void_p(wb.data_ptr()), wb.numel(),
+                                          ctypes.c_void_p(x.data_ptr()),
+                                          ctypes.c_void_p(bg.data_ptr()), n, m, batch, None)
+        assert st == 0
+        torch.cuda.synchronize()
+        return y.cpu().numpy().reshape(batch, n)
+
+    y1, y2 = run(), run()
+    assert np.array_equal(y1, y2)
+    ref = x.cpu().numpy().astype(np.float64) @ w.astype(np.float64).T + bias
+    assert orc.rel_l2(y1, ref) <= GEMM_TOL
+
+
 # --- host-slice ABI (drop-in for the &[f32]/&[u8] signature) --------------------------
 
 def test_host_slice_entry_points(hk, orc):
