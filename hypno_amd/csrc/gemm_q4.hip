@@ -172,7 +172,13 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   // same 2 bytes later (the block starts 18 bytes into the stage's 36), so
   // the dword-aligned read starts at 16 + 8 eh and ends at most at the row's
   // end.
-  const int er = t >> 2, eb = (t >> 1) & 1, eh = t & 1;
+  // The four threads of a row are lanes 4k..4k+3; lanes 4k+4..4k+7 take a
+  // row whose swizzle differs in its low bit (k's two low bits swapped), so
+  // every 8 lanes of a 16-byte LDS write cover all eight chunk slots of the
+  // 128-byte row stride (no bank conflict).
+  const int erk = (t >> 2) & 15;
+  const int er = (t >> 6) * 16 + ((erk & 12) | ((erk & 1) << 1) | ((erk >> 1) & 1));
+  const int eb = (t >> 1) & 1, eh = t & 1;
   const bool evalid = n0 + er < a.N;
   const uint32_t esel = eb ? 0x07060504u : 0x05040302u;  // block at byte 0 / 2 mod 4
   const uint8_t* erow = a.w + (size_t)min(n0 + er, a.N - 1) * w_row + 16 * eb + 8 * eh;
