@@ -197,20 +197,16 @@ int f16_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const floa
     cus = ds->cus;
   }
   hipError_t e;
-  const bool v2 = batch >= kGemmMinBatch && f16_gemm_v2_ok(w, n, m, batch);
-  if (v2 || (batch >= kGemmMinBatch && f16_gemm_ok(w, n, m, batch))) {
+  if (batch >= kGemmMinBatch && f16_gemm_v2_ok(w, n, m, batch)) {
     void* ws = nullptr;
     {
       std::lock_guard<std::mutex> g(g_mu);
       DevBuf& b = ds->workspaces[s];
-      e = ensure(b, v2 ? f16_gemm_v2_workspace_bytes(batch, n, m, cus)
-                       : gemm_workspace_bytes(batch, m),
-                 s);
+      e = ensure(b, f16_gemm_v2_workspace_bytes(batch, n, m, cus), s);
       if (e != hipSuccess) return hip_fail(e, "GEMM workspace");
       ws = b.p;
     }
-    e = v2 ? launch_f16_gemm_v2(y, w, x, bias, n, m, batch, ws, cus, s)
-           : launch_f16_gemm(y, w, x, bias, n, m, batch, ws, cus, s);
+    e = launch_f16_gemm_v2(y, w, x, bias, n, m, batch, ws, cus, s);
     if (e != hipSuccess) return hip_fail(e, "f16 GEMM launch");
     return HYPNO_HIP_OK;
   }

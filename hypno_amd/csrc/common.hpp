@@ -219,7 +219,6 @@ hipError_t launch_f16_generic(float* y, const uint8_t* w, const float* x, const 
 bool f16_gemv_fast_ok(const uint8_t* w, size_t n, size_t m);
 hipError_t launch_f16_gemv_fast(float* y, const uint8_t* w, const float* x, const float* bias,
                                 size_t n, size_t m, int num_cus, hipStream_t s);
-bool f16_gemm_ok(const uint8_t* w, size_t n, size_t m, size_t batch);
 // X -> fp16 [Mp][K] in natural column order (FP16-weight GEMM pre-pass).
 hipError_t launch_x_f16_plain(const float* x, size_t batch, size_t m, void* ws, hipStream_t s);
 // DMA-fed FP16-weight GEMM (gemm_q4.hip).
@@ -228,8 +227,5 @@ size_t f16_gemm_v2_workspace_bytes(size_t batch, size_t n, size_t m, int num_cus
 hipError_t launch_f16_gemm_v2(float* y, const uint8_t* w, const float* x, const float* bias,
                               size_t n, size_t m, size_t batch, void* ws, int num_cus,
                               hipStream_t s);
-hipError_t launch_f16_gemm(float* y, const uint8_t* w, const float* x, const float* bias,
-                           size_t n, size_t m, size_t batch, void* workspace, int num_cus,
-                           hipStream_t s);
 
 }  // namespace hypno

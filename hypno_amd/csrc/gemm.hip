@@ -1,4 +1,7 @@
-// Batched-prefill GEMM on CDNA4 MFMA: Y[M][N] = X[M][K] . W[N][K]^T (+ bias).
+// Q4_0 prefill GEMM for shapes the main kernel (gemm_q4.hip) does not take
+// (K % 64 == 0 but K % 256 != 0, 4-byte-aligned weights), and the fp16
+// activation pre-passes shared with gemm_q4.hip:
+// Y[M][N] = X[M][K] . W[N][K]^T (+ bias).
 //
 // Pre-pass: X (fp32) is rounded to fp16 into a workspace padded to a multiple
 // of the 128-row tile (float4 loads, one 16-byte store per 8 columns).  For
@@ -12,15 +15,13 @@
 // through two LDS buffers: while the waves compute step s from one buffer,
 // the global loads of step s+1 are already in flight into registers, and are
 // then written to the other buffer (one barrier per step).
-//   Q4_0: each thread takes one (row, block) of the step's 128 x 2 weight
+//   Each thread takes one (row, block) of the step's 128 x 2 weight
 //   blocks, loads its 20-byte window (the 64 threads of a wave read
 //   contiguous memory), expands the 32 nibbles to exact fp16 integers
 //   (nibble - 8) into LDS, and stores the fp32 scale.  Every 32-column block
 //   is one v_mfma_f32_16x16x32_f16 with a zero accumulator per 16 x 16 tile;
 //   the partial is multiplied by the block's fp32 scale into fp32
 //   accumulators.
-//   FP16: the weight tile is copied to LDS as is and the MFMA accumulates
-//   across K directly.
 // Split-K: when the tile grid has fewer than two work-groups per CU, K is
 // split in two and the halves are added into the zeroed Y with atomics (two
 // addends onto zero: the sum is the same in either order).
@@ -46,12 +47,6 @@ bool q4_0_gemm_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t bat
   if (((uintptr_t)w & 3) != 0) return false;
   if (n > (size_t)0x7FFFFFFF || m > (size_t)0x7FFFFFFF || batch > (size_t)0x7FFFFFFF) return false;
   return w_len / kBlockBytes >= n * (m / kBlockElems);
-}
-
-bool f16_gemm_ok(const uint8_t* w, size_t n, size_t m, size_t batch) {
-  if (m == 0 || m % kBK != 0 || n == 0 || batch == 0) return false;
-  if (((uintptr_t)w & 15) != 0) return false;
-  return n <= (size_t)0x7FFFFFFF && m <= (size_t)0x7FFFFFFF && batch <= (size_t)0x7FFFFFFF;
 }
 
 // X fp32 [M][K] -> Xh fp16 [Mp][K] (zero rows M..Mp-1); optionally zero Y.
@@ -117,18 +112,17 @@ __device__ __forceinline__ u32x4 unpack_nib8(uint32_t dw) {
 // Global loads of one K step held in registers until they are written to LDS.
 struct StepRegs {
   u32x4 a[4];  // X: 4 x 16 bytes
-  u32x4 b[4];  // W: Q4_0 uses b[0] + bw (20-byte window); FP16 uses all four
+  u32x4 b;  // W: this thread's 20-byte window (16 + 4 bytes)
   uint32_t bw;
 };
 
-template <bool kQ4>
 __global__ void __launch_bounds__(256, 2)
 gemm_kernel(float* __restrict__ y, const uint8_t* __restrict__ w, const u32x4* __restrict__ xh,
             const float* __restrict__ bias, int M, int N, int K, int ksplit) {
   extern __shared__ __align__(16) uint8_t smem[];
   // LDS: 2 x {A tile, B tile} fp16 + 2 x scales [2 blocks][128]
   _Float16* As0 = reinterpret_cast<_Float16*>(smem);
-  const size_t buf_bytes = (size_t)2 * kTileHalves * 2 + (kQ4 ? 2 * kBN * 4 : 0);
+  const size_t buf_bytes = (size_t)2 * kTileHalves * 2 + 2 * kBN * 4;
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -140,7 +134,7 @@ gemm_kernel(float* __restrict__ y, const uint8_t* __restrict__ w, const u32x4* _
   const int k_len = K / ksplit;
   const int k_begin = kz * k_len;
   const int steps = k_len / kBK;
-  const size_t row_bytes = kQ4 ? (size_t)K / 32 * 18 : (size_t)K * 2;
+  const size_t row_bytes = (size_t)K / 32 * 18;
   const int kgroups = K / 8;
 
   // Q4_0 staging role: (row, block) of the step's 128 x 2 blocks
@@ -159,20 +153,10 @@ gemm_kernel(float* __restrict__ y, const uint8_t* __restrict__ w, const u32x4* _
       const int row = c >> 3, col = c & 7;
       r.a[i] = load_global<u32x4>(xh + (size_t)(m0 + row) * kgroups + k0 / 8 + col);
     }
-    if (kQ4) {
-      const size_t boff = (size_t)(k0 / 32 + qkb) * 18;
-      const uint8_t* p = qrow_ptr + (boff & ~(size_t)3);
-      r.b[0] = load_global<u32x4>(p);
-      r.bw = load_global<uint32_t>(p + 16);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int c = t + 256 * i;
-        const int row = c >> 3, col = c & 7;
-        const int rr = n0 + row < N ? n0 + row : 0;
-        r.b[i] = load_global<u32x4>(w + (size_t)rr * row_bytes + (size_t)(k0 + col * 8) * 2);
-      }
-    }
+    const size_t boff = (size_t)(k0 / 32 + qkb) * 18;
+    const uint8_t* p = qrow_ptr + (boff & ~(size_t)3);
+    r.b = load_global<u32x4>(p);
+    r.bw = load_global<uint32_t>(p + 16);
   };
 
   auto store_step = [&](int buf, const StepRegs& r) {
@@ -184,24 +168,13 @@ gemm_kernel(float* __restrict__ y, const uint8_t* __restrict__ w, const u32x4* _
       const int row = c >> 3, col = c & 7;
       *reinterpret_cast<u32x4*>(&As[row * kLdsRow + col * 8]) = r.a[i];
     }
-    if (kQ4) {
-      float* Sc = reinterpret_cast<float*>(Bs + kTileHalves);
-      const uint32_t d[5] = {r.b[0].x, r.b[0].y, r.b[0].z, r.b[0].w, r.bw};
-      Sc[qkb * kBN + qrow] = qvalid ? f16_bits_to_f32(d[0] >> sh_d) : 0.0f;
+    float* Sc = reinterpret_cast<float*>(Bs + kTileHalves);
+    const uint32_t d[5] = {r.b.x, r.b.y, r.b.z, r.b.w, r.bw};
+    Sc[qkb * kBN + qrow] = qvalid ? f16_bits_to_f32(d[0] >> sh_d) : 0.0f;
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const uint32_t q = __builtin_amdgcn_perm(d[j + 1], d[j], sel_q);
-        *reinterpret_cast<u32x4*>(&Bs[qrow * kLdsRow + qkb * 32 + j * 8]) = unpack_nib8(q);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int c = t + 256 * i;
-        const int row = c >> 3, col = c & 7;
-        u32x4 v = r.b[i];
-        if (n0 + row >= N) v = u32x4{0u, 0u, 0u, 0u};
-        *reinterpret_cast<u32x4*>(&Bs[row * kLdsRow + col * 8]) = v;
-      }
+    for (int j = 0; j < 4; j++) {
+      const uint32_t q = __builtin_amdgcn_perm(d[j + 1], d[j], sel_q);
+      *reinterpret_cast<u32x4*>(&Bs[qrow * kLdsRow + qkb * 32 + j * 8]) = unpack_nib8(q);
     }
   };
 
@@ -229,26 +202,18 @@ gemm_kernel(float* __restrict__ y, const uint8_t* __restrict__ w, const u32x4* _
       for (int j = 0; j < 4; j++)
         b[j] = *reinterpret_cast<const half8*>(
             &Bs[(wn * 64 + j * 16 + frag_row) * kLdsRow + kb * 32 + frag_k]);
-      if (kQ4) {
-        float sc[4];
+      float sc[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) sc[j] = Sc[kb * kBN + wn * 64 + j * 16 + frag_row];
+      for (int j = 0; j < 4; j++) sc[j] = Sc[kb * kBN + wn * 64 + j * 16 + frag_row];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+      for (int i = 0; i < 4; i++)
 #pragma unroll
-          for (int j = 0; j < 4; j++) {
-            const floatx4 part = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                a[i], b[j], floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        for (int j = 0; j < 4; j++) {
+          const floatx4 part = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              a[i], b[j], floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
-            for (int r = 0; r < 4; r++) acc[i][j][r] = fmaf(sc[j], part[r], acc[i][j][r]);
-          }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-          for (int j = 0; j < 4; j++)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-      }
+          for (int r = 0; r < 4; r++) acc[i][j][r] = fmaf(sc[j], part[r], acc[i][j][r]);
+        }
     }
   };
 
@@ -314,40 +279,27 @@ hipError_t launch_x_f16_plain(const float* x, size_t batch, size_t m, void* ws, 
   return launch_x_prepass(x, batch, m, ws, false, nullptr, 0, s);
 }
 
-template <bool kQ4>
-static hipError_t launch_gemm(float* y, const uint8_t* w, const float* x, const float* bias,
-                              size_t n, size_t m, size_t batch, void* ws, int num_cus,
-                              hipStream_t s) {
+hipError_t launch_q4_0_gemm(float* y, const uint8_t* w, const float* x, const float* bias,
+                            size_t n, size_t m, size_t batch, void* ws, int num_cus,
+                            hipStream_t s) {
   const size_t tiles_n = (n + kBN - 1) / kBN;
   const size_t tiles_m = round_up(batch, kBM) / kBM;
   const int ksplit = pick_ksplit(tiles_n * tiles_m, m, num_cus);
-  hipError_t e = launch_x_prepass(x, batch, m, ws, kQ4, ksplit > 1 ? y : nullptr,
+  hipError_t e = launch_x_prepass(x, batch, m, ws, true, ksplit > 1 ? y : nullptr,
                                   ksplit > 1 ? n * batch : 0, s);
   if (e != hipSuccess) return e;
-  const size_t lds = 2 * ((size_t)2 * kTileHalves * 2 + (kQ4 ? 2 * kBN * 4 : 0));
+  const size_t lds = 2 * ((size_t)2 * kTileHalves * 2 + 2 * kBN * 4);
   static bool attr_set = false;
   if (!attr_set) {
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_kernel<kQ4>),
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
   const dim3 grid((unsigned)tiles_n, (unsigned)tiles_m, (unsigned)ksplit);
-  hipLaunchKernelGGL(gemm_kernel<kQ4>, grid, dim3(256), lds, s, y, w, (const u32x4*)ws, bias,
+  hipLaunchKernelGGL(gemm_kernel, grid, dim3(256), lds, s, y, w, (const u32x4*)ws, bias,
                      (int)batch, (int)n, (int)m, ksplit);
   return hipGetLastError();
-}
-
-hipError_t launch_q4_0_gemm(float* y, const uint8_t* w, const float* x, const float* bias,
-                            size_t n, size_t m, size_t batch, void* ws, int num_cus,
-                            hipStream_t s) {
-  return launch_gemm<true>(y, w, x, bias, n, m, batch, ws, num_cus, s);
-}
-
-hipError_t launch_f16_gemm(float* y, const uint8_t* w, const float* x, const float* bias,
-                           size_t n, size_t m, size_t batch, void* ws, int num_cus,
-                           hipStream_t s) {
-  return launch_gemm<false>(y, w, x, bias, n, m, batch, ws, num_cus, s);
 }
 
 }  // namespace hypno
