@@ -20,7 +20,10 @@ Also reported, in the same JSON line:
                 GEMM at Llama-3.2-3B MLP shapes (M = 512), configs[3] the
                 Mistral-7B decode stream (224 GEMVs, one plan launch) and the
                 M-sweep {1, 8, 64, 512, 2048}, configs[4] the lm_head in Q4_0
-                and FP16 at M = 1 and 128.
+                and FP16 at M = 1 and 128; model_load: a TinyLlama-shaped
+                .hypno file opened with its payloads uploaded to HBM
+                (pipelined pinned upload, against a pageable copy and the
+                reference's host-only open).
 
 Inputs are synthetic: weights N(0, 0.02) from a seeded torch generator,
 quantised on the GPU by the bit-exact Q4_0 quantizer; activations N(0, 1).
@@ -336,6 +339,117 @@ def lm_head(torch, lib):
                         "of 512/1024), M in {1,128}, Q4_0 and FP16 weights", "results": out}
 
 
+PCIE_PEAK_GBS = 64.0  # MI355X host link: PCIe 5.0 x16, one direction
+
+
+def write_hypno(path, metadata, tensors):
+    """Write (name, shape, dtype code, bytes-like payload) tensors as a .hypno
+    file with the converter's layout (format.rs:13-24, sft_convert.rs:121-289):
+    header, metadata pairs, tensor table, payloads at 64-byte boundaries."""
+    import struct
+    head = bytearray(struct.pack("<4sIII", b"HYPN", 1, len(metadata), len(tensors)))
+    for k, v in metadata:
+        kb, vb = k.encode(), v.encode()
+        head += struct.pack("<I", len(kb)) + kb + struct.pack("<I", len(vb)) + vb
+    table = sum(4 + len(n.encode()) + 4 + 8 * len(s) + 20 for n, s, _, _ in tensors)
+    cur = (len(head) + table + ALIGN - 1) // ALIGN * ALIGN
+    offs = []
+    for _, _, _, payload in tensors:
+        offs.append(cur)
+        cur = (cur + len(payload) + ALIGN - 1) // ALIGN * ALIGN
+    for (name, shape, dtype, payload), off in zip(tensors, offs):
+        nb = name.encode()
+        head += struct.pack("<I", len(nb)) + nb + struct.pack("<I", len(shape))
+        head += b"".join(struct.pack("<Q", d) for d in shape)
+        head += struct.pack("<IQQ", dtype, off, len(payload))
+    with open(path, "wb") as f:
+        f.write(head)
+        for (_, _, _, payload), off in zip(tensors, offs):
+            f.seek(off)
+            f.write(payload)
+        f.truncate(cur)
+    return cur
+
+
+def model_load(torch, lib):
+    """A TinyLlama-1.1B-shaped .hypno file (22 layers x 7 Q4_0 projections and
+    two FP32 norms per layer) in the page cache, opened with every payload
+    uploaded to HBM (hypno_hip_model_open), beside a host-only open (what
+    HypnoModel::open costs: map + parse) and one pageable host-to-device copy
+    of the mapped payload span (torch tensor over the mapping, .to("cuda"))."""
+    import mmap
+    import shutil
+    import tempfile
+    import warnings
+
+    import numpy as np
+
+    import hypno_amd as hk
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    shapes = [(n, m) for _ in range(LAYERS) for (_, n, m) in TINYLLAMA]
+    arena, offs = make_q4_arena(torch, lib, shapes, seed=4321, stream=st)
+    host = arena.cpu().numpy()
+    del arena
+    names = {"q": "self_attn.q_proj", "k": "self_attn.k_proj", "v": "self_attn.v_proj",
+             "o": "self_attn.o_proj", "gate": "mlp.gate_proj", "up": "mlp.up_proj",
+             "down": "mlp.down_proj"}
+    ones = np.ones(2048, np.float32).tobytes()
+    tensors = []
+    for i, ((n, m), (off, nb)) in enumerate(zip(shapes, offs)):
+        layer, short = divmod(i, len(TINYLLAMA))[0], TINYLLAMA[i % len(TINYLLAMA)][0]
+        if short == "q":
+            for norm in ("input_layernorm", "post_attention_layernorm"):
+                tensors.append((f"model.layers.{layer}.{norm}.weight", (2048,), 0, ones))
+        tensors.append((f"model.layers.{layer}.{names[short]}.weight", (n, m), 3,
+                        memoryview(host[off:off + nb])))
+    tmp = tempfile.mkdtemp(prefix="hypno_bench_")
+    try:
+        path = os.path.join(tmp, "tinyllama_q4_0.hypno")
+        size = write_hypno(path, [("architecture", "LlamaForCausalLM"),
+                                  ("num_hidden_layers", str(LAYERS)),
+                                  ("weight_layout", "row_major")], tensors)
+        hk.HypnoModel.open(path, device=False).close()
+        up, parse = [], []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            m = hk.HypnoModel.open(path)
+            up.append(time.perf_counter() - t0)
+            infos = m.manifest.tensors
+            span = infos[-1].offset + infos[-1].data_len - (infos[0].offset // ALIGN * ALIGN)
+            m.close()
+            t0 = time.perf_counter()
+            hk.HypnoModel.open(path, device=False).close()
+            parse.append(time.perf_counter() - t0)
+        with open(path, "rb") as f:
+            mm = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ)
+            with warnings.catch_warnings():
+                warnings.simplefilter("ignore")
+                src = torch.frombuffer(mm, dtype=torch.uint8)[infos[0].offset // ALIGN * ALIGN:]
+            naive = []
+            for _ in range(2):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                dev = src.to("cuda")
+                torch.cuda.synchronize()
+                naive.append(time.perf_counter() - t0)
+                del dev
+            del src
+            mm.close()
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    t_up, t_naive = sorted(up)[1], min(naive)
+    return {"workload": "TinyLlama-1.1B-shaped .hypno file (154 Q4_0 projections + 44 FP32 "
+                        "norms) from the page cache to HBM: hypno_hip_model_open, median of 3 (the "
+                        "first also creates the pinned staging pool)",
+            "file_bytes": size, "payload_span_bytes": span,
+            "open_upload_ms": round(t_up * 1e3, 2),
+            "first_open_ms": round(up[0] * 1e3, 2),
+            "upload_gbs": round(span / t_up / 1e9, 2),
+            "frac_pcie_peak": round(span / t_up / 1e9 / PCIE_PEAK_GBS, 3),
+            "host_only_open_ms": round(sorted(parse)[1] * 1e3, 3),
+            "pageable_copy_gbs": round(span / t_naive / 1e9, 2)}
+
+
 def single_gemv(torch, lib):
     """one 2048 x 2048 Q4_0 GEMV (TinyLlama q_proj), M = 1."""
     r = q4_case(torch, lib, 2048, 2048, 1, seed=2048, reps=50)
@@ -490,7 +604,7 @@ def main():
         sec = {}
         for key, fn in (("c0_single_gemv", single_gemv), ("c2_prefill_gemm", prefill_gemm),
                         ("c3_mistral_stream", mistral_stream), ("c3_m_sweep", mistral_m_sweep),
-                        ("c4_lm_head", lm_head)):
+                        ("c4_lm_head", lm_head), ("model_load", model_load)):
             print(f"[bench] secondary: {key}", file=sys.stderr, flush=True)
             sec[key] = fn(torch, lib)
         line["secondary"] = sec

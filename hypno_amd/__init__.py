@@ -21,4 +21,6 @@ from .kernels import (  # noqa: F401
     unregister_weight,
 )
 
+from .model import FormatError, HypnoModel  # noqa: F401
+
 __version__ = "0.1.0"

@@ -33,6 +33,16 @@ SIGNATURES = {
     "hypno_hip_q4_0_gemv_plan_launches": (_i, [_vp]),
     "hypno_hip_q4_0_gemv_plan_destroy": (_i, [_vp]),
     "hypno_hip_stream_synchronize": (_i, [_vp]),
+    "hypno_hip_model_open": (_i, [ctypes.c_char_p, _u32, ctypes.POINTER(_vp)]),
+    "hypno_hip_model_close": (_i, [_vp]),
+    "hypno_hip_model_header": (_i, [_vp, ctypes.POINTER(_u32), ctypes.POINTER(_u32),
+                                    ctypes.POINTER(_u32)]),
+    "hypno_hip_model_metadata_at": (_i, [_vp, _sz, ctypes.POINTER(ctypes.c_char_p),
+                                         ctypes.POINTER(ctypes.c_char_p)]),
+    "hypno_hip_model_metadata": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p)]),
+    "hypno_hip_model_tensor_at": (_i, [_vp, _sz, _vp]),
+    "hypno_hip_model_find_tensor": (_i, [_vp, ctypes.c_char_p, _vp]),
+    "hypno_hip_model_is_col_major": (_i, [_vp]),
 }
 
 
@@ -41,6 +51,17 @@ class GemvDesc(ctypes.Structure):
     _fields_ = [("y", ctypes.c_void_p), ("w_q", ctypes.c_void_p), ("w_len", ctypes.c_size_t),
                 ("x", ctypes.c_void_p), ("bias", ctypes.c_void_p), ("n", ctypes.c_size_t),
                 ("m", ctypes.c_size_t)]
+
+class TensorInfo(ctypes.Structure):
+    """struct hypno_hip_tensor_info of include/hypno_hip.h."""
+    _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_uint32), ("ndim", ctypes.c_uint32),
+                ("shape", ctypes.POINTER(ctypes.c_uint64)), ("offset", ctypes.c_uint64),
+                ("data_len", ctypes.c_uint64), ("host", ctypes.c_void_p),
+                ("device", ctypes.c_void_p)]
+
+
+MODEL_HOST_ONLY = 1  # HYPNO_HIP_MODEL_HOST_ONLY
+ENOENT, EFILE, EFORMAT = 2, 9, 74  # HYPNO_HIP_ENOENT / _EFILE / _EFORMAT
 
 _lib = None
 

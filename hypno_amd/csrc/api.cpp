@@ -295,6 +295,17 @@ int host_matmul(float* y, const uint8_t* w, size_t w_len, uint32_t dtype, const 
 
 }  // namespace
 
+namespace hypno {
+
+int set_last_error(int status, const std::string& msg) {
+  g_last_error = msg;
+  return status;
+}
+
+int hip_status(hipError_t e, const char* what) { return hip_fail(e, what); }
+
+}  // namespace hypno
+
 extern "C" {
 
 int hypno_hip_abi_version(void) { return HYPNO_HIP_ABI_VERSION; }
@@ -306,6 +317,9 @@ const char* hypno_hip_strerror(int status) {
     case HYPNO_HIP_ENOMEM: return "out of memory";
     case HYPNO_HIP_EDEVICE: return "device or HIP runtime error";
     case HYPNO_HIP_ENOTSUP: return "dtype not supported on this path";
+    case HYPNO_HIP_ENOENT: return "no such file, tensor or metadata key";
+    case HYPNO_HIP_EFILE: return "file could not be opened, mapped or read";
+    case HYPNO_HIP_EFORMAT: return "malformed .hypno file";
     default: return "unknown status";
   }
 }

@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <string>
+
 namespace hypno {
 
 // Native 4 x u32 vector: loads and stores of it are single instructions
@@ -227,5 +229,11 @@ size_t f16_gemm_v2_workspace_bytes(size_t batch, size_t n, size_t m, int num_cus
 hipError_t launch_f16_gemm_v2(float* y, const uint8_t* w, const float* x, const float* bias,
                               size_t n, size_t m, size_t batch, void* ws, int num_cus,
                               hipStream_t s);
+
+// Status reporting shared by the C ABI sources (api.cpp): record `msg` as the
+// calling thread's last error and return `status`; hip_status maps a HIP error
+// to ENOMEM / EDEVICE the same way.
+int set_last_error(int status, const std::string& msg);
+int hip_status(hipError_t e, const char* what);
 
 }  // namespace hypno

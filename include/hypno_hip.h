@@ -42,6 +42,9 @@ extern "C" {
 #define HYPNO_HIP_ENOMEM 12   /* device or pinned-host allocation failed */
 #define HYPNO_HIP_EDEVICE 5   /* HIP runtime / launch error, or no device */
 #define HYPNO_HIP_ENOTSUP 95  /* dtype outside this path (FP32, Q8_0) */
+#define HYPNO_HIP_ENOENT 2    /* no such file, tensor or metadata key */
+#define HYPNO_HIP_EFILE 9     /* a file could not be opened, mapped or read */
+#define HYPNO_HIP_EFORMAT 74  /* malformed .hypno file (format.rs:109-131) */
 
 /* Weight dtypes: hypno's DType codes (dtype.rs:4-15). */
 #define HYPNO_DTYPE_FP32 0u
@@ -167,6 +170,71 @@ int hypno_hip_q4_0_gemv_plan_destroy(hypno_hip_gemv_plan* plan);
 
 /* Block until all work this library queued on `stream` is done. */
 int hypno_hip_stream_synchronize(void* stream);
+
+/* ---------------------------------------------------------------------------
+ * .hypno model files (format.rs, loader.rs).  Replaces HypnoModel
+ * (loader.rs:20-169): the file is mapped read-only and its manifest parsed
+ * with the reference's checks and errors; unless HOST_ONLY is given, every
+ * tensor payload is then uploaded once to the current device, so decode and
+ * prefill calls take device pointers straight from the model.  Host pointers
+ * are the zero-copy mapping (what HypnoModel::get_tensor_data returns); the
+ * device copy keeps each tensor's in-file alignment (64 bytes for files
+ * written by hypno's converter).  Strings, shapes and both pointers stay
+ * valid until hypno_hip_model_close.
+ * Errors: ENOENT (file missing), EFILE (open / mmap / read failure),
+ * EFORMAT (one per FormatError variant: bad magic, version, short buffer,
+ * UTF-8, unknown dtype, tensor out of file bounds), ENOMEM / EDEVICE
+ * (upload).  A tensor name whose bytes run past the end of the file is
+ * EFORMAT here (the reference reads it unchecked, loader.rs:96-97).
+ * ------------------------------------------------------------------------- */
+typedef struct hypno_hip_model hypno_hip_model;
+
+typedef struct hypno_hip_tensor_info {
+  const char* name;       /* NUL-terminated UTF-8 */
+  uint32_t dtype;         /* HYPNO_DTYPE_* (dtype.rs:4-15) */
+  uint32_t ndim;
+  const uint64_t* shape;  /* [ndim] (NULL when ndim == 0) */
+  uint64_t offset;        /* absolute byte offset in the file */
+  uint64_t data_len;      /* payload bytes */
+  const uint8_t* host;    /* [data_len] in the read-only mapping */
+  const uint8_t* device;  /* [data_len] on the model's device; NULL if host-only
+                             or data_len == 0 */
+} hypno_hip_tensor_info;
+
+/* Parse and map only; no device is touched (tools, CPU-side checks). */
+#define HYPNO_HIP_MODEL_HOST_ONLY 1u
+
+/* HypnoModel::open (loader.rs:39-134), plus the upload to the current
+ * device (pinned, pipelined: file reads overlap the host-to-device copies). */
+int hypno_hip_model_open(const char* path, uint32_t flags, hypno_hip_model** model);
+
+/* Unmap the file and free the device copy. */
+int hypno_hip_model_close(hypno_hip_model* model);
+
+/* The header fields (format.rs:13-24); any pointer may be NULL. */
+int hypno_hip_model_header(const hypno_hip_model* model, uint32_t* version,
+                           uint32_t* metadata_kv_count, uint32_t* tensor_count);
+
+/* Metadata entry i in file order (HypnoManifest::metadata). */
+int hypno_hip_model_metadata_at(const hypno_hip_model* model, size_t i, const char** key,
+                                const char** value);
+
+/* HypnoModel::get_metadata (loader.rs:158-163): first entry with this key;
+ * ENOENT if none. */
+int hypno_hip_model_metadata(const hypno_hip_model* model, const char* key, const char** value);
+
+/* Tensor i in file order (HypnoManifest::tensors). */
+int hypno_hip_model_tensor_at(const hypno_hip_model* model, size_t i,
+                              hypno_hip_tensor_info* info);
+
+/* HypnoModel::find_tensor / get_tensor_data (loader.rs:139-156): first tensor
+ * with this name; ENOENT if none. */
+int hypno_hip_model_find_tensor(const hypno_hip_model* model, const char* name,
+                                hypno_hip_tensor_info* info);
+
+/* HypnoModel::is_col_major (loader.rs:166-168): 1 if metadata
+ * "weight_layout" is "col_major", else 0 (also for a NULL model). */
+int hypno_hip_model_is_col_major(const hypno_hip_model* model);
 
 #ifdef __cplusplus
 }
