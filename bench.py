@@ -190,6 +190,52 @@ def decode_stream(torch, lib, steps, warmup, value_only=False):
     del g_grp, g_call
     res.update({"ms_grouped": ms_grp, "launches_grouped": sum(p.launches for p in groups),
                 "ms_per_call": ms_call, "launches_per_call": len(calls)})
+    # (d) the same groups with the steps either side of the GEMVs: RMS norm
+    # before [q,k,v] and [gate,up], silu(gate)*up before [down] — fused into
+    # the GEMVs' staging, against the same work as separate kernels
+    eps = 1e-5
+    norms = [(1.0 + 0.1 * torch.randn(2048, generator=gen, device="cuda"),
+              1.0 + 0.1 * torch.randn(2048, generator=gen, device="cuda")) for _ in range(LAYERS)]
+    ups = [torch.randn(5632, generator=gen, device="cuda") for _ in range(LAYERS)]
+    fused = []
+    for layer in range(LAYERS):
+        lj = {nm: (y, w, x, n, m) for lyr, nm, y, w, x, n, m in jobs if lyr == layer}
+        n1, n2 = norms[layer]
+
+        def j(nm, pro):
+            y, w, x, n, m = lj[nm]
+            return (y, w, x, None, n, m, pro)
+        fused += [hk.GemvPlan([j(nm, ("rms_norm", n1, eps)) for nm in ("q", "k", "v")]),
+                  hk.GemvPlan([j("o", None)]),
+                  hk.GemvPlan([j(nm, ("rms_norm", n2, eps)) for nm in ("gate", "up")]),
+                  hk.GemvPlan([j("down", ("silu_mul", ups[layer]))])]
+
+    def run_fused():
+        for p in fused:
+            p.run()
+
+    ms_fused, g_f = time_graph(torch, run_fused, steps, warmup)
+    # separate kernels write the GEMVs' inputs from the residual stream and
+    # the gate vector, as the reference's in-place norm and silu do
+    hidden = torch.randn(2048, generator=gen, device="cuda")
+    gate_v = torch.randn(5632, generator=gen, device="cuda")
+
+    def run_separate():
+        for layer in range(LAYERS):
+            x = xs[layer]
+            hk.rms_norm(hidden, norms[layer][0], eps, out=x["attn"])
+            groups[4 * layer].run()
+            groups[4 * layer + 1].run()
+            hk.rms_norm(hidden, norms[layer][1], eps, out=x["mlp"])
+            groups[4 * layer + 2].run()
+            hk.silu_mul(gate_v, ups[layer], out=x["down"])
+            groups[4 * layer + 3].run()
+
+    ms_sep, g_s = time_graph(torch, run_separate, steps, warmup)
+    del g_f, g_s
+    res.update({"ms_fused": ms_fused, "launches_fused": sum(p.launches for p in fused),
+                "ms_separate": ms_sep,
+                "launches_separate": sum(p.launches for p in groups) + 3 * LAYERS})
     return res
 
 
@@ -563,6 +609,13 @@ def main():
             "launches": d["launches_grouped"],
             "ms_per_step": round(d["ms_grouped"], 5),
             "gbs": round(d["weight_bytes"] / (d["ms_grouped"] * 1e-3) / 1e9, 2)}
+        config["decode_step_fused"] = {
+            "desc": "the grouped decode step with RMS norm before [q,k,v] and [gate,up] and "
+                    "silu(gate)*up before [down] applied inside the GEMVs' activation staging",
+            "launches": d["launches_fused"],
+            "ms_per_step": round(d["ms_fused"], 5),
+            "vs_separate_kernels_ms": round(d["ms_separate"], 5),
+            "separate_launches": d["launches_separate"]}
         config["per_call"] = {
             "desc": "drop-in path: one hypno_hip_matmul_q4_0_dev call per matrix, "
                     "replayed as one HIP graph",

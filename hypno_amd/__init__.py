@@ -18,6 +18,9 @@ from .kernels import (  # noqa: F401
     matmul_vec_q4_0,
     quantize_f32_to_q4_0,
     register_weight,
+    rms_norm,
+    rms_norm_in_place,
+    silu_mul,
     unregister_weight,
 )
 

@@ -32,6 +32,9 @@ SIGNATURES = {
     "hypno_hip_q4_0_gemv_plan_run": (_i, [_vp, _vp]),
     "hypno_hip_q4_0_gemv_plan_launches": (_i, [_vp]),
     "hypno_hip_q4_0_gemv_plan_destroy": (_i, [_vp]),
+    "hypno_hip_q4_0_gemv_plan_create_ex": (_i, [_vp, _vp, _sz, _vp]),
+    "hypno_hip_rms_norm_dev": (_i, [_vp, _vp, _vp, _sz, _sz, ctypes.c_float, _vp]),
+    "hypno_hip_silu_mul_dev": (_i, [_vp, _vp, _vp, _sz, _vp]),
     "hypno_hip_stream_synchronize": (_i, [_vp]),
     "hypno_hip_model_open": (_i, [ctypes.c_char_p, _u32, ctypes.POINTER(_vp)]),
     "hypno_hip_model_close": (_i, [_vp]),
@@ -51,6 +54,14 @@ class GemvDesc(ctypes.Structure):
     _fields_ = [("y", ctypes.c_void_p), ("w_q", ctypes.c_void_p), ("w_len", ctypes.c_size_t),
                 ("x", ctypes.c_void_p), ("bias", ctypes.c_void_p), ("n", ctypes.c_size_t),
                 ("m", ctypes.c_size_t)]
+
+class GemvPrologue(ctypes.Structure):
+    """struct hypno_hip_gemv_prologue of include/hypno_hip.h."""
+    _fields_ = [("kind", ctypes.c_uint32), ("aux", ctypes.c_void_p), ("eps", ctypes.c_float)]
+
+
+PROLOGUE_NONE, PROLOGUE_RMS_NORM, PROLOGUE_SILU_MUL = 0, 1, 2
+
 
 class TensorInfo(ctypes.Structure):
     """struct hypno_hip_tensor_info of include/hypno_hip.h."""

@@ -429,10 +429,17 @@ struct hypno_hip_gemv_plan {
     int njobs = 0;
     int total_steps = 0;
   };
+  // A job the streaming kernel cannot take: the any-shape kernel, after a
+  // stand-alone prologue into `staged` when the job has one.
+  struct Generic {
+    hypno_hip_gemv_desc d;
+    hypno_hip_gemv_prologue pro;
+    float* staged = nullptr;  // [m], plan-owned
+  };
   int device = 0;
   int cus = 256;
   std::vector<Group> groups;
-  std::vector<hypno_hip_gemv_desc> generic;  // run by the any-shape kernel
+  std::vector<Generic> generic;
 };
 
 namespace {
@@ -469,6 +476,8 @@ int close_group(hypno_hip_gemv_plan* pl, hypno_hip_gemv_plan::Group& grp,
 void free_plan(hypno_hip_gemv_plan* pl) {
   for (auto& g : pl->groups)
     if (g.d_jobs) (void)hipFree(g.d_jobs);
+  for (auto& g : pl->generic)
+    if (g.staged) (void)hipFree(g.staged);
   delete pl;
 }
 
@@ -478,6 +487,12 @@ extern "C" {
 
 int hypno_hip_q4_0_gemv_plan_create(const hypno_hip_gemv_desc* descs, size_t count,
                                     hypno_hip_gemv_plan** plan) {
+  return hypno_hip_q4_0_gemv_plan_create_ex(descs, nullptr, count, plan);
+}
+
+int hypno_hip_q4_0_gemv_plan_create_ex(const hypno_hip_gemv_desc* descs,
+                                       const hypno_hip_gemv_prologue* prologues, size_t count,
+                                       hypno_hip_gemv_plan** plan) {
   if (!plan) return fail(HYPNO_HIP_EINVAL, "plan_create: NULL plan pointer");
   *plan = nullptr;
   if (!descs && count) return fail(HYPNO_HIP_EINVAL, "plan_create: NULL descriptors");
@@ -505,8 +520,31 @@ int hypno_hip_q4_0_gemv_plan_create(const hypno_hip_gemv_desc* descs, size_t cou
       free_plan(pl);
       return fail(HYPNO_HIP_EINVAL, "plan_create: descriptor %zu shape overflows", i);
     }
-    if (!(q4_0_gemv_fast_ok(d.w_q, d.w_len, d.n, d.m) && aligned16(d.x))) {
-      pl->generic.push_back(d);
+    hypno_hip_gemv_prologue pro = {HYPNO_HIP_PROLOGUE_NONE, nullptr, 0.0f};
+    if (prologues) pro = prologues[i];
+    if (pro.kind > HYPNO_HIP_PROLOGUE_SILU_MUL) {
+      free_plan(pl);
+      return fail(HYPNO_HIP_EINVAL, "plan_create: descriptor %zu has unknown prologue %u", i,
+                  pro.kind);
+    }
+    if (pro.kind != HYPNO_HIP_PROLOGUE_NONE && (!pro.aux || d.m == 0)) {
+      free_plan(pl);
+      return fail(HYPNO_HIP_EINVAL, "plan_create: descriptor %zu: prologue needs aux and m > 0",
+                  i);
+    }
+    if (!(q4_0_gemv_fast_ok(d.w_q, d.w_len, d.n, d.m) && aligned16(d.x) &&
+          (pro.kind == HYPNO_HIP_PROLOGUE_NONE || aligned16(pro.aux)))) {
+      hypno_hip_gemv_plan::Generic gj;
+      gj.d = d;
+      gj.pro = pro;
+      if (pro.kind != HYPNO_HIP_PROLOGUE_NONE) {
+        hipError_t e = hipMalloc(&gj.staged, d.m * sizeof(float));
+        if (e != hipSuccess) {
+          free_plan(pl);
+          return hip_fail(e, "plan_create: prologue staging");
+        }
+      }
+      pl->generic.push_back(gj);
       continue;
     }
     if (!gemv_group_add(grp.geom, d.m)) {
@@ -517,11 +555,15 @@ int hypno_hip_q4_0_gemv_plan_create(const hypno_hip_gemv_desc* descs, size_t cou
       }
       gemv_group_add(grp.geom, d.m);
     }
+    if (pro.kind != HYPNO_HIP_PROLOGUE_NONE) grp.geom.pro = 1;
     GemvJob j;
     j.w = d.w_q;
     j.x = d.x;
     j.y = d.y;
     j.bias = d.bias;
+    j.aux = pro.aux;
+    j.pro = (int)pro.kind;
+    j.eps = pro.eps;
     j.n = (int)d.n;
     j.B = (int)(d.m / 32);
     j.rps = 0;
@@ -545,8 +587,17 @@ int hypno_hip_q4_0_gemv_plan_run(const hypno_hip_gemv_plan* plan, void* stream) 
                                           plan->cus, s);
     if (e != hipSuccess) return hip_fail(e, "plan_run: GEMV launch");
   }
-  for (const auto& d : plan->generic) {
-    hipError_t e = launch_q4_0_generic(d.y, d.w_q, d.w_len, d.x, d.bias, d.n, d.m, 1, s);
+  for (const auto& g : plan->generic) {
+    const hypno_hip_gemv_desc& d = g.d;
+    const float* x = d.x;
+    hipError_t e = hipSuccess;
+    if (g.pro.kind == HYPNO_HIP_PROLOGUE_RMS_NORM)
+      e = launch_rms_norm(g.staged, d.x, g.pro.aux, d.m, 1, g.pro.eps, s);
+    else if (g.pro.kind == HYPNO_HIP_PROLOGUE_SILU_MUL)
+      e = launch_silu_mul(g.staged, d.x, g.pro.aux, d.m, s);
+    if (e != hipSuccess) return hip_fail(e, "plan_run: prologue launch");
+    if (g.staged) x = g.staged;
+    e = launch_q4_0_generic(d.y, d.w_q, d.w_len, x, d.bias, d.n, d.m, 1, s);
     if (e != hipSuccess) return hip_fail(e, "plan_run: generic launch");
   }
   return HYPNO_HIP_OK;
@@ -554,13 +605,35 @@ int hypno_hip_q4_0_gemv_plan_run(const hypno_hip_gemv_plan* plan, void* stream) 
 
 int hypno_hip_q4_0_gemv_plan_launches(const hypno_hip_gemv_plan* plan) {
   if (!plan) return 0;
-  return (int)(plan->groups.size() + plan->generic.size());
+  int n = (int)(plan->groups.size() + plan->generic.size());
+  for (const auto& g : plan->generic) n += g.staged ? 1 : 0;
+  return n;
 }
 
 int hypno_hip_q4_0_gemv_plan_destroy(hypno_hip_gemv_plan* plan) {
   if (!plan) return HYPNO_HIP_OK;
   (void)hipDeviceSynchronize();
   free_plan(plan);
+  return HYPNO_HIP_OK;
+}
+
+int hypno_hip_rms_norm_dev(float* out, const float* x, const float* weight, size_t n,
+                           size_t rows, float eps, void* stream) {
+  if (n == 0 || rows == 0) return HYPNO_HIP_OK;
+  if (!out || !x || !weight) return fail(HYPNO_HIP_EINVAL, "rms_norm: NULL pointer");
+  if (mul_overflows(n, rows) || rows > 0x7FFFFFFF)
+    return fail(HYPNO_HIP_EINVAL, "rms_norm: shape overflows");
+  hipError_t e = launch_rms_norm(out, x, weight, n, rows, eps, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "rms_norm launch");
+  return HYPNO_HIP_OK;
+}
+
+int hypno_hip_silu_mul_dev(float* out, const float* gate, const float* up, size_t n,
+                           void* stream) {
+  if (n == 0) return HYPNO_HIP_OK;
+  if (!out || !gate || !up) return fail(HYPNO_HIP_EINVAL, "silu_mul: NULL pointer");
+  hipError_t e = launch_silu_mul(out, gate, up, n, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "silu_mul launch");
   return HYPNO_HIP_OK;
 }
 

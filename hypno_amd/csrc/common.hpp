@@ -148,16 +148,25 @@ bool q4_0_gemv_fast_ok(const uint8_t* w, size_t w_len, size_t n, size_t m);
 hipError_t launch_q4_0_gemv_fast(float* y, const uint8_t* w, const float* x, const float* bias,
                                  size_t n, size_t m, int num_cus, hipStream_t s);
 
+// Step applied to a job's input vector while it is staged (values of
+// HYPNO_HIP_PROLOGUE_* in include/hypno_hip.h).
+constexpr int kProNone = 0;
+constexpr int kProRmsNorm = 1;  // x * (1 / sqrt(mean(x^2) + eps)) * aux
+constexpr int kProSiluMul = 2;  // x / (1 + exp(-x)) * aux
+
 // One GEMV of a multi-job launch (device-side descriptor).
 struct GemvJob {
   const uint8_t* w;
   const float* x;
   float* y;
   const float* bias;
+  const float* aux;  // prologue operand (norm weight or up), [m]
   int n;      // rows
   int B;      // blocks per row = m / 32
   int rps;    // rows per step = T / B
   int step0;  // first global step of this job
+  int pro;    // kPro*
+  float eps;  // kProRmsNorm
 };
 
 // Work-group shape shared by the jobs of one launch.
@@ -167,6 +176,7 @@ struct GemvGroupGeom {
   int W = 0;     // waves
   int S = 0;     // steps per partial-sum chunk
   int maxB = 0;  // largest B (activation staging size)
+  int pro = 0;   // some job stages a prologue operand too
   size_t lds = 0;
 };
 
@@ -229,6 +239,13 @@ size_t f16_gemm_v2_workspace_bytes(size_t batch, size_t n, size_t m, int num_cus
 hipError_t launch_f16_gemm_v2(float* y, const uint8_t* w, const float* x, const float* bias,
                               size_t n, size_t m, size_t batch, void* ws, int num_cus,
                               hipStream_t s);
+
+// Decode-step neighbours of the GEMV (prologue.hip).  rms_norm: `rows` rows
+// of n, out may alias x; silu_mul: n elements, out may alias gate.
+hipError_t launch_rms_norm(float* out, const float* x, const float* weight, size_t n,
+                           size_t rows, float eps, hipStream_t s);
+hipError_t launch_silu_mul(float* out, const float* gate, const float* up, size_t n,
+                           hipStream_t s);
 
 // Status reporting shared by the C ABI sources (api.cpp): record `msg` as the
 // calling thread's last error and return `status`; hip_status maps a HIP error

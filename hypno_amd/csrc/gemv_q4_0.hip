@@ -130,7 +130,8 @@ static void finish_geometry(GemvGroupGeom& g) {
   g.W = g.T / 64;
   g.S = 64;
   const size_t loop = (size_t)g.S * (g.T / 8) * 4;  // 8-lane group partials
-  const size_t xs = (size_t)g.maxB * (16 * kLimbs + 4);  // activation limbs, exponents
+  // activation limbs and exponents, then one float per wave (prologue sums)
+  const size_t xs = (size_t)g.maxB * (16 * kLimbs + 4) + 4 * (size_t)g.W;
   g.lds = xs > loop ? xs : loop;
 }
 
@@ -318,7 +319,11 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
   // (cooperatively: thread i handles elements [8i, 8i+8) of x, four threads
   // per block), park them in LDS as [limb][block][4 dwords] plus one
   // exponent per block, and keep this lane's block column in registers.
-  auto enter = [&](int j, int g) {
+  // A prologue first turns x into rms_norm(x) or silu(x) * up, element by
+  // element in registers (the RMS sum: per-thread FMA chains, wave sums, then
+  // the waves' sums in a fixed order, so every work-group gets the same
+  // scale).
+  auto enter = [&](int j, int g) __attribute__((always_inline)) {
     J = get(j);
     cj = j;
     const int steps = job_steps(J);
@@ -330,10 +335,42 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
     uint32_t* limbs = reinterpret_cast<uint32_t*>(smem);
     int* exps = reinterpret_cast<int*>(smem + (size_t)kLimbs * 16 * B);
     const float4* xv = reinterpret_cast<const float4*>(J.x);
-    for (int i = t; i < B * 4; i += T) {  // whole 4-thread groups stay together
-      const float4 v0 = load_global<float4>(xv + 2 * i);
-      const float4 v1 = load_global<float4>(xv + 2 * i + 1);
-      const float xs[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    const float4* av = reinterpret_cast<const float4*>(J.aux);
+    auto load8 = [&](const float4* p, int i, float* o) __attribute__((always_inline)) {
+      const float4 v0 = load_global<float4>(p + 2 * i);
+      const float4 v1 = load_global<float4>(p + 2 * i + 1);
+      o[0] = v0.x; o[1] = v0.y; o[2] = v0.z; o[3] = v0.w;
+      o[4] = v1.x; o[5] = v1.y; o[6] = v1.z; o[7] = v1.w;
+    };
+    auto sumsq8 = [&](const float* xs, float ss) __attribute__((always_inline)) {
+#pragma unroll
+      for (int k = 0; k < 8; k++) ss = fmaf(xs[k], xs[k], ss);
+      return ss;
+    };
+    // Sum of the work-group's partial sums in a fixed order; the last
+    // barrier also orders the limb writes below after every wsum read.
+    auto inv_rms_of = [&](float ss) __attribute__((always_inline)) {
+      float* wsum = reinterpret_cast<float*>(exps + B);
+      ss = wave_sum(ss);
+      if ((t & 63) == 0) wsum[t >> 6] = ss;
+      __syncthreads();
+      float tot = 0.0f;
+      for (int w = 0; w < (T >> 6); w++) tot += wsum[w];
+      return 1.0f / sqrtf(tot / (float)(B * 32) + J.eps);
+    };
+    auto prologue = [&](float* xs, const float* as, float inv_rms) __attribute__((always_inline)) {
+      if (J.pro == kProRmsNorm) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) xs[k] = xs[k] * inv_rms * as[k];
+      } else if (J.pro == kProSiluMul) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) xs[k] = xs[k] / (1.0f + expf(-xs[k])) * as[k];
+      }
+    };
+    // Group i (elements [8i, 8i+8)) -> i4 limbs and, for the block's first
+    // group, the block exponent.  The four groups of a block are consecutive
+    // lanes, all active together.
+    auto convert = [&](int i, const float* xs) __attribute__((always_inline)) {
       // Largest |x| of the block by its bit pattern (ordered like the value
       // for non-negative floats; inf and NaN compare above every finite).
       uint32_t mb = 0;
@@ -354,6 +391,40 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
         limbs[(l * B * 4) + i] = w ^ 0x88888888u;
       }
       if ((i & 3) == 0) exps[i >> 2] = mb >= 0x7F800000u ? kBadExp : e - kMantBits;
+    };
+    if (B * 4 <= T) {
+      // One group per thread at most: x and the prologue operand are read
+      // once and stay in registers across the RMS reduction.
+      const bool act = t < B * 4;
+      float xs[8] = {}, as[8] = {};
+      if (act) {
+        load8(xv, t, xs);
+        if (J.pro != kProNone) load8(av, t, as);
+      }
+      float inv_rms = 1.0f;
+      if (J.pro == kProRmsNorm) inv_rms = inv_rms_of(sumsq8(xs, 0.0f));
+      if (act) {
+        prologue(xs, as, inv_rms);
+        convert(t, xs);
+      }
+    } else {
+      float inv_rms = 1.0f;
+      if (J.pro == kProRmsNorm) {
+        float ss = 0.0f;
+        for (int i = t; i < B * 4; i += T) {
+          float xs[8];
+          load8(xv, i, xs);
+          ss = sumsq8(xs, ss);
+        }
+        inv_rms = inv_rms_of(ss);
+      }
+      for (int i = t; i < B * 4; i += T) {  // whole 4-thread groups stay together
+        float xs[8], as[8];
+        load8(xv, i, xs);
+        if (J.pro != kProNone) load8(av, i, as);
+        prologue(xs, as, inv_rms);
+        convert(i, xs);
+      }
     }
     __syncthreads();
     const int kb = t % B;
@@ -438,13 +509,18 @@ hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
       per_cu < 1)
     per_cu = 1;
   int grid = total_steps < num_cus * per_cu ? total_steps : num_cus * per_cu;
-  // A single matrix: every work-group stages all of x (4K bytes) before its
-  // first step, so each one should stream at least about twice that in
-  // weights (14 rows x K/32 x 18 B >= 8K B): about n/14 work-groups, rounded
-  // to a whole number per CU (a partial round leaves most CUs idle while a
-  // few run a second work-group), at least one per CU.
-  if (njobs == 1) {
-    const int per = (job0.n / 14 + num_cus / 2) / num_cus;
+  // Every work-group stages a job's whole x (4K bytes, and as much again for
+  // a prologue operand) before streaming its rows, so each one should stream
+  // at least about twice that in weights: for one matrix about n/14
+  // work-groups.  Rounded to a whole number per CU (a partial round leaves
+  // most CUs idle while a few run a second work-group), at least one per CU.
+  // Measured on a TinyLlama decode step (88 small launches): 577 -> 543 us,
+  // 669 -> 614 us with fused norms; 1x or 4x the staging bytes do worse.
+  {
+    const long long wbytes = (long long)total_steps * g.T * kBlockBytes;
+    const long long stage = 4LL * kBlockElems * g.maxB * (g.pro ? 2 : 1);
+    const long long ws = wbytes / (2 * stage);
+    const int per = (int)((ws + num_cus / 2) / num_cus);
     const int cap = (per > 1 ? per : 1) * num_cus;
     if (grid > cap) grid = cap;
   }
@@ -467,6 +543,9 @@ hipError_t launch_q4_0_gemv_fast(float* y, const uint8_t* w, const float* x, con
   J.x = x;
   J.y = y;
   J.bias = bias;
+  J.aux = nullptr;
+  J.pro = kProNone;
+  J.eps = 0.0f;
   J.n = (int)n;
   J.B = (int)(m / 32);
   J.rps = g.T / J.B;

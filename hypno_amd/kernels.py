@@ -31,6 +31,7 @@ __all__ = [
     "DType", "HypnoHipError", "matmul_q4_0", "matmul_f16", "matmul_vec_q4_0",
     "matmul_vec_f16", "matmul_vec_auto", "batch_matmul", "quantize_f32_to_q4_0",
     "dequantize_q4_0", "register_weight", "unregister_weight", "device_count", "GemvPlan",
+    "rms_norm", "rms_norm_in_place", "silu_mul",
 ]
 
 
@@ -225,16 +226,38 @@ class GemvPlan:
     """Several independent Q4_0 GEMVs (one token each) run as one launch.
 
     `jobs` is a sequence of (y, w_q, x, bias, n, m) with GPU tensors, each with
-    the meaning of matmul_q4_0's arguments.  The plan keeps the tensors'
-    addresses: refill the x tensors in place and call run() again."""
+    the meaning of matmul_q4_0's arguments, optionally followed by a prologue
+    applied to x as the GEMV stages it: ("rms_norm", norm_weight, eps)
+    (ops::rms_norm, kernels.rs:592-625) or ("silu_mul", up) (silu(x) * up,
+    transformer.rs:446-449); x itself is left unchanged.  The plan keeps the
+    tensors' addresses: refill the x tensors in place and call run() again."""
 
     def __init__(self, jobs):
-        from ._lib import GemvDesc
+        from ._lib import (PROLOGUE_NONE, PROLOGUE_RMS_NORM, PROLOGUE_SILU_MUL, GemvDesc,
+                           GemvPrologue)
         lib = load()
         self._keep = []
         descs = (GemvDesc * len(jobs))()
-        for i, (y, w, x, bias, n, m) in enumerate(jobs):
+        pros = (GemvPrologue * len(jobs))()
+        any_pro = False
+        for i, job in enumerate(jobs):
+            y, w, x, bias, n, m = job[:6]
+            pro = job[6] if len(job) > 6 else None
             _check_lengths(y, x, bias, n, m, 1)
+            pros[i].kind = PROLOGUE_NONE
+            if pro is not None:
+                kind, aux = pro[0], pro[1]
+                if _numel(aux) < m:
+                    raise ValueError(f"prologue operand has {_numel(aux)} elements, expected {m}")
+                pros[i].aux = _dev_ptr(aux, "f32", "prologue operand").value
+                if kind == "rms_norm":
+                    pros[i].kind, pros[i].eps = PROLOGUE_RMS_NORM, float(pro[2])
+                elif kind == "silu_mul":
+                    pros[i].kind = PROLOGUE_SILU_MUL
+                else:
+                    raise ValueError(f"unknown prologue {kind!r}")
+                self._keep.append(aux)
+                any_pro = True
             descs[i].y = _dev_ptr(y, "f32", "y").value
             descs[i].w_q = _dev_ptr(w, "u8", "w_q").value
             descs[i].w_len = _nbytes(w)
@@ -244,7 +267,8 @@ class GemvPlan:
             descs[i].m = m
             self._keep.append((y, w, x, bias))
         self._plan = ctypes.c_void_p()
-        check(lib.hypno_hip_q4_0_gemv_plan_create(descs, len(jobs), ctypes.byref(self._plan)),
+        check(lib.hypno_hip_q4_0_gemv_plan_create_ex(descs, pros if any_pro else None, len(jobs),
+                                                     ctypes.byref(self._plan)),
               "gemv_plan_create")
         self.device = self._keep[0][0].device if self._keep else None
 
@@ -267,6 +291,48 @@ class GemvPlan:
             self.close()
         except Exception:
             pass
+
+
+# --- the decode step's neighbours of the GEMV (device tensors) -----------------------
+
+def rms_norm(x, weight, eps: float, rows: int = 1, out=None):
+    """ops::rms_norm (ops.rs:52-55 -> kernels.rs:592-625) over `rows` rows of
+    x (GPU float32), into `out` (a new tensor by default)."""
+    if out is None:
+        out = _torch().empty_like(x)
+    elif _numel(out) != _numel(x):
+        raise ValueError("out and x differ in size")
+    _rms_norm(out, x, weight, eps, rows)
+    return out
+
+
+def rms_norm_in_place(x, weight, eps: float, rows: int = 1) -> None:
+    """ops::rms_norm_in_place (ops.rs:59-61)."""
+    _rms_norm(x, x, weight, eps, rows)
+
+
+def _rms_norm(out, x, weight, eps, rows):
+    n = _numel(x) // rows if rows else 0
+    if rows and n * rows != _numel(x):
+        raise ValueError("x does not split into `rows` equal rows")
+    if _numel(weight) < n:
+        raise ValueError(f"weight has {_numel(weight)} elements, expected {n}")
+    check(load().hypno_hip_rms_norm_dev(_dev_ptr(out, "f32", "out"), _dev_ptr(x, "f32", "x"),
+                                        _dev_ptr(weight, "f32", "weight"), n, rows,
+                                        ctypes.c_float(eps), _stream(x.device)), "rms_norm")
+
+
+def silu_mul(gate, up, out=None):
+    """silu_in_place(gate); gate *= up (ops.rs:81-83, transformer.rs:446-449)
+    as out = silu(gate) * up (out=gate for the in-place form)."""
+    if _numel(up) < _numel(gate):
+        raise ValueError("up is shorter than gate")
+    if out is None:
+        out = _torch().empty_like(gate)
+    check(load().hypno_hip_silu_mul_dev(_dev_ptr(out, "f32", "out"), _dev_ptr(gate, "f32", "gate"),
+                                        _dev_ptr(up, "f32", "up"), _numel(gate),
+                                        _stream(gate.device)), "silu_mul")
+    return out
 
 
 # --- weight residency for the host-slice path -------------------------------------

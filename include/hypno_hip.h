@@ -159,6 +159,32 @@ typedef struct hypno_hip_gemv_plan hypno_hip_gemv_plan;
 int hypno_hip_q4_0_gemv_plan_create(const hypno_hip_gemv_desc* descs, size_t count,
                                     hypno_hip_gemv_plan** plan);
 
+/* Steps either side of the decode GEMV, applied to a plan job's input while
+ * the GEMV stages it (no extra pass over HBM, no extra launch), or as
+ * stand-alone device calls:
+ *   RMS_NORM  x' = rms_norm_fused(x, aux, eps) (kernels.rs:592-625;
+ *             transformer.rs:301,435 before q/k/v and gate/up)
+ *   SILU_MUL  x' = silu(x) * aux, silu(v) = v / (1 + exp(-v))
+ *             (transformer.rs:446-449, turbo.rs:235-237 before down)
+ * aux is a device vector of m floats (the norm weight, or the up
+ * projection's output).  x itself is not modified. */
+#define HYPNO_HIP_PROLOGUE_NONE 0u
+#define HYPNO_HIP_PROLOGUE_RMS_NORM 1u
+#define HYPNO_HIP_PROLOGUE_SILU_MUL 2u
+
+typedef struct hypno_hip_gemv_prologue {
+  uint32_t kind;     /* HYPNO_HIP_PROLOGUE_* */
+  const float* aux;  /* [m] device; NULL for NONE */
+  float eps;         /* RMS_NORM: rms_norm_eps (transformer.rs:59) */
+} hypno_hip_gemv_prologue;
+
+/* plan_create with one prologue per descriptor (prologues may be NULL: none).
+ * Jobs the streaming kernel cannot take run the prologue as a separate
+ * kernel into a plan-owned buffer, then the generic GEMV. */
+int hypno_hip_q4_0_gemv_plan_create_ex(const hypno_hip_gemv_desc* descs,
+                                       const hypno_hip_gemv_prologue* prologues, size_t count,
+                                       hypno_hip_gemv_plan** plan);
+
 /* Run every GEMV of the plan on `stream` (usually one kernel launch). */
 int hypno_hip_q4_0_gemv_plan_run(const hypno_hip_gemv_plan* plan, void* stream);
 
@@ -167,6 +193,17 @@ int hypno_hip_q4_0_gemv_plan_launches(const hypno_hip_gemv_plan* plan);
 
 /* Free the plan (waits for the device first). */
 int hypno_hip_q4_0_gemv_plan_destroy(hypno_hip_gemv_plan* plan);
+
+/* ops::rms_norm / rms_norm_in_place (ops.rs:52-61 -> kernels.rs:592-625) on
+ * `rows` consecutive rows of n floats: out[r] = x[r] * inv_rms(x[r]) * weight.
+ * out may equal x.  Device pointers. */
+int hypno_hip_rms_norm_dev(float* out, const float* x, const float* weight, size_t n,
+                           size_t rows, float eps, void* stream);
+
+/* silu_in_place(gate) then gate *= up (transformer.rs:446-449): out[i] =
+ * silu(gate[i]) * up[i] over n floats; out may equal gate.  Device pointers. */
+int hypno_hip_silu_mul_dev(float* out, const float* gate, const float* up, size_t n,
+                           void* stream);
 
 /* Block until all work this library queued on `stream` is done. */
 int hypno_hip_stream_synchronize(void* stream);

@@ -44,6 +44,15 @@ def lib():
     L.orc_quantize_q4_0.restype = sz
     L.orc_dequantize_q4_0.argtypes = [vp, sz, vp]
     L.orc_dequantize_q4_0.restype = sz
+    for name in ("orc_rms_norm_avx2", "orc_rms_norm_scalar"):
+        getattr(L, name).argtypes = [vp, vp, sz, fp]
+        getattr(L, name).restype = None
+    L.orc_rms_norm.argtypes = [vp, vp, sz, sz, fp]
+    L.orc_rms_norm.restype = None
+    L.orc_batch_rms_norm.argtypes = [vp, vp, vp, sz, sz, fp]
+    L.orc_batch_rms_norm.restype = None
+    L.orc_silu_mul.argtypes = [vp, vp, vp, sz]
+    L.orc_silu_mul.restype = None
     for name in ("orc_matmul_q4_0", "orc_matmul_q4_0_scalar", "orc_matmul_q4_0_avx2",
                  "orc_matmul_f16", "orc_matmul_f16_scalar", "orc_matmul_f16_avx2"):
         getattr(L, name).argtypes = [vp, vp, sz, vp, vp, sz, sz]
@@ -234,3 +243,40 @@ def rel_l2(y, ref) -> float:
     ref = np.asarray(ref, np.float64)
     den = np.linalg.norm(ref)
     return float(np.linalg.norm(y - ref) / den) if den > 0 else float(np.linalg.norm(y - ref))
+
+
+def rms_norm(x, weight, eps, rows=1) -> np.ndarray:
+    """ops::rms_norm (ops.rs:52-55 -> kernels.rs:592-625) on `rows` rows; returns a copy."""
+    y = _c(x, np.float32).ravel().copy()
+    w = _c(weight, np.float32)
+    n = y.size // rows
+    lib().orc_rms_norm(_p(y), _p(w), n, rows, eps)
+    return y
+
+
+def rms_norm_variant(x, weight, eps, kind) -> np.ndarray:
+    """One branch of rms_norm_fused: kind "avx2" (kernels.rs:599-619) or
+    "scalar" (kernels.rs:621-624); one row."""
+    y = _c(x, np.float32).ravel().copy()
+    w = _c(weight, np.float32)
+    fn = lib().orc_rms_norm_avx2 if kind == "avx2" else lib().orc_rms_norm_scalar
+    fn(_p(y), _p(w), y.size, eps)
+    return y
+
+
+def batch_rms_norm(x, weight, dim, batch, eps) -> np.ndarray:
+    """turbo::batch_rms_norm (turbo.rs:288-303), the f64-accumulating form."""
+    a = _c(x, np.float32).ravel()
+    w = _c(weight, np.float32)
+    out = np.empty(dim * batch, np.float32)
+    lib().orc_batch_rms_norm(_p(out), _p(a), _p(w), dim, batch, eps)
+    return out
+
+
+def silu_mul(gate, up) -> np.ndarray:
+    """silu_in_place(gate); gate *= up (ops.rs:81-83, transformer.rs:446-449)."""
+    g = _c(gate, np.float32).ravel()
+    u = _c(up, np.float32).ravel()
+    out = np.empty(g.size, np.float32)
+    lib().orc_silu_mul(_p(out), _p(g), _p(u), g.size)
+    return out

@@ -26,6 +26,12 @@
  *                       running hypno could pin them)
  *   orc_matmul_f16_*    fp64 brute force; exact integer KAT (ops.rs:114-121)
  *   orc_batch_matmul    per-token equality with the GEMV; turbo.rs KATs
+ *   orc_rms_norm_*      reference KATs ops.rs:131-136, turbo.rs:716-735 (the
+ *                       f64 batch_rms_norm within 1e-6 of the SIMD form),
+ *                       turbo.rs:924-951; closed forms (constant rows, the
+ *                       n % 8 tail's divide form) and an fp64 brute force
+ *   orc_silu_mul        reference KAT turbo.rs:979-990; silu(v) - silu(-v) = v
+ *                       and fp64 closed form
  *
  * Build: oracle/Makefile (gcc, -ffp-contract=off, no fast-math; the AVX2
  * kernels use target attributes so the library runs on any x86-64 host and
@@ -347,6 +353,31 @@ __attribute__((target("f16c"))) void orc_f16_to_f32_f16c(const uint16_t* src, fl
     for (size_t i = 0; i < n; i++) dst[i] = _cvtsh_ss(src[i]);
 }
 
+/* rms_norm_fused, AVX2 branch (kernels.rs:592-619): one 8-wide FMA chain
+ * of v*v over the first n8 = n - n % 8 elements, hsum256, the tail's x*x
+ * added one by one (no FMA), divided by n; the n8 elements become
+ * (v * inv_rms) * w with inv_rms = 1 / sqrt(mean + eps), the tail
+ * x / sqrt(mean + eps) * w.  In place. */
+__attribute__((target("avx2,fma"))) void orc_rms_norm_avx2(float* x, const float* weight,
+                                                           size_t n, float eps) {
+    size_t n8 = n - (n % 8);
+    __m256 sq = _mm256_setzero_ps();
+    for (size_t i = 0; i < n8; i += 8) {
+        __m256 v = _mm256_loadu_ps(x + i);
+        sq = _mm256_fmadd_ps(v, v, sq);
+    }
+    float mean_sq = hsum256(sq);
+    for (size_t i = n8; i < n; i++) mean_sq += x[i] * x[i];
+    mean_sq /= (float)n;
+    __m256 inv_rms = _mm256_set1_ps(1.0f / sqrtf(mean_sq + eps));
+    for (size_t i = 0; i < n8; i += 8) {
+        __m256 v = _mm256_loadu_ps(x + i);
+        __m256 w = _mm256_loadu_ps(weight + i);
+        _mm256_storeu_ps(x + i, _mm256_mul_ps(_mm256_mul_ps(v, inv_rms), w));
+    }
+    for (size_t i = n8; i < n; i++) x[i] = x[i] / sqrtf(mean_sq + eps) * weight[i];
+}
+
 int orc_have_avx2_fma(void) {
     __builtin_cpu_init();
     return __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
@@ -358,6 +389,10 @@ int orc_have_f16c(void) {
 #else
 int orc_have_avx2_fma(void) { return 0; }
 int orc_have_f16c(void) { return 0; }
+void orc_rms_norm_scalar(float* x, const float* weight, size_t n, float eps);
+void orc_rms_norm_avx2(float* x, const float* weight, size_t n, float eps) {
+    orc_rms_norm_scalar(x, weight, n, eps);
+}
 void orc_matmul_q4_0_avx2(float* y, const uint8_t* w, size_t w_len, const float* x,
                           const float* bias, size_t n, size_t m) {
     orc_matmul_q4_0_scalar(y, w, w_len, x, bias, n, m);
@@ -474,5 +509,52 @@ void orc_matmul_q4_0_absdot_f64(double* y, const uint8_t* w, size_t w_len, const
             s += fabs((double)deq[e % 32] * (double)x[k]);
         }
         y[r] = s;
+    }
+}
+
+/* rms_norm_fused, scalar fallback (kernels.rs:621-624): sequential sum of
+ * v*v, / n, inv_rms = 1 / sqrt(mean + eps), x * inv_rms * w.  In place. */
+void orc_rms_norm_scalar(float* x, const float* weight, size_t n, float eps) {
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; i++) sum += x[i] * x[i];
+    float mean_sq = sum / (float)n;
+    float inv_rms = 1.0f / sqrtf(mean_sq + eps);
+    for (size_t i = 0; i < n; i++) x[i] = x[i] * inv_rms * weight[i];
+}
+
+/* ops::rms_norm_in_place -> kernels::rms_norm_fused (ops.rs:59-61,
+ * kernels.rs:592-625): AVX2 when present, else scalar; `rows` rows of n. */
+void orc_rms_norm(float* x, const float* weight, size_t n, size_t rows, float eps) {
+    for (size_t r = 0; r < rows; r++) {
+        if (orc_have_avx2_fma())
+            orc_rms_norm_avx2(x + r * n, weight, n, eps);
+        else
+            orc_rms_norm_scalar(x + r * n, weight, n, eps);
+    }
+}
+
+/* turbo::batch_rms_norm (turbo.rs:288-303): f64 sum of squares,
+ * rms = (f32)sqrt(ss / dim + eps) in f64, inv = 1 / rms in f32,
+ * out = inp * inv * w. */
+void orc_batch_rms_norm(float* out, const float* inp, const float* weight, size_t dim,
+                        size_t batch, float eps) {
+    for (size_t r = 0; r < batch; r++) {
+        const float* in = inp + r * dim;
+        double ss = 0.0;
+        for (size_t i = 0; i < dim; i++) ss += (double)in[i] * (double)in[i];
+        float rms = (float)sqrt(ss / (double)dim + (double)eps);
+        float inv = 1.0f / rms;
+        for (size_t i = 0; i < dim; i++) out[r * dim + i] = in[i] * inv * weight[i];
+    }
+}
+
+/* ops::silu_in_place then gate *= up (ops.rs:81-83, transformer.rs:446-449):
+ * out[i] = (g / (1 + exp(-g))) * up[i] with libm expf (what Rust's f32::exp
+ * calls on Linux). */
+void orc_silu_mul(float* out, const float* gate, const float* up, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        float g = gate[i];
+        float s = g / (1.0f + expf(-g));
+        out[i] = s * up[i];
     }
 }
