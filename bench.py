@@ -385,6 +385,44 @@ def lm_head(torch, lib):
                         "of 512/1024), M in {1,128}, Q4_0 and FP16 weights", "results": out}
 
 
+def q8_0_decode(torch, lib):
+    """Q8_0 weights (34-byte blocks, 1.0625 B per weight) at the Mistral-7B
+    projection shapes, M = 1: GPU time per hypno_hip_matmul_q8_0_dev call over
+    >= 512 MB of distinct weight copies.  The reference dequantises the whole
+    tensor to fp32 on every such call (ops.rs:33-36)."""
+    import hypno_amd as hk
+    out = {}
+    gen = torch.Generator(device="cuda").manual_seed(88)
+    for name, n, m in (("q_o", 4096, 4096), ("k_v", 1024, 4096), ("gate_up", 14336, 4096),
+                       ("down", 4096, 14336)):
+        nb = n * m // 32 * 34
+        stride = (nb + 255) // 256 * 256
+        copies = max(2, -(-(512 * 2**20) // nb))
+        arena = torch.empty(copies * stride, dtype=torch.uint8, device="cuda")
+        for c in range(copies):
+            w = torch.randn(n * m, generator=gen, device="cuda").mul_(0.02)
+            arena[c * stride:c * stride + nb].copy_(hk.quantize_f32_to_q8_0(w))
+            del w
+        x = torch.randn(m, generator=gen, device="cuda")
+        y = torch.empty(n, device="cuda")
+        xp, yp = ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr())
+        base = arena.data_ptr()
+
+        def issue(sp, i, base=base, stride=stride, copies=copies, nb=nb, n=n, m=m):
+            rc = lib.lib.hypno_hip_matmul_q8_0_dev(yp, ctypes.c_void_p(base + (i % copies) * stride),
+                                                   nb, xp, None, n, m, 1, sp)
+            if rc:
+                lib.check(rc, "matmul_q8_0")
+
+        us = time_calls_graph(torch, issue, reps=copies * 4)
+        out[f"{name}_M1"] = {"us": round(us, 2), "weight_gbs": round(nb / us / 1e3, 1),
+                             "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
+        del arena, x, y
+        torch.cuda.empty_cache()
+    return {"workload": "Q8_0 Mistral-7B projections, M = 1, one call per matrix, rotating "
+                        ">= 512 MB of weight copies", "results": out}
+
+
 PCIE_PEAK_GBS = 64.0  # MI355X host link: PCIe 5.0 x16, one direction
 
 
@@ -657,7 +695,8 @@ def main():
         sec = {}
         for key, fn in (("c0_single_gemv", single_gemv), ("c2_prefill_gemm", prefill_gemm),
                         ("c3_mistral_stream", mistral_stream), ("c3_m_sweep", mistral_m_sweep),
-                        ("c4_lm_head", lm_head), ("model_load", model_load)):
+                        ("c4_lm_head", lm_head), ("model_load", model_load),
+                        ("q8_0_decode", q8_0_decode)):
             print(f"[bench] secondary: {key}", file=sys.stderr, flush=True)
             sec[key] = fn(torch, lib)
         line["secondary"] = sec

@@ -10,13 +10,16 @@ from .kernels import (  # noqa: F401
     HypnoHipError,
     batch_matmul,
     dequantize_q4_0,
+    dequantize_q8_0,
     device_count,
     matmul_f16,
     matmul_q4_0,
+    matmul_q8_0,
     matmul_vec_auto,
     matmul_vec_f16,
     matmul_vec_q4_0,
     quantize_f32_to_q4_0,
+    quantize_f32_to_q8_0,
     register_weight,
     rms_norm,
     rms_norm_in_place,

@@ -177,6 +177,40 @@ int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
   return HYPNO_HIP_OK;
 }
 
+// Q8_0 (ops.rs:33-36, turbo.rs:334-341): the reference dequantises the
+// whole tensor and slices rows of it, so a buffer shorter than n*m elements
+// is a panic there (EINVAL here).  Tokens go one by one through the GEMV.
+int q8_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const float* bias,
+             size_t n, size_t m, size_t batch, hipStream_t s) {
+  if (n == 0 || batch == 0) return HYPNO_HIP_OK;
+  if (!y || !x) return fail(HYPNO_HIP_EINVAL, "y and x must not be NULL");
+  if (mul_overflows(n, batch) || mul_overflows(m, batch) || mul_overflows(n, m))
+    return fail(HYPNO_HIP_EINVAL, "shape overflows size_t");
+  if (w_len / kQ8BlockBytes * kBlockElems < n * m)
+    return fail(HYPNO_HIP_EINVAL, "Q8_0 weights: %zu bytes hold fewer than n*m = %zu elements",
+                w_len, n * m);
+  if (!w && n * m) return fail(HYPNO_HIP_EINVAL, "w is NULL");
+  int cus = 256;
+  {
+    std::lock_guard<std::mutex> g(g_mu);
+    DeviceState* ds = nullptr;
+    int st = device_state(&ds);
+    if (st) return st;
+    cus = ds->cus;
+  }
+  hipError_t e;
+  if (q8_0_gemv_fast_ok(w, w_len, n, m) && aligned16(x)) {
+    for (size_t t = 0; t < batch; t++) {
+      e = launch_q8_0_gemv_fast(y + t * n, w, x + t * m, bias, n, m, cus, s);
+      if (e != hipSuccess) return hip_fail(e, "q8_0 GEMV launch");
+    }
+    return HYPNO_HIP_OK;
+  }
+  e = launch_q8_0_generic(y, w, x, bias, n, m, batch, s);
+  if (e != hipSuccess) return hip_fail(e, "q8_0 generic launch");
+  return HYPNO_HIP_OK;
+}
+
 int f16_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const float* bias,
             size_t n, size_t m, size_t batch, hipStream_t s) {
   if (n == 0 || batch == 0) return HYPNO_HIP_OK;
@@ -226,9 +260,9 @@ int f16_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const floa
 
 int host_matmul(float* y, const uint8_t* w, size_t w_len, uint32_t dtype, const float* x,
                 const float* bias, size_t n, size_t m, size_t batch) {
-  if (dtype == HYPNO_DTYPE_FP32 || dtype == HYPNO_DTYPE_Q8_0)
-    return fail(HYPNO_HIP_ENOTSUP, "dtype %u is not on the Q4_0/FP16 path", dtype);
-  if (dtype != HYPNO_DTYPE_Q4_0 && dtype != HYPNO_DTYPE_FP16)
+  if (dtype == HYPNO_DTYPE_FP32)
+    return fail(HYPNO_HIP_ENOTSUP, "dtype %u is not on the quantised/FP16 path", dtype);
+  if (dtype != HYPNO_DTYPE_Q4_0 && dtype != HYPNO_DTYPE_FP16 && dtype != HYPNO_DTYPE_Q8_0)
     return fail(HYPNO_HIP_EINVAL, "unknown dtype %u", dtype);
   if (n == 0 || batch == 0) return HYPNO_HIP_OK;
   if (!y || (!x && m) || (!w && w_len))
@@ -238,6 +272,9 @@ int host_matmul(float* y, const uint8_t* w, size_t w_len, uint32_t dtype, const 
     return fail(HYPNO_HIP_EINVAL, "shape overflows size_t");
   if (dtype == HYPNO_DTYPE_FP16 && (mul_overflows(n, m) || w_len < 2 * n * m))
     return fail(HYPNO_HIP_EINVAL, "fp16 weights: w_len %zu < 2*n*m", w_len);
+  if (dtype == HYPNO_DTYPE_Q8_0 &&
+      (mul_overflows(n, m) || w_len / kQ8BlockBytes * kBlockElems < n * m))
+    return fail(HYPNO_HIP_EINVAL, "Q8_0 weights: %zu bytes hold fewer than n*m elements", w_len);
 
   // One host-slice call at a time: the staging buffers and the registry's
   // device copies are shared by all callers.
@@ -281,6 +318,8 @@ int host_matmul(float* y, const uint8_t* w, size_t w_len, uint32_t dtype, const 
   }
   if (dtype == HYPNO_DTYPE_Q4_0)
     st = q4_0_dev((float*)ds->y.p, dw, w_len, (const float*)ds->x.p, db, n, m, batch, s);
+  else if (dtype == HYPNO_DTYPE_Q8_0)
+    st = q8_0_dev((float*)ds->y.p, dw, w_len, (const float*)ds->x.p, db, n, m, batch, s);
   else
     st = f16_dev((float*)ds->y.p, dw, w_len, (const float*)ds->x.p, db, n, m, batch, s);
   if (st) {
@@ -342,6 +381,11 @@ int hypno_hip_matmul_f16(float* y, const uint8_t* w, size_t w_len, const float* 
   return host_matmul(y, w, w_len, HYPNO_DTYPE_FP16, x, bias, n, m, 1);
 }
 
+int hypno_hip_matmul_q8_0(float* y, const uint8_t* w_q, size_t w_len, const float* x,
+                          const float* bias, size_t n, size_t m) {
+  return host_matmul(y, w_q, w_len, HYPNO_DTYPE_Q8_0, x, bias, n, m, 1);
+}
+
 int hypno_hip_matmul_vec_auto(float* y, const uint8_t* w, size_t w_len, uint32_t dtype,
                               const float* x, const float* bias, size_t n, size_t m) {
   return host_matmul(y, w, w_len, dtype, x, bias, n, m, 1);
@@ -399,6 +443,30 @@ int hypno_hip_matmul_q4_0_dev(float* y, const uint8_t* w_q, size_t w_len, const 
 int hypno_hip_matmul_f16_dev(float* y, const uint8_t* w, size_t w_len, const float* x,
                              const float* bias, size_t n, size_t m, size_t batch, void* stream) {
   return f16_dev(y, w, w_len, x, bias, n, m, batch, (hipStream_t)stream);
+}
+
+int hypno_hip_matmul_q8_0_dev(float* y, const uint8_t* w_q, size_t w_len, const float* x,
+                              const float* bias, size_t n, size_t m, size_t batch,
+                              void* stream) {
+  return q8_0_dev(y, w_q, w_len, x, bias, n, m, batch, (hipStream_t)stream);
+}
+
+int hypno_hip_quantize_q8_0_dev(uint8_t* out, const float* src, size_t n_elems, void* stream) {
+  const size_t nb = n_elems / kBlockElems;
+  if (nb == 0) return HYPNO_HIP_OK;
+  if (!out || !src) return fail(HYPNO_HIP_EINVAL, "quantize: NULL pointer");
+  hipError_t e = launch_quantize_q8_0(out, src, nb, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "quantize launch");
+  return HYPNO_HIP_OK;
+}
+
+int hypno_hip_dequantize_q8_0_dev(float* out, const uint8_t* q, size_t q_len, void* stream) {
+  const size_t nb = q_len / kQ8BlockBytes;
+  if (nb == 0) return HYPNO_HIP_OK;
+  if (!out || !q) return fail(HYPNO_HIP_EINVAL, "dequantize: NULL pointer");
+  hipError_t e = launch_dequantize_q8_0(out, q, nb, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "dequantize launch");
+  return HYPNO_HIP_OK;
 }
 
 int hypno_hip_quantize_q4_0_dev(uint8_t* out, const float* src, size_t n_elems, void* stream) {

@@ -55,6 +55,7 @@ __device__ __forceinline__ T load_const(const void* p) {
 
 constexpr int kBlockElems = 32;  // Q4_0 block: 32 weights (dtype.rs:40-45)
 constexpr int kBlockBytes = 18;  // fp16 scale + 16 packed bytes (dtype.rs:48-54)
+constexpr int kQ8BlockBytes = 34;  // Q8_0: fp16 scale + 32 bytes q + 128 (dtype.rs:50)
 
 // f16 bits -> f32, exact (v_cvt_f32_f16).
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
@@ -147,6 +148,16 @@ hipError_t launch_q4_0_generic(float* y, const uint8_t* w, size_t w_len, const f
 bool q4_0_gemv_fast_ok(const uint8_t* w, size_t w_len, size_t n, size_t m);
 hipError_t launch_q4_0_gemv_fast(float* y, const uint8_t* w, const float* x, const float* bias,
                                  size_t n, size_t m, int num_cus, hipStream_t s);
+// Q8_0 codec (codec.hip) and any-shape GEMV (gemv_q4_0.hip; requires the
+// buffer to hold all n*m elements, as matmul_f32 does).
+hipError_t launch_quantize_q8_0(uint8_t* out, const float* src, size_t n_blocks, hipStream_t s);
+hipError_t launch_dequantize_q8_0(float* out, const uint8_t* q, size_t n_blocks, hipStream_t s);
+hipError_t launch_q8_0_generic(float* y, const uint8_t* w, const float* x, const float* bias,
+                               size_t n, size_t m, size_t batch, hipStream_t s);
+// Q8_0 (34-byte blocks), same conditions with w_len >= n*m/32*34.
+bool q8_0_gemv_fast_ok(const uint8_t* w, size_t w_len, size_t n, size_t m);
+hipError_t launch_q8_0_gemv_fast(float* y, const uint8_t* w, const float* x, const float* bias,
+                                 size_t n, size_t m, int num_cus, hipStream_t s);
 
 // Step applied to a job's input vector while it is staged (values of
 // HYPNO_HIP_PROLOGUE_* in include/hypno_hip.h).
@@ -169,8 +180,13 @@ struct GemvJob {
   float eps;  // kProRmsNorm
 };
 
+// Weight block formats of the streaming GEMV.
+constexpr int kFmtQ4_0 = 0;
+constexpr int kFmtQ8_0 = 1;
+
 // Work-group shape shared by the jobs of one launch.
 struct GemvGroupGeom {
+  int fmt = kFmtQ4_0;
   int Tbase = 0; // lcm over jobs of lcm(B, 64)
   int T = 0;     // threads: Tbase doubled up to at least 256 (when it fits)
   int W = 0;     // waves

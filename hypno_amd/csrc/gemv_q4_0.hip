@@ -1,4 +1,4 @@
-// Q4_0 matrix-vector kernels for gfx950.
+// Q4_0 and Q8_0 matrix-vector kernels for gfx950.
 //
 //  * q4_0_generic_kernel: any m (blocks straddling rows), any alignment, short
 //    weight buffers, bias, and any number of tokens.  One wave per
@@ -6,6 +6,9 @@
 //    matmul_q4_0_scalar (kernels.rs:362-400).
 //  * q4_0_gemv_jobs_kernel: the decode GEMV (one token) over one job or a
 //    table of independent jobs in a single launch.  See the comment above it.
+//  * q8_0_generic_kernel / q8_0_gemv_jobs_kernel: the same for Q8_0 weights
+//    (ops.rs:33-36 semantics: dequantised rows, fp32 accumulation); the
+//    streaming kernel is the Q4_0 one instantiated for 34-byte blocks.
 #include "common.hpp"
 
 namespace hypno {
@@ -58,6 +61,42 @@ hipError_t launch_q4_0_generic(float* y, const uint8_t* w, size_t w_len, const f
   return hipGetLastError();
 }
 
+// Q8_0 for any shape: ops.rs:33-36 dequantises the tensor and runs matmul_f32
+// over the flattened rows [r*m, (r+1)*m) (kernels.rs:234-241), so a block
+// may straddle two rows.  One wave per (token, row); lanes take the row's
+// elements in strides of 64.  The caller guarantees the buffer holds all
+// n*m elements (a shorter one is a panic in the reference).
+__global__ void __launch_bounds__(256)
+q8_0_generic_kernel(float* __restrict__ y, const uint8_t* __restrict__ w,
+                    const float* __restrict__ x, const float* __restrict__ bias, size_t n,
+                    size_t m, size_t batch) {
+  const size_t wave = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (wave >= n * batch) return;  // wave-uniform
+  const size_t t = wave / n;
+  const size_t r = wave - t * n;
+  const float* xt = x + t * m;
+  float acc = 0.0f;
+  for (size_t j = lane; j < m; j += 64) {
+    const size_t e = r * m + j;
+    const uint8_t* blk = w + (e / kBlockElems) * kQ8BlockBytes;
+    const float d = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+    acc = fmaf((float)((int)blk[2 + e % kBlockElems] - 128) * d, xt[j], acc);
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) y[t * n + r] = acc + (bias ? bias[r] : 0.0f);
+}
+
+hipError_t launch_q8_0_generic(float* y, const uint8_t* w, const float* x, const float* bias,
+                               size_t n, size_t m, size_t batch, hipStream_t s) {
+  const size_t waves = n * batch;
+  if (waves == 0) return hipSuccess;
+  const size_t grid = (waves + 3) / 4;
+  hipLaunchKernelGGL(q8_0_generic_kernel, dim3((unsigned)grid), dim3(256), 0, s, y, w, x, bias, n,
+                     m, batch);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Streaming decode GEMV over a table of jobs (one token, m % 256 == 0)
 //
@@ -102,9 +141,40 @@ hipError_t launch_q4_0_generic(float* y, const uint8_t* w, size_t w_len, const f
 // most 2^-19 of the block's largest |x| (a normwise error near 1e-6 on
 // N(0,1) activations, against the 1e-4 bound), for 20 dot instructions per
 // block.
-constexpr int kLimbs = 5;
-constexpr int kMantBits = 18;
-constexpr int kDigitBias = 0x88888;
+//
+// Q8_0 blocks (34 bytes: fp16 d, then 32 bytes u = q + 128) use the same
+// scheme with signed base-256 digits: m = rint(x * 2^(22-e)), |m| <= 2^22,
+// m + 0x808080 in [0, 2^24) split into three bytes u_l, the digit u_l - 128
+// stored as the i8 value u_l ^ 0x80; v_dot4_i32_i8 multiplies four
+// (u - 128) weights (u ^ 0x80 read as i8) with four digits, 24 dot
+// instructions per block, x rounded to 2^-23 of the block's largest |x|.
+template <int F>
+struct Fmt;
+template <>
+struct Fmt<kFmtQ4_0> {
+  static constexpr int kBytes = 18;       // block bytes
+  static constexpr int kLimbs = 5;        // digits of x
+  static constexpr int kLimbDwords = 4;   // dwords per block per digit plane
+  static constexpr int kMantBits = 18;
+  static constexpr int kDigitBias = 0x88888;
+  struct Slot {  // this lane's 20-byte window of one step
+    u32x4 a;
+    uint32_t b;
+  };
+};
+template <>
+struct Fmt<kFmtQ8_0> {
+  static constexpr int kBytes = 34;
+  static constexpr int kLimbs = 3;
+  static constexpr int kLimbDwords = 8;
+  static constexpr int kMantBits = 22;
+  static constexpr int kDigitBias = 0x808080;
+  struct Slot {  // this lane's 36-byte window of one step
+    u32x4 a;
+    u32x4 b;
+    uint32_t c;
+  };
+};
 constexpr int kBadExp = -100000;  // block with inf or NaN activations
 
 static int gcd_int(int a, int b) {
@@ -130,8 +200,10 @@ static void finish_geometry(GemvGroupGeom& g) {
   g.W = g.T / 64;
   g.S = 64;
   const size_t loop = (size_t)g.S * (g.T / 8) * 4;  // 8-lane group partials
-  // activation limbs and exponents, then one float per wave (prologue sums)
-  const size_t xs = (size_t)g.maxB * (16 * kLimbs + 4) + 4 * (size_t)g.W;
+  // activation digits and exponents, then one float per wave (prologue sums)
+  const size_t digits = g.fmt == kFmtQ8_0 ? 4 * Fmt<kFmtQ8_0>::kLimbs * 8
+                                          : 4 * Fmt<kFmtQ4_0>::kLimbs * 4;
+  const size_t xs = (size_t)g.maxB * (digits + 4) + 4 * (size_t)g.W;
   g.lds = xs > loop ? xs : loop;
 }
 
@@ -160,17 +232,20 @@ bool q4_0_gemv_fast_ok(const uint8_t* w, size_t w_len, size_t n, size_t m) {
   return w_len / kBlockBytes >= n * (m / kBlockElems);
 }
 
-// One ring slot: this lane's 20-byte window of one step.
-struct Slot {
-  u32x4 a;
-  uint32_t b;
-};
+bool q8_0_gemv_fast_ok(const uint8_t* w, size_t w_len, size_t n, size_t m) {
+  if (n == 0 || n > (size_t)0x3FFFFFFF) return false;
+  if (((uintptr_t)w & 15) != 0) return false;
+  GemvGroupGeom g;
+  g.fmt = kFmtQ8_0;
+  if (!gemv_group_add(g, m)) return false;
+  return w_len / Fmt<kFmtQ8_0>::kBytes >= n * (m / kBlockElems);
+}
 
 // Prefetch cursor (work-group uniform): the job the ring is reading and the
 // address of the next step to fetch.
 struct RingCursor {
   const uint8_t* next;  // first byte of the next step to fetch
-  int bps;              // bytes per step = rps * B * 18
+  int bps;              // bytes per step = rps * B * block bytes
   int end;              // one past the job's last global step
   int last_units;       // blocks in the job's last (possibly partial) step
   int j;
@@ -178,8 +253,14 @@ struct RingCursor {
 
 __device__ __forceinline__ int job_steps(const GemvJob& J) { return (J.n + J.rps - 1) / J.rps; }
 
-__global__ void __launch_bounds__(1024)
-q4_0_gemv_jobs_kernel(GemvLaunch L) {
+template <int F>
+__device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
+  using FT = Fmt<F>;
+  using Slot = typename FT::Slot;
+  constexpr int kLimbs = FT::kLimbs;
+  constexpr int kLD = FT::kLimbDwords;
+  constexpr int kMantBits = FT::kMantBits;
+  constexpr int kDigitBias = FT::kDigitBias;
   extern __shared__ __align__(16) uint8_t smem[];
   const int T = blockDim.x;
   const int t = threadIdx.x;
@@ -195,7 +276,7 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
     const GemvJob J = get(j);
     const int steps = job_steps(J);
     RingCursor c;
-    c.bps = J.rps * J.B * 18;
+    c.bps = J.rps * J.B * FT::kBytes;
     c.next = J.w + (size_t)(g - J.step0) * c.bps;
     c.end = J.step0 + steps;
     c.last_units = (J.n - (steps - 1) * J.rps) * J.B;
@@ -217,13 +298,16 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
   }
 
   // Ring loads are unconditional (a lane with nothing to fetch re-reads the
-  // first 20 bytes of a job's weights, always in bounds): a load under a
+  // first bytes of a job's weights, always in bounds): a load under a
   // branch is waited for at once, which would serialise the ring.  The job
   // table is read only when the ring crosses into the next job.
   RingCursor pc = cursor_at(j0, s_begin);
   int pg = s_begin;  // next step the ring fetches
   const uint8_t* wsafe = pc.next;
-  const uint32_t win = (uint32_t)(18 * t) & ~3u;  // window start inside a step
+  // Window start inside a step: the block at byte kBytes * t, rounded down to
+  // a dword (a block starts at byte 0 or 2 of its window; the last block of
+  // a step or matrix has an odd index, so its window ends with it).
+  const uint32_t win = (uint32_t)(FT::kBytes * t) & ~3u;
   auto issue = [&]() -> Slot {
     const uint8_t* p = wsafe;
     if (pg < s_end) {
@@ -234,8 +318,14 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
     }
     pg++;
     Slot r;
-    r.a = load_global<u32x4>(p);
-    r.b = load_global<uint32_t>(p + 16);
+    if constexpr (F == kFmtQ4_0) {
+      r.a = load_global<u32x4>(p);
+      r.b = load_global<uint32_t>(p + 16);
+    } else {
+      r.a = load_global<u32x4>(p);
+      r.b = load_global<u32x4>(p + 16);
+      r.c = load_global<uint32_t>(p + 32);
+    }
     return r;
   };
   Slot ring0 = issue();  // ring0 holds steps s_begin, s_begin+3, ...
@@ -243,7 +333,7 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
   Slot ring2 = issue();
 
   // Byte selectors for v_perm_b32: a block starts at byte 0 (t even) or 2
-  // (t odd) of its window; nibble dword j is bytes [2+4j, 6+4j) of the block.
+  // (t odd) of its window; weight dword j is bytes [2+4j, 6+4j) of the block.
   const bool odd = (t & 1) != 0;
   const uint32_t sel_q = odd ? 0x07060504u : 0x05040302u;
   const uint32_t sh_d = odd ? 16u : 0u;
@@ -260,8 +350,8 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
   int job_last = 0;       // the job's last global step
   int last_units = 0;     // blocks in that step
   int c0 = s_begin;       // first step of the open partial-sum chunk
-  u32x4 xl[kLimbs];     // this lane's block column of x as i4 limbs
-  int xe = 0;           // its exponent: x = 2^xe * sum_k 16^k * digit_k
+  u32x4 xl[kLimbs * kLD / 4];  // this lane's block column of x as digit planes
+  int xe = 0;           // its exponent: x = 2^xe * sum_k base^k * digit_k
   float xnan = 0.0f;    // NaN when the block holds a non-finite activation
 
   // Sum the parked partials of steps [c0, c1) into y (one thread per row, in
@@ -333,7 +423,7 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
     c0 = g;
     const int B = J.B;
     uint32_t* limbs = reinterpret_cast<uint32_t*>(smem);
-    int* exps = reinterpret_cast<int*>(smem + (size_t)kLimbs * 16 * B);
+    int* exps = reinterpret_cast<int*>(smem + (size_t)kLimbs * kLD * 4 * B);
     const float4* xv = reinterpret_cast<const float4*>(J.x);
     const float4* av = reinterpret_cast<const float4*>(J.aux);
     auto load8 = [&](const float4* p, int i, float* o) __attribute__((always_inline)) {
@@ -383,12 +473,26 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
 #pragma unroll
       for (int k = 0; k < 8; k++)
         u[k] = (uint32_t)((int)rintf(ldexpf(xs[k], kMantBits - e)) + kDigitBias);
+      if constexpr (F == kFmtQ4_0) {
 #pragma unroll
-      for (int l = 0; l < kLimbs; l++) {
-        uint32_t w = 0;
+        for (int l = 0; l < kLimbs; l++) {
+          uint32_t w = 0;
 #pragma unroll
-        for (int k = 0; k < 8; k++) w |= ((u[k] >> (4 * l)) & 15u) << (4 * k);
-        limbs[(l * B * 4) + i] = w ^ 0x88888888u;
+          for (int k = 0; k < 8; k++) w |= ((u[k] >> (4 * l)) & 15u) << (4 * k);
+          limbs[(l * B * 4) + i] = w ^ 0x88888888u;
+        }
+      } else {
+#pragma unroll
+        for (int l = 0; l < kLimbs; l++) {
+          uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+          for (int k = 0; k < 4; k++) {
+            w0 |= ((u[k] >> (8 * l)) & 255u) << (8 * k);
+            w1 |= ((u[k + 4] >> (8 * l)) & 255u) << (8 * k);
+          }
+          limbs[(l * B * 8) + 2 * i] = w0 ^ 0x80808080u;
+          limbs[(l * B * 8) + 2 * i + 1] = w1 ^ 0x80808080u;
+        }
       }
       if ((i & 3) == 0) exps[i >> 2] = mb >= 0x7F800000u ? kBadExp : e - kMantBits;
     };
@@ -429,8 +533,9 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
     __syncthreads();
     const int kb = t % B;
 #pragma unroll
-    for (int l = 0; l < kLimbs; l++)
-      xl[l] = *reinterpret_cast<const u32x4*>(limbs + l * B * 4 + kb * 4);
+    for (int v = 0; v < kLimbs * kLD / 4; v++)  // plane v / (kLD / 4), piece v % (kLD / 4)
+      xl[v] = *reinterpret_cast<const u32x4*>(limbs + (v / (kLD / 4)) * B * kLD + kb * kLD +
+                                              (v % (kLD / 4)) * 4);
     const int ex = exps[kb];
     xe = ex == kBadExp ? 0 : ex;
     xnan = ex == kBadExp ? __builtin_nanf("") : 0.0f;
@@ -452,25 +557,48 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
     const int vu = ss == job_last ? last_units : T;
     float partial = 0.0f;
     if (t < vu) {
-      const uint32_t d[5] = {sl.a.x, sl.a.y, sl.a.z, sl.a.w, sl.b};
-      const float scale = f16_bits_to_f32(d[0] >> sh_d);
-      // D_l = sum_i (nib_i - 8) * digit_l(x_i): nib ^ 8 read as signed i4 is
-      // nib - 8; eight products per v_dot8_i32_i4, exact in int32.
-      int acc[kLimbs] = {};
+      if constexpr (F == kFmtQ4_0) {
+        const uint32_t d[5] = {sl.a.x, sl.a.y, sl.a.z, sl.a.w, sl.b};
+        const float scale = f16_bits_to_f32(d[0] >> sh_d);
+        // D_l = sum_i (nib_i - 8) * digit_l(x_i): nib ^ 8 read as signed i4
+        // is nib - 8; eight products per v_dot8_i32_i4, exact in int32.
+        int acc[kLimbs] = {};
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const uint32_t q = __builtin_amdgcn_perm(d[j + 1], d[j], sel_q) ^ 0x88888888u;
+        for (int j = 0; j < 4; j++) {
+          const uint32_t q = __builtin_amdgcn_perm(d[j + 1], d[j], sel_q) ^ 0x88888888u;
 #pragma unroll
-        for (int l = 0; l < kLimbs; l++)
-          acc[l] = __builtin_amdgcn_sdot8((int)q, (int)xl[l][j], acc[l], false);
+          for (int l = 0; l < kLimbs; l++)
+            acc[l] = __builtin_amdgcn_sdot8((int)q, (int)xl[l][j], acc[l], false);
+        }
+        // sum_l 16^l * D_l: the top four limbs in int32 (|h| < 2^24, so the
+        // conversion to fp32 is exact), the last step in fp32.
+        int h = acc[kLimbs - 1];
+#pragma unroll
+        for (int l = kLimbs - 2; l >= 1; l--) h = (h << 4) + acc[l];
+        const float r = fmaf((float)h, 16.0f, (float)acc[0]);
+        partial = ldexpf(scale * r, xe) + xnan;
+      } else {
+        const uint32_t d[9] = {sl.a.x, sl.a.y, sl.a.z, sl.a.w, sl.b.x,
+                               sl.b.y, sl.b.z, sl.b.w, sl.c};
+        const float scale = f16_bits_to_f32(d[0] >> sh_d);
+        // D_l = sum_i (u_i - 128) * digit_l(x_i): u ^ 0x80 read as i8 is
+        // u - 128; four products per v_dot4_i32_i8, exact in int32
+        // (|D_l| <= 32 * 128 * 128).
+        int acc[kLimbs] = {};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const uint32_t q = __builtin_amdgcn_perm(d[j + 1], d[j], sel_q) ^ 0x80808080u;
+#pragma unroll
+          for (int l = 0; l < kLimbs; l++)
+            acc[l] = __builtin_amdgcn_sdot4((int)q, (int)xl[2 * l + (j >> 2)][j & 3], acc[l],
+                                            false);
+        }
+        // 65536 D_2 + 256 D_1 + D_0: the top two in int32 (|h| < 2^28), the
+        // rest in fp32 (a relative rounding of 2^-24 on the block sum).
+        const int h = acc[2] * 256 + acc[1];
+        const float r = fmaf((float)h, 256.0f, (float)acc[0]);
+        partial = ldexpf(scale * r, xe) + xnan;
       }
-      // sum_l 16^l * D_l: the top four limbs in int32 (|h| < 2^24, so the
-      // conversion to fp32 is exact), the last step in fp32.
-      int h = acc[kLimbs - 1];
-#pragma unroll
-      for (int l = kLimbs - 2; l >= 1; l--) h = (h << 4) + acc[l];
-      const float r = fmaf((float)h, 16.0f, (float)acc[0]);
-      partial = ldexpf(scale * r, xe) + xnan;
     }
     partial = group8_sum(partial);
     if ((t & 7) == 7) part[(ss - c0) * T8 + (t >> 3)] = partial;
@@ -490,22 +618,31 @@ q4_0_gemv_jobs_kernel(GemvLaunch L) {
   flush(s_end);
 }
 
-static bool g_lds_attr_set = false;
+__global__ void __launch_bounds__(1024) q4_0_gemv_jobs_kernel(GemvLaunch L) {
+  gemv_jobs_body<kFmtQ4_0>(L);
+}
+
+__global__ void __launch_bounds__(1024) q8_0_gemv_jobs_kernel(GemvLaunch L) {
+  gemv_jobs_body<kFmtQ8_0>(L);
+}
+
+static bool g_lds_attr_set[2] = {false, false};
 
 hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
                                   const GemvJob& job0, int njobs, int total_steps, int num_cus,
                                   hipStream_t s) {
-  if (!g_lds_attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(q4_0_gemv_jobs_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+  const bool q8 = g.fmt == kFmtQ8_0;
+  const void* kern = q8 ? reinterpret_cast<const void*>(q8_0_gemv_jobs_kernel)
+                        : reinterpret_cast<const void*>(q4_0_gemv_jobs_kernel);
+  if (!g_lds_attr_set[q8]) {
+    hipError_t e =
+        hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
     if (e != hipSuccess) return e;
-    g_lds_attr_set = true;
+    g_lds_attr_set[q8] = true;
   }
   // As many work-groups as can be resident at once (registers and LDS).
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &per_cu, reinterpret_cast<const void*>(q4_0_gemv_jobs_kernel), g.T, g.lds) !=
-          hipSuccess ||
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, g.T, g.lds) != hipSuccess ||
       per_cu < 1)
     per_cu = 1;
   int grid = total_steps < num_cus * per_cu ? total_steps : num_cus * per_cu;
@@ -517,7 +654,8 @@ hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
   // Measured on a TinyLlama decode step (88 small launches): 577 -> 543 us,
   // 669 -> 614 us with fused norms; 1x or 4x the staging bytes do worse.
   {
-    const long long wbytes = (long long)total_steps * g.T * kBlockBytes;
+    const long long wbytes =
+        (long long)total_steps * g.T * (q8 ? Fmt<kFmtQ8_0>::kBytes : kBlockBytes);
     const long long stage = 4LL * kBlockElems * g.maxB * (g.pro ? 2 : 1);
     const long long ws = wbytes / (2 * stage);
     const int per = (int)((ws + num_cus / 2) / num_cus);
@@ -530,13 +668,18 @@ hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
   L.njobs = njobs;
   L.total_steps = total_steps;
   L.S = g.S;
-  hipLaunchKernelGGL(q4_0_gemv_jobs_kernel, dim3(grid), dim3(g.T), g.lds, s, L);
+  if (q8)
+    hipLaunchKernelGGL(q8_0_gemv_jobs_kernel, dim3(grid), dim3(g.T), g.lds, s, L);
+  else
+    hipLaunchKernelGGL(q4_0_gemv_jobs_kernel, dim3(grid), dim3(g.T), g.lds, s, L);
   return hipGetLastError();
 }
 
-hipError_t launch_q4_0_gemv_fast(float* y, const uint8_t* w, const float* x, const float* bias,
-                                 size_t n, size_t m, int num_cus, hipStream_t s) {
+static hipError_t launch_gemv_fast(int fmt, float* y, const uint8_t* w, const float* x,
+                                   const float* bias, size_t n, size_t m, int num_cus,
+                                   hipStream_t s) {
   GemvGroupGeom g;
+  g.fmt = fmt;
   gemv_group_add(g, m);
   GemvJob J;
   J.w = w;
@@ -552,6 +695,16 @@ hipError_t launch_q4_0_gemv_fast(float* y, const uint8_t* w, const float* x, con
   J.step0 = 0;
   const int steps = (J.n + J.rps - 1) / J.rps;
   return launch_q4_0_gemv_group(g, nullptr, J, 1, steps, num_cus, s);
+}
+
+hipError_t launch_q4_0_gemv_fast(float* y, const uint8_t* w, const float* x, const float* bias,
+                                 size_t n, size_t m, int num_cus, hipStream_t s) {
+  return launch_gemv_fast(kFmtQ4_0, y, w, x, bias, n, m, num_cus, s);
+}
+
+hipError_t launch_q8_0_gemv_fast(float* y, const uint8_t* w, const float* x, const float* bias,
+                                 size_t n, size_t m, int num_cus, hipStream_t s) {
+  return launch_gemv_fast(kFmtQ8_0, y, w, x, bias, n, m, num_cus, s);
 }
 
 }  // namespace hypno

@@ -31,7 +31,8 @@ __all__ = [
     "DType", "HypnoHipError", "matmul_q4_0", "matmul_f16", "matmul_vec_q4_0",
     "matmul_vec_f16", "matmul_vec_auto", "batch_matmul", "quantize_f32_to_q4_0",
     "dequantize_q4_0", "register_weight", "unregister_weight", "device_count", "GemvPlan",
-    "rms_norm", "rms_norm_in_place", "silu_mul",
+    "rms_norm", "rms_norm_in_place", "silu_mul", "matmul_q8_0", "quantize_f32_to_q8_0",
+    "dequantize_q8_0",
 ]
 
 
@@ -129,6 +130,7 @@ def _matmul(y, w, dtype: DType, x, bias, n: int, m: int, batch: int) -> None:
         xp = _dev_ptr(x, "f32", "x")
         bp = _dev_ptr(bias, "f32", "bias") if bias is not None else None
         fn = {DType.Q4_0: lib.hypno_hip_matmul_q4_0_dev,
+              DType.Q8_0: lib.hypno_hip_matmul_q8_0_dev,
               DType.FP16: lib.hypno_hip_matmul_f16_dev}.get(dtype)
         if fn is None:
             raise HypnoHipError(95, f"matmul dtype {dtype.name}")
@@ -163,6 +165,12 @@ def matmul_f16(y, w, x, bias, n: int, m: int) -> None:
     _matmul(y, w, DType.FP16, x, bias, n, m, 1)
 
 
+def matmul_q8_0(y, w_q, x, bias, n: int, m: int) -> None:
+    """y[n] = dequantize_q8_0(W_q)[n][m] . x[m] (+ bias): the Q8_0 arm of
+    matmul_vec_auto (ops.rs:33-36), streamed instead of dequantised."""
+    _matmul(y, w_q, DType.Q8_0, x, bias, n, m, 1)
+
+
 def matmul_vec_q4_0(y, w_q, x, bias, n: int, m: int) -> None:
     """ops.rs:15-17."""
     matmul_q4_0(y, w_q, x, bias, n, m)
@@ -174,22 +182,22 @@ def matmul_vec_f16(y, w, x, bias, n: int, m: int) -> None:
 
 
 def matmul_vec_auto(y, w, dtype, x, bias, n: int, m: int) -> None:
-    """Dtype switch of ops.rs:25-38 for this path: FP16 and Q4_0.  FP32 and
-    Q8_0 weights are outside it and raise HypnoHipError (ENOTSUP)."""
+    """Dtype switch of ops.rs:25-38: FP16, Q4_0 and Q8_0.  FP32 weights are
+    outside this path and raise HypnoHipError (ENOTSUP)."""
     dtype = DType(int(dtype))
-    if dtype not in (DType.Q4_0, DType.FP16):
+    if dtype not in (DType.Q4_0, DType.Q8_0, DType.FP16):
         raise HypnoHipError(95, f"matmul_vec_auto dtype {dtype.name}")
     _matmul(y, w, dtype, x, bias, n, m, 1)
 
 
 def batch_matmul(y, w, dtype, x, n: int, dim: int, batch: int, col_major: bool = False) -> None:
-    """turbo::batch_matmul (turbo.rs:306-343) for FP16 / Q4_0 row-major weights:
+    """turbo::batch_matmul (turbo.rs:306-343) for FP16 / Q4_0 / Q8_0 row-major weights:
     X[batch][dim] -> Y[batch][n] in one GPU call.  The column-major Q4_0 layout
     (kernels.rs:403-535) is outside this path and raises."""
     dtype = DType(int(dtype))
     if col_major:
         raise HypnoHipError(95, "batch_matmul col_major")
-    if dtype not in (DType.Q4_0, DType.FP16):
+    if dtype not in (DType.Q4_0, DType.Q8_0, DType.FP16):
         raise HypnoHipError(95, f"batch_matmul dtype {dtype.name}")
     _matmul(y, w, dtype, x, None, n, dim, batch)
 
@@ -217,6 +225,29 @@ def dequantize_q4_0(q):
     check(load().hypno_hip_dequantize_q4_0_dev(_dev_ptr(out, "f32", "out"),
                                                 _dev_ptr(q, "u8", "q"), q.numel(),
                                                 _stream(q.device)), "dequantize_q4_0")
+    return out
+
+
+def quantize_f32_to_q8_0(data):
+    """quant.rs:177-191 on the GPU: floor(len/32) blocks of 34 bytes, bit-exact."""
+    torch = _torch()
+    src = data.reshape(-1)
+    nb = src.numel() // 32
+    out = torch.empty(nb * 34, dtype=torch.uint8, device=src.device)
+    check(load().hypno_hip_quantize_q8_0_dev(_dev_ptr(out, "u8", "out"),
+                                              _dev_ptr(src, "f32", "data"), src.numel(),
+                                              _stream(src.device)), "quantize_q8_0")
+    return out
+
+
+def dequantize_q8_0(q):
+    """quant.rs:194-206 on the GPU: floor(len/34) blocks -> fp32, bit-exact."""
+    torch = _torch()
+    nb = q.numel() // 34
+    out = torch.empty(nb * 32, dtype=torch.float32, device=q.device)
+    check(load().hypno_hip_dequantize_q8_0_dev(_dev_ptr(out, "f32", "out"),
+                                                _dev_ptr(q, "u8", "q"), q.numel(),
+                                                _stream(q.device)), "dequantize_q8_0")
     return out
 
 

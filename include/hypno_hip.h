@@ -41,7 +41,7 @@ extern "C" {
 #define HYPNO_HIP_EINVAL 22   /* null pointer, bad shape or length, bad dtype */
 #define HYPNO_HIP_ENOMEM 12   /* device or pinned-host allocation failed */
 #define HYPNO_HIP_EDEVICE 5   /* HIP runtime / launch error, or no device */
-#define HYPNO_HIP_ENOTSUP 95  /* dtype outside this path (FP32, Q8_0) */
+#define HYPNO_HIP_ENOTSUP 95  /* dtype outside this path (FP32) */
 #define HYPNO_HIP_ENOENT 2    /* no such file, tensor or metadata key */
 #define HYPNO_HIP_EFILE 9     /* a file could not be opened, mapped or read */
 #define HYPNO_HIP_EFORMAT 74  /* malformed .hypno file (format.rs:109-131) */
@@ -82,14 +82,23 @@ int hypno_hip_matmul_q4_0(float* y, const uint8_t* w_q, size_t w_len, const floa
 int hypno_hip_matmul_f16(float* y, const uint8_t* w, size_t w_len, const float* x,
                          const float* bias, size_t n, size_t m);
 
+/* Replaces the Q8_0 arm of ops::matmul_vec_auto (ops.rs:33-36): y = the
+ * dequantised rows [r*m, (r+1)*m) of w_q (34-byte blocks: fp16 d, then 32
+ * bytes u; weight = (u - 128) * d) times x, fp32 accumulation, + bias.  The
+ * buffer must hold all n*m elements (EINVAL otherwise; the reference panics).
+ * The reference dequantises the whole tensor to fp32 on every call; this one
+ * streams the blocks. */
+int hypno_hip_matmul_q8_0(float* y, const uint8_t* w_q, size_t w_len, const float* x,
+                          const float* bias, size_t n, size_t m);
+
 /* Replaces ops::matmul_vec_auto(y, w, dtype, x, bias, n, m) (ops.rs:25-38) for
- * the dtypes of this path (FP16, Q4_0); FP32 and Q8_0 return ENOTSUP. */
+ * FP16, Q4_0 and Q8_0; FP32 returns ENOTSUP. */
 int hypno_hip_matmul_vec_auto(float* y, const uint8_t* w, size_t w_len, uint32_t dtype,
                               const float* x, const float* bias, size_t n, size_t m);
 
 /* Replaces turbo::batch_matmul(y, w, dtype, x, n, dim, batch, false)
- * (turbo.rs:306-333) for FP16 and Q4_0: X[batch][dim] -> Y[batch][n] in one
- * device call instead of one GEMV per token.  No bias. */
+ * (turbo.rs:306-341) for FP16, Q4_0 and Q8_0: X[batch][dim] -> Y[batch][n] in
+ * one device call instead of one GEMV per token.  No bias. */
 int hypno_hip_batch_matmul(float* y, const uint8_t* w, size_t w_len, uint32_t dtype,
                            const float* x, size_t n, size_t dim, size_t batch);
 
@@ -120,6 +129,20 @@ int hypno_hip_matmul_q4_0_dev(float* y, const uint8_t* w_q, size_t w_len, const 
 int hypno_hip_matmul_f16_dev(float* y, const uint8_t* w, size_t w_len, const float* x,
                              const float* bias, size_t n, size_t m, size_t batch,
                              void* stream);
+
+/* Q8_0 on device pointers (ops.rs:33-36 for batch == 1; turbo.rs:334-341
+ * semantics for batch > 1, token by token). */
+int hypno_hip_matmul_q8_0_dev(float* y, const uint8_t* w_q, size_t w_len, const float* x,
+                              const float* bias, size_t n, size_t m, size_t batch,
+                              void* stream);
+
+/* quantize_f32_to_q8_0 (quant.rs:177-191) on the device, bit-exact:
+ * floor(n_elems/32) blocks written to out (34 bytes each). */
+int hypno_hip_quantize_q8_0_dev(uint8_t* out, const float* src, size_t n_elems, void* stream);
+
+/* dequantize_q8_0 (quant.rs:194-206) on the device, bit-exact:
+ * floor(q_len/34) blocks -> 32 fp32 values each. */
+int hypno_hip_dequantize_q8_0_dev(float* out, const uint8_t* q, size_t q_len, void* stream);
 
 /* quantize_f32_to_q4_0 (quant.rs:108-117) on the device, bit-exact:
  * floor(n_elems/32) blocks written to out (18 bytes each). */

@@ -53,6 +53,14 @@ def lib():
     L.orc_batch_rms_norm.restype = None
     L.orc_silu_mul.argtypes = [vp, vp, vp, sz]
     L.orc_silu_mul.restype = None
+    L.orc_quantize_q8_0.argtypes = [vp, sz, vp]
+    L.orc_quantize_q8_0.restype = sz
+    L.orc_dequantize_q8_0.argtypes = [vp, sz, vp]
+    L.orc_dequantize_q8_0.restype = sz
+    L.orc_matmul_q8_0.argtypes = [vp, vp, sz, vp, vp, sz, sz]
+    L.orc_matmul_q8_0.restype = ctypes.c_int
+    L.orc_matmul_q8_0_f64.argtypes = [vp, vp, sz, vp, vp, sz, sz]
+    L.orc_matmul_q8_0_f64.restype = None
     for name in ("orc_matmul_q4_0", "orc_matmul_q4_0_scalar", "orc_matmul_q4_0_avx2",
                  "orc_matmul_f16", "orc_matmul_f16_scalar", "orc_matmul_f16_avx2"):
         getattr(L, name).argtypes = [vp, vp, sz, vp, vp, sz, sz]
@@ -280,3 +288,40 @@ def silu_mul(gate, up) -> np.ndarray:
     out = np.empty(g.size, np.float32)
     lib().orc_silu_mul(_p(out), _p(g), _p(u), g.size)
     return out
+
+
+def quantize_q8_0(w) -> np.ndarray:
+    """quantize_f32_to_q8_0 (quant.rs:177-191) over the flattened array."""
+    a = _c(w, np.float32).ravel()
+    out = np.empty((a.size // 32) * 34, np.uint8)
+    lib().orc_quantize_q8_0(_p(a), a.size, _p(out))
+    return out
+
+
+def dequantize_q8_0(q) -> np.ndarray:
+    """dequantize_q8_0 (quant.rs:194-206)."""
+    b = _c(q, np.uint8).ravel()
+    out = np.empty((b.size // 34) * 32, np.float32)
+    lib().orc_dequantize_q8_0(_p(b), b.size, _p(out))
+    return out
+
+
+def matmul_q8_0(w_q, x, bias, n, m) -> np.ndarray:
+    """ops::matmul_vec_auto's Q8_0 arm (ops.rs:33-36): dequantize, matmul_f32."""
+    w = _c(w_q, np.uint8).ravel()
+    xx = _c(x, np.float32).ravel()
+    b = _c(bias, np.float32) if bias is not None else None
+    y = np.empty(n, np.float32)
+    rc = lib().orc_matmul_q8_0(_p(y), _p(w), w.size, _p(xx), _p(b), n, m)
+    if rc != 0:
+        raise ValueError("Q8_0 weights shorter than n*m elements (the reference panics)")
+    return y
+
+
+def matmul_q8_0_f64(w_q, x, bias, n, m) -> np.ndarray:
+    w = _c(w_q, np.uint8).ravel()
+    xx = _c(x, np.float32).ravel()
+    b = _c(bias, np.float32) if bias is not None else None
+    y = np.empty(n, np.float64)
+    lib().orc_matmul_q8_0_f64(_p(y), _p(w), w.size, _p(xx), _p(b), n, m)
+    return y

@@ -26,6 +26,13 @@
  *                       running hypno could pin them)
  *   orc_matmul_f16_*    fp64 brute force; exact integer KAT (ops.rs:114-121)
  *   orc_batch_matmul    per-token equality with the GEMV; turbo.rs KATs
+ *   orc_quantize_q8_0   no reference test covers Q8_0: hand-computed blocks
+ *                       (divide by the rounded f16 scale, half-away ties,
+ *                       clamp to +-127, zero / NaN / overflowing scales)
+ *   orc_dequantize_q8_0 closed form (u - 128) * d, exact
+ *   orc_matmul_q8_0     dequantize + matmul_f32_scalar order; fp64 brute
+ *                       force and exact integer cases (the AVX2 / AVX-512
+ *                       f32 orders are not restated: tolerance-based)
  *   orc_rms_norm_*      reference KATs ops.rs:131-136, turbo.rs:716-735 (the
  *                       f64 batch_rms_norm within 1e-6 of the SIMD form),
  *                       turbo.rs:924-951; closed forms (constant rows, the
@@ -556,5 +563,88 @@ void orc_silu_mul(float* out, const float* gate, const float* up, size_t n) {
         float g = gate[i];
         float s = g / (1.0f + expf(-g));
         out[i] = s * up[i];
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Q8_0 (quant.rs:74-103, 176-206; ops.rs:33-36; turbo.rs:334-341)           */
+/* ------------------------------------------------------------------------ */
+
+#define Q8_BLOCK_BYTES 34
+
+/* quantize_f32_to_q8_0, quant.rs:177-191: floor(len/32) blocks;
+ * amax = fold(0, f32::max) over |v|; d = f16 RNE(amax / 127) (1.0 when
+ * amax == 0); q = clamp(round_half_away(v / f32(d)), -127, 127) — divides by
+ * the ROUNDED scale (unlike Q4_0); byte = q + 128. */
+size_t orc_quantize_q8_0(const float* src, size_t n, uint8_t* out) {
+    size_t nb = n / 32;
+    for (size_t b = 0; b < nb; b++) {
+        const float* v = src + b * 32;
+        uint8_t* o = out + b * Q8_BLOCK_BYTES;
+        float max_abs = 0.0f;
+        for (int i = 0; i < 32; i++) max_abs = fmaxf(max_abs, fabsf(v[i]));
+        uint16_t d = orc_f32_to_f16(max_abs > 0.0f ? max_abs / 127.0f : 1.0f);
+        float scale = orc_f16_to_f32(d);
+        o[0] = (uint8_t)(d & 0xFF);
+        o[1] = (uint8_t)(d >> 8);
+        for (int i = 0; i < 32; i++) {
+            int32_t q = clamp_i32(sat_f32_to_i32(roundf(v[i] / scale)), -127, 127);
+            o[2 + i] = (uint8_t)(q + 128);
+        }
+    }
+    return nb * Q8_BLOCK_BYTES;
+}
+
+/* dequantize_q8_0, quant.rs:194-206 (Q8_0Block::dequantize, quant.rs:90-95):
+ * floor(len/34) blocks; element i = (u_i - 128) * d in f32 (exact). */
+size_t orc_dequantize_q8_0(const uint8_t* q, size_t q_len, float* out) {
+    size_t nb = q_len / Q8_BLOCK_BYTES;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* blk = q + b * Q8_BLOCK_BYTES;
+        float scale = orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+        for (int i = 0; i < 32; i++) out[b * 32 + i] = (float)((int32_t)blk[2 + i] - 128) * scale;
+    }
+    return nb * 32;
+}
+
+/* matmul_vec_auto's Q8_0 arm, ops.rs:33-36: dequantize_q8_0 then matmul_f32
+ * in its scalar order (kernels.rs:234-241: s += w*x over the row, then
+ * s + (bias or 0.0)); rows are the flattened ranges [r*m, (r+1)*m) of the
+ * dequantised tensor.  Returns -1 (the reference panics) when the buffer
+ * holds fewer than n*m elements, else 0. */
+int orc_matmul_q8_0(float* y, const uint8_t* w, size_t w_len, const float* x, const float* bias,
+                    size_t n, size_t m) {
+    size_t avail = (w_len / Q8_BLOCK_BYTES) * 32;
+    if (avail < n * m) return -1;
+    float* deq = (float*)malloc((avail ? avail : 1) * sizeof(float));
+    if (!deq) return -2;
+    orc_dequantize_q8_0(w, w_len, deq);
+    long long nn = (long long)n;
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (long long r = 0; r < nn; r++) {
+        const float* row = deq + (size_t)r * m;
+        float s = 0.0f;
+        for (size_t j = 0; j < m; j++) s += row[j] * x[j];
+        y[r] = s + (bias ? bias[r] : 0.0f);
+    }
+    free(deq);
+    return 0;
+}
+
+/* fp64 brute force of the same product (the tolerance reference). */
+void orc_matmul_q8_0_f64(double* y, const uint8_t* w, size_t w_len, const float* x,
+                         const float* bias, size_t n, size_t m) {
+    (void)w_len;
+    long long nn = (long long)n;
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (long long r = 0; r < nn; r++) {
+        double s = 0.0;
+        for (size_t j = 0; j < m; j++) {
+            size_t e = (size_t)r * m + j;
+            const uint8_t* blk = w + (e / 32) * Q8_BLOCK_BYTES;
+            double d = (double)orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+            s += (double)((int32_t)blk[2 + e % 32] - 128) * d * (double)x[j];
+        }
+        y[r] = s + (bias ? (double)bias[r] : 0.0);
     }
 }

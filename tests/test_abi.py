@@ -45,9 +45,11 @@ def test_host_validation_without_device(lib):
     x = np.zeros(32, np.float32)
     w = np.zeros(18 * 4, np.uint8)
     vp = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
-    # FP32 and Q8_0 are outside this path (ops.rs:30,33)
+    # FP32 is outside this path (ops.rs:30)
     assert lib.hypno_hip_matmul_vec_auto(vp(y), vp(w), w.size, 0, vp(x), None, 4, 32) == 95
-    assert lib.hypno_hip_matmul_vec_auto(vp(y), vp(w), w.size, 2, vp(x), None, 4, 32) == 95
+    # Q8_0: 72 bytes hold 2 blocks = 64 elements < n*m = 128 (a panic in ops.rs:34-35)
+    assert lib.hypno_hip_matmul_vec_auto(vp(y), vp(w), w.size, 2, vp(x), None, 4, 32) == 22
+    assert lib.hypno_hip_matmul_q8_0(vp(y), vp(w), w.size, vp(x), None, 4, 32) == 22
     assert lib.hypno_hip_matmul_vec_auto(vp(y), vp(w), w.size, 7, vp(x), None, 4, 32) == 22
     assert b"dtype" in lib.hypno_hip_last_error()
     # NULL y / x

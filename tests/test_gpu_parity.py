@@ -534,9 +534,12 @@ def test_error_paths(torch, hk, orc):
         hk.matmul_q4_0(torch.empty(n + 1, device="cuda"), q, x, None, n, m)
     with pytest.raises(ValueError):
         hk.matmul_q4_0(y, q, torch.zeros(m - 1, device="cuda"), None, n, m)
-    with pytest.raises(hk.HypnoHipError) as e:
-        hk.matmul_vec_auto(y, q, hk.DType.Q8_0, x, None, n, m)
+    with pytest.raises(hk.HypnoHipError) as e:   # FP32 weights are not on this path
+        hk.matmul_vec_auto(y, q, hk.DType.FP32, x, None, n, m)
     assert e.value.status == 95
+    with pytest.raises(hk.HypnoHipError) as e:   # Q4_0-sized bytes are short for Q8_0
+        hk.matmul_vec_auto(y, q, hk.DType.Q8_0, x, None, n, m)
+    assert e.value.status == 22
     with pytest.raises(hk.HypnoHipError) as e:   # fp16 buffer too short
         hk.matmul_f16(y, torch.zeros(2 * n * m - 2, dtype=torch.uint8, device="cuda"), x, None,
                       n, m)
