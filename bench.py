@@ -23,7 +23,8 @@ Also reported, in the same JSON line:
                 and FP16 at M = 1 and 128; model_load: a TinyLlama-shaped
                 .hypno file opened with its payloads uploaded to HBM
                 (pipelined pinned upload, against a pageable copy and the
-                reference's host-only open).
+                reference's host-only open); q8_0_decode and col_major: the
+                Q8_0 and column-major Q4_0 GEMVs at the Mistral shapes.
 
 Inputs are synthetic: weights N(0, 0.02) from a seeded torch generator,
 quantised on the GPU by the bit-exact Q4_0 quantizer; activations N(0, 1).
@@ -423,6 +424,32 @@ def q8_0_decode(torch, lib):
                         ">= 512 MB of weight copies", "results": out}
 
 
+def col_major(torch, lib):
+    """Column-major Q4_0 (kernels.rs:403-535) at the Mistral-7B shapes, M = 1:
+    W_col[m][n] streamed once per call (plus the fixed-order split
+    reduction), rotating >= 512 MB of weight copies."""
+    out = {}
+    for name, n, m in (("q_o", 4096, 4096), ("gate_up", 14336, 4096), ("down", 4096, 14336)):
+        arena, ptrs, nb = rotating_q4(torch, lib, m, n, seed=n + m)  # m columns of n outputs
+        x = torch.randn(m, device="cuda")
+        y = torch.empty(n, device="cuda")
+        xp, yp = ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr())
+
+        def issue(sp, i, ptrs=ptrs, nb=nb, n=n, m=m):
+            rc = lib.lib.hypno_hip_matmul_q4_0_col_dev(yp, ctypes.c_void_p(ptrs[i % len(ptrs)]),
+                                                       nb, xp, None, n, m, 1, sp)
+            if rc:
+                lib.check(rc, "matmul_q4_0_col")
+
+        us = time_calls_graph(torch, issue, reps=len(ptrs) * 2)
+        out[f"{name}_M1"] = {"us": round(us, 2), "weight_gbs": round(nb / us / 1e3, 1),
+                             "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
+        del arena, x, y
+        torch.cuda.empty_cache()
+    return {"workload": "column-major Q4_0 Mistral-7B projections, M = 1, rotating >= 512 MB "
+                        "of weight copies", "results": out}
+
+
 PCIE_PEAK_GBS = 64.0  # MI355X host link: PCIe 5.0 x16, one direction
 
 
@@ -696,7 +723,7 @@ def main():
         for key, fn in (("c0_single_gemv", single_gemv), ("c2_prefill_gemm", prefill_gemm),
                         ("c3_mistral_stream", mistral_stream), ("c3_m_sweep", mistral_m_sweep),
                         ("c4_lm_head", lm_head), ("model_load", model_load),
-                        ("q8_0_decode", q8_0_decode)):
+                        ("q8_0_decode", q8_0_decode), ("col_major", col_major)):
             print(f"[bench] secondary: {key}", file=sys.stderr, flush=True)
             sec[key] = fn(torch, lib)
         line["secondary"] = sec

@@ -14,8 +14,10 @@ from .kernels import (  # noqa: F401
     device_count,
     matmul_f16,
     matmul_q4_0,
+    matmul_q4_0_col,
     matmul_q8_0,
     matmul_vec_auto,
+    matmul_vec_col,
     matmul_vec_f16,
     matmul_vec_q4_0,
     quantize_f32_to_q4_0,

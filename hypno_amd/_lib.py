@@ -23,6 +23,10 @@ SIGNATURES = {
     "hypno_hip_matmul_q8_0": (_i, [_vp, _vp, _sz, _vp, _vp, _sz, _sz]),
     "hypno_hip_matmul_vec_auto": (_i, [_vp, _vp, _sz, _u32, _vp, _vp, _sz, _sz]),
     "hypno_hip_batch_matmul": (_i, [_vp, _vp, _sz, _u32, _vp, _sz, _sz, _sz]),
+    "hypno_hip_matmul_q4_0_col": (_i, [_vp, _vp, _sz, _vp, _vp, _sz, _sz]),
+    "hypno_hip_matmul_vec_col": (_i, [_vp, _vp, _sz, _u32, _vp, _vp, _sz, _sz]),
+    "hypno_hip_batch_matmul_col": (_i, [_vp, _vp, _sz, _u32, _vp, _sz, _sz, _sz]),
+    "hypno_hip_matmul_q4_0_col_dev": (_i, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _vp]),
     "hypno_hip_weight_register": (_i, [_vp, _sz]),
     "hypno_hip_weight_unregister": (_i, [_vp]),
     "hypno_hip_matmul_q4_0_dev": (_i, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _vp]),

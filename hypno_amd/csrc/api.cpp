@@ -211,6 +211,41 @@ int q8_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
   return HYPNO_HIP_OK;
 }
 
+// Column-major Q4_0 (kernels.rs:403-535): tokens one by one, as
+// turbo.rs:322-326 does.
+int q4_0_col_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const float* bias,
+                 size_t n, size_t m, size_t batch, hipStream_t s) {
+  if (n == 0 || batch == 0) return HYPNO_HIP_OK;
+  if (!y || (!x && m)) return fail(HYPNO_HIP_EINVAL, "y and x must not be NULL");
+  if (!w && w_len) return fail(HYPNO_HIP_EINVAL, "w_q is NULL but w_len > 0");
+  if (mul_overflows(n, batch) || mul_overflows(m, batch) || m > 0x7FFFFFFF ||
+      n / kBlockElems > 0x7FFFFFFF)
+    return fail(HYPNO_HIP_EINVAL, "shape out of range");
+  int cus = 256;
+  DeviceState* ds = nullptr;
+  {
+    std::lock_guard<std::mutex> g(g_mu);
+    int st = device_state(&ds);
+    if (st) return st;
+    cus = ds->cus;
+  }
+  void* ws = nullptr;
+  const size_t wsb = q4_0_col_workspace_bytes(n, m, cus);
+  hipError_t e;
+  if (wsb) {
+    std::lock_guard<std::mutex> g(g_mu);
+    DevBuf& b = ds->workspaces[s];
+    e = ensure(b, wsb, s);
+    if (e != hipSuccess) return hip_fail(e, "column-major workspace");
+    ws = b.p;
+  }
+  for (size_t t = 0; t < batch; t++) {
+    e = launch_q4_0_col(y + t * n, w, w_len, x + t * m, bias, n, m, ws, cus, s);
+    if (e != hipSuccess) return hip_fail(e, "column-major Q4_0 launch");
+  }
+  return HYPNO_HIP_OK;
+}
+
 int f16_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const float* bias,
             size_t n, size_t m, size_t batch, hipStream_t s) {
   if (n == 0 || batch == 0) return HYPNO_HIP_OK;
@@ -259,7 +294,7 @@ int f16_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const floa
 // --- host-slice path ----------------------------------------------------------
 
 int host_matmul(float* y, const uint8_t* w, size_t w_len, uint32_t dtype, const float* x,
-                const float* bias, size_t n, size_t m, size_t batch) {
+                const float* bias, size_t n, size_t m, size_t batch, bool col = false) {
   if (dtype == HYPNO_DTYPE_FP32)
     return fail(HYPNO_HIP_ENOTSUP, "dtype %u is not on the quantised/FP16 path", dtype);
   if (dtype != HYPNO_DTYPE_Q4_0 && dtype != HYPNO_DTYPE_FP16 && dtype != HYPNO_DTYPE_Q8_0)
@@ -316,7 +351,9 @@ int host_matmul(float* y, const uint8_t* w, size_t w_len, uint32_t dtype, const 
       return hip_fail(e, "bias upload");
     db = (float*)ds->bias.p;
   }
-  if (dtype == HYPNO_DTYPE_Q4_0)
+  if (dtype == HYPNO_DTYPE_Q4_0 && col)
+    st = q4_0_col_dev((float*)ds->y.p, dw, w_len, (const float*)ds->x.p, db, n, m, batch, s);
+  else if (dtype == HYPNO_DTYPE_Q4_0)
     st = q4_0_dev((float*)ds->y.p, dw, w_len, (const float*)ds->x.p, db, n, m, batch, s);
   else if (dtype == HYPNO_DTYPE_Q8_0)
     st = q8_0_dev((float*)ds->y.p, dw, w_len, (const float*)ds->x.p, db, n, m, batch, s);
@@ -394,6 +431,27 @@ int hypno_hip_matmul_vec_auto(float* y, const uint8_t* w, size_t w_len, uint32_t
 int hypno_hip_batch_matmul(float* y, const uint8_t* w, size_t w_len, uint32_t dtype,
                            const float* x, size_t n, size_t dim, size_t batch) {
   return host_matmul(y, w, w_len, dtype, x, nullptr, n, dim, batch);
+}
+
+int hypno_hip_matmul_q4_0_col(float* y, const uint8_t* w_q, size_t w_len, const float* x,
+                              const float* bias, size_t n, size_t m) {
+  return host_matmul(y, w_q, w_len, HYPNO_DTYPE_Q4_0, x, bias, n, m, 1, true);
+}
+
+int hypno_hip_matmul_vec_col(float* y, const uint8_t* w, size_t w_len, uint32_t dtype,
+                             const float* x, const float* bias, size_t n, size_t m) {
+  return host_matmul(y, w, w_len, dtype, x, bias, n, m, 1, true);
+}
+
+int hypno_hip_batch_matmul_col(float* y, const uint8_t* w, size_t w_len, uint32_t dtype,
+                               const float* x, size_t n, size_t dim, size_t batch) {
+  return host_matmul(y, w, w_len, dtype, x, nullptr, n, dim, batch, true);
+}
+
+int hypno_hip_matmul_q4_0_col_dev(float* y, const uint8_t* w_q, size_t w_len, const float* x,
+                                  const float* bias, size_t n, size_t m, size_t batch,
+                                  void* stream) {
+  return q4_0_col_dev(y, w_q, w_len, x, bias, n, m, batch, (hipStream_t)stream);
 }
 
 int hypno_hip_weight_register(const uint8_t* host, size_t len) {

@@ -32,7 +32,7 @@ __all__ = [
     "matmul_vec_f16", "matmul_vec_auto", "batch_matmul", "quantize_f32_to_q4_0",
     "dequantize_q4_0", "register_weight", "unregister_weight", "device_count", "GemvPlan",
     "rms_norm", "rms_norm_in_place", "silu_mul", "matmul_q8_0", "quantize_f32_to_q8_0",
-    "dequantize_q8_0",
+    "dequantize_q8_0", "matmul_q4_0_col", "matmul_vec_col",
 ]
 
 
@@ -119,7 +119,7 @@ def _check_lengths(y, x, bias, n, m, batch):
         raise ValueError(f"bias has {_numel(bias)} elements, expected at least {n}")
 
 
-def _matmul(y, w, dtype: DType, x, bias, n: int, m: int, batch: int) -> None:
+def _matmul(y, w, dtype: DType, x, bias, n: int, m: int, batch: int, col: bool = False) -> None:
     _check_lengths(y, x, bias, n, m, batch)
     lib = load()
     tensors = [a for a in (y, w, x, bias) if a is not None]
@@ -129,7 +129,8 @@ def _matmul(y, w, dtype: DType, x, bias, n: int, m: int, batch: int) -> None:
         wp = _dev_ptr(w, "u8", "w")
         xp = _dev_ptr(x, "f32", "x")
         bp = _dev_ptr(bias, "f32", "bias") if bias is not None else None
-        fn = {DType.Q4_0: lib.hypno_hip_matmul_q4_0_dev,
+        fn = {DType.Q4_0: (lib.hypno_hip_matmul_q4_0_col_dev if col
+                           else lib.hypno_hip_matmul_q4_0_dev),
               DType.Q8_0: lib.hypno_hip_matmul_q8_0_dev,
               DType.FP16: lib.hypno_hip_matmul_f16_dev}.get(dtype)
         if fn is None:
@@ -144,13 +145,13 @@ def _matmul(y, w, dtype: DType, x, bias, n: int, m: int, batch: int) -> None:
     xp = _host_ptr(x, np.float32, "x")
     bp = _host_ptr(bias, np.float32, "bias") if bias is not None else None
     if batch == 1:
-        check(lib.hypno_hip_matmul_vec_auto(yp, wp, w.nbytes, int(dtype), xp, bp, n, m),
-              f"matmul {dtype.name}")
+        fn = lib.hypno_hip_matmul_vec_col if col else lib.hypno_hip_matmul_vec_auto
+        check(fn(yp, wp, w.nbytes, int(dtype), xp, bp, n, m), f"matmul {dtype.name}")
     else:
         if bias is not None:
             raise ValueError("batch_matmul takes no bias (turbo.rs:306-333)")
-        check(lib.hypno_hip_batch_matmul(yp, wp, w.nbytes, int(dtype), xp, n, m, batch),
-              f"batch_matmul {dtype.name}")
+        fn = lib.hypno_hip_batch_matmul_col if col else lib.hypno_hip_batch_matmul
+        check(fn(yp, wp, w.nbytes, int(dtype), xp, n, m, batch), f"batch_matmul {dtype.name}")
 
 
 # --- the reference's entry points --------------------------------------------------
@@ -169,6 +170,22 @@ def matmul_q8_0(y, w_q, x, bias, n: int, m: int) -> None:
     """y[n] = dequantize_q8_0(W_q)[n][m] . x[m] (+ bias): the Q8_0 arm of
     matmul_vec_auto (ops.rs:33-36), streamed instead of dequantised."""
     _matmul(y, w_q, DType.Q8_0, x, bias, n, m, 1)
+
+
+def matmul_q4_0_col(y, w_q, x, bias, n: int, m: int) -> None:
+    """Column-major Q4_0 (kernels.rs:414-535): w_q holds W_col[m][n] — for each
+    input index k, n outputs quantised in blocks along n — and
+    y[j] = sum_k W_col[k][j] * x[k] (+ bias)."""
+    _matmul(y, w_q, DType.Q4_0, x, bias, n, m, 1, col=True)
+
+
+def matmul_vec_col(y, w, dtype, x, bias, n: int, m: int) -> None:
+    """ops::matmul_vec_col (ops.rs:41-51): Q4_0 column-major, other dtypes as
+    matmul_vec_auto."""
+    dtype = DType(int(dtype))
+    if dtype not in (DType.Q4_0, DType.Q8_0, DType.FP16):
+        raise HypnoHipError(95, f"matmul_vec_col dtype {dtype.name}")
+    _matmul(y, w, dtype, x, bias, n, m, 1, col=True)
 
 
 def matmul_vec_q4_0(y, w_q, x, bias, n: int, m: int) -> None:
@@ -191,15 +208,13 @@ def matmul_vec_auto(y, w, dtype, x, bias, n: int, m: int) -> None:
 
 
 def batch_matmul(y, w, dtype, x, n: int, dim: int, batch: int, col_major: bool = False) -> None:
-    """turbo::batch_matmul (turbo.rs:306-343) for FP16 / Q4_0 / Q8_0 row-major weights:
-    X[batch][dim] -> Y[batch][n] in one GPU call.  The column-major Q4_0 layout
-    (kernels.rs:403-535) is outside this path and raises."""
+    """turbo::batch_matmul (turbo.rs:306-343) for FP16 / Q4_0 / Q8_0 weights:
+    X[batch][dim] -> Y[batch][n] in one call; col_major selects the
+    column-major Q4_0 kernel (turbo.rs:322-326; other dtypes ignore it)."""
     dtype = DType(int(dtype))
-    if col_major:
-        raise HypnoHipError(95, "batch_matmul col_major")
     if dtype not in (DType.Q4_0, DType.Q8_0, DType.FP16):
         raise HypnoHipError(95, f"batch_matmul dtype {dtype.name}")
-    _matmul(y, w, dtype, x, None, n, dim, batch)
+    _matmul(y, w, dtype, x, None, n, dim, batch, col=bool(col_major))
 
 
 # --- codec (device) ---------------------------------------------------------------

@@ -102,6 +102,26 @@ int hypno_hip_matmul_vec_auto(float* y, const uint8_t* w, size_t w_len, uint32_t
 int hypno_hip_batch_matmul(float* y, const uint8_t* w, size_t w_len, uint32_t dtype,
                            const float* x, size_t n, size_t dim, size_t batch);
 
+/* Replaces kernels::matmul_q4_0_col(y, w_q, x, bias, n, m) (kernels.rs:414-535),
+ * the kernel a col_major model uses (loader.rs:166-168): w_q holds W_col[m][n]
+ * (for each input index k, n outputs in Q4_0 blocks along n; floor(n/32)
+ * blocks per k, outputs past 32*floor(n/32) get only the bias), and
+ * y[j] = sum_k W_col[k][j] * x[k] (+ bias).  Blocks past a short buffer
+ * contribute nothing.  Fixed summation order (the reference's AVX2 form
+ * depends on the thread count). */
+int hypno_hip_matmul_q4_0_col(float* y, const uint8_t* w_q, size_t w_len, const float* x,
+                              const float* bias, size_t n, size_t m);
+
+/* Replaces ops::matmul_vec_col (ops.rs:41-51): Q4_0 -> the column-major
+ * kernel, every other dtype as hypno_hip_matmul_vec_auto. */
+int hypno_hip_matmul_vec_col(float* y, const uint8_t* w, size_t w_len, uint32_t dtype,
+                             const float* x, const float* bias, size_t n, size_t m);
+
+/* turbo::batch_matmul with col_major = true (turbo.rs:322-326): Q4_0 weights
+ * are column-major, other dtypes as hypno_hip_batch_matmul. */
+int hypno_hip_batch_matmul_col(float* y, const uint8_t* w, size_t w_len, uint32_t dtype,
+                               const float* x, size_t n, size_t dim, size_t batch);
+
 /* ---------------------------------------------------------------------------
  * Weight residency.  hypno hands the kernel zero-copy slices of a read-only
  * mmap (loader.rs:139-148).  Registering such a slice uploads it once; later
@@ -124,6 +144,12 @@ int hypno_hip_weight_unregister(const uint8_t* host);
 int hypno_hip_matmul_q4_0_dev(float* y, const uint8_t* w_q, size_t w_len, const float* x,
                               const float* bias, size_t n, size_t m, size_t batch,
                               void* stream);
+
+/* Column-major Q4_0 on device pointers (semantics of
+ * hypno_hip_matmul_q4_0_col; batch > 1: token by token, turbo.rs:322-326). */
+int hypno_hip_matmul_q4_0_col_dev(float* y, const uint8_t* w_q, size_t w_len, const float* x,
+                                  const float* bias, size_t n, size_t m, size_t batch,
+                                  void* stream);
 
 /* Same with FP16 W (kernels.rs:571; turbo.rs:316-320). */
 int hypno_hip_matmul_f16_dev(float* y, const uint8_t* w, size_t w_len, const float* x,

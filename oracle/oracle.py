@@ -61,6 +61,10 @@ def lib():
     L.orc_matmul_q8_0.restype = ctypes.c_int
     L.orc_matmul_q8_0_f64.argtypes = [vp, vp, sz, vp, vp, sz, sz]
     L.orc_matmul_q8_0_f64.restype = None
+    L.orc_matmul_q4_0_col.argtypes = [vp, vp, sz, vp, vp, sz, sz]
+    L.orc_matmul_q4_0_col.restype = None
+    L.orc_matmul_q4_0_col_f64.argtypes = [vp, vp, sz, vp, vp, sz, sz]
+    L.orc_matmul_q4_0_col_f64.restype = None
     for name in ("orc_matmul_q4_0", "orc_matmul_q4_0_scalar", "orc_matmul_q4_0_avx2",
                  "orc_matmul_f16", "orc_matmul_f16_scalar", "orc_matmul_f16_avx2"):
         getattr(L, name).argtypes = [vp, vp, sz, vp, vp, sz, sz]
@@ -324,4 +328,23 @@ def matmul_q8_0_f64(w_q, x, bias, n, m) -> np.ndarray:
     b = _c(bias, np.float32) if bias is not None else None
     y = np.empty(n, np.float64)
     lib().orc_matmul_q8_0_f64(_p(y), _p(w), w.size, _p(xx), _p(b), n, m)
+    return y
+
+
+def matmul_q4_0_col(w_q, x, bias, n, m) -> np.ndarray:
+    """matmul_q4_0_col_scalar (kernels.rs:506-535): W_col[m][n], y[n]."""
+    w = _c(w_q, np.uint8).ravel()
+    xx = _c(x, np.float32).ravel()
+    b = _c(bias, np.float32) if bias is not None else None
+    y = np.empty(n, np.float32)
+    lib().orc_matmul_q4_0_col(_p(y), _p(w), w.size, _p(xx), _p(b), n, m)
+    return y
+
+
+def matmul_q4_0_col_f64(w_q, x, bias, n, m) -> np.ndarray:
+    w = _c(w_q, np.uint8).ravel()
+    xx = _c(x, np.float32).ravel()
+    b = _c(bias, np.float32) if bias is not None else None
+    y = np.empty(n, np.float64)
+    lib().orc_matmul_q4_0_col_f64(_p(y), _p(w), w.size, _p(xx), _p(b), n, m)
     return y

@@ -33,6 +33,10 @@
  *   orc_matmul_q8_0     dequantize + matmul_f32_scalar order; fp64 brute
  *                       force and exact integer cases (the AVX2 / AVX-512
  *                       f32 orders are not restated: tolerance-based)
+ *   orc_matmul_q4_0_col matmul_q4_0_col_scalar order; no reference test
+ *                       checks it numerically: exact integer cases, fp64,
+ *                       n % 32 != 0 tails and short buffers (the AVX2 form's
+ *                       bits depend on the thread count: not restated)
  *   orc_rms_norm_*      reference KATs ops.rs:131-136, turbo.rs:716-735 (the
  *                       f64 batch_rms_norm within 1e-6 of the SIMD form),
  *                       turbo.rs:924-951; closed forms (constant rows, the
@@ -646,5 +650,57 @@ void orc_matmul_q8_0_f64(double* y, const uint8_t* w, size_t w_len, const float*
             s += (double)((int32_t)blk[2 + e % 32] - 128) * d * (double)x[j];
         }
         y[r] = s + (bias ? (double)bias[r] : 0.0);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Column-major Q4_0 (kernels.rs:403-535)                                     */
+/* ------------------------------------------------------------------------ */
+
+/* matmul_q4_0_col_scalar, kernels.rs:506-535: y = 0; for each input index k,
+ * blocks_per_col = n / 32 blocks of column k (byte offset k * nb * 18), each
+ * adding deq * x[k] to y[32b + i] (i < n); a block past w_len ends column k
+ * (and, offsets only growing, every later one); then y += bias. */
+void orc_matmul_q4_0_col(float* y, const uint8_t* w, size_t w_len, const float* x,
+                         const float* bias, size_t n, size_t m) {
+    size_t nb = n / 32;
+    size_t col_bytes = nb * Q4_BLOCK_BYTES;
+    for (size_t i = 0; i < n; i++) y[i] = 0.0f;
+    for (size_t k = 0; k < m; k++) {
+        float xk = x[k];
+        for (size_t b = 0; b < nb; b++) {
+            size_t bo = k * col_bytes + b * Q4_BLOCK_BYTES;
+            if (bo + Q4_BLOCK_BYTES > w_len) break;
+            float scale = orc_f16_to_f32((uint16_t)(w[bo] | (w[bo + 1] << 8)));
+            for (int i = 0; i < 16; i++) {
+                uint8_t byte = w[bo + 2 + i];
+                float v0 = (float)((int32_t)(byte & 0x0F) - 8) * scale;
+                float v1 = (float)((int32_t)((byte >> 4) & 0x0F) - 8) * scale;
+                size_t r = b * 32 + 2 * (size_t)i;
+                if (r < n) y[r] += v0 * xk;
+                if (r + 1 < n) y[r + 1] += v1 * xk;
+            }
+        }
+    }
+    if (bias)
+        for (size_t i = 0; i < n; i++) y[i] += bias[i];
+}
+
+/* fp64 of the same sum (the tolerance reference). */
+void orc_matmul_q4_0_col_f64(double* y, const uint8_t* w, size_t w_len, const float* x,
+                             const float* bias, size_t n, size_t m) {
+    size_t nb = n / 32;
+    for (size_t i = 0; i < n; i++) y[i] = bias ? (double)bias[i] : 0.0;
+    for (size_t k = 0; k < m; k++) {
+        for (size_t b = 0; b < nb; b++) {
+            size_t bo = (k * nb + b) * Q4_BLOCK_BYTES;
+            if (bo + Q4_BLOCK_BYTES > w_len) break;
+            double d = (double)orc_f16_to_f32((uint16_t)(w[bo] | (w[bo + 1] << 8)));
+            for (int i = 0; i < 32; i++) {
+                uint8_t byte = w[bo + 2 + i / 2];
+                int q = (int)((i & 1) ? (byte >> 4) : (byte & 0x0F)) - 8;
+                y[b * 32 + i] += (double)q * d * (double)x[k];
+            }
+        }
     }
 }

@@ -72,9 +72,10 @@ def test_python_mirror_validation():
         hk.matmul_q4_0(np.zeros(4, np.float32), w, x[:31], None, 4, 32)
     with pytest.raises(ValueError):
         hk.matmul_q4_0(np.zeros(4, np.float64), w, x, None, 4, 32)
-    with pytest.raises(hk.HypnoHipError):
-        hk.batch_matmul(np.zeros(8, np.float32), w, hk.DType.Q4_0, np.zeros(64, np.float32),
+    with pytest.raises(hk.HypnoHipError) as e:   # FP32 weights are not on this path
+        hk.batch_matmul(np.zeros(8, np.float32), w, hk.DType.FP32, np.zeros(64, np.float32),
                         4, 32, 2, col_major=True)
+    assert e.value.status == 95
     assert hk.DType.Q4_0.data_bytes(32) == 18 and hk.DType.Q4_0.data_bytes(33) == 36
     assert hk.DType.FP16.data_bytes(10) == 20 and int(hk.DType.Q4_0) == 3
 
