@@ -253,7 +253,9 @@ struct RingCursor {
 
 __device__ __forceinline__ int job_steps(const GemvJob& J) { return (J.n + J.rps - 1) / J.rps; }
 
-template <int F>
+// PRO: some job of the launch has a prologue (a separate instantiation, so
+// launches without one keep the smaller staging code and register budget).
+template <int F, bool PRO>
 __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
   using FT = Fmt<F>;
   using Slot = typename FT::Slot;
@@ -496,39 +498,25 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
       }
       if ((i & 3) == 0) exps[i >> 2] = mb >= 0x7F800000u ? kBadExp : e - kMantBits;
     };
-    if (B * 4 <= T) {
-      // One group per thread at most: x and the prologue operand are read
-      // once and stay in registers across the RMS reduction.
-      const bool act = t < B * 4;
-      float xs[8] = {}, as[8] = {};
-      if (act) {
-        load8(xv, t, xs);
-        if (J.pro != kProNone) load8(av, t, as);
-      }
-      float inv_rms = 1.0f;
-      if (J.pro == kProRmsNorm) inv_rms = inv_rms_of(sumsq8(xs, 0.0f));
-      if (act) {
-        prologue(xs, as, inv_rms);
-        convert(t, xs);
-      }
-    } else {
-      float inv_rms = 1.0f;
-      if (J.pro == kProRmsNorm) {
-        float ss = 0.0f;
-        for (int i = t; i < B * 4; i += T) {
-          float xs[8];
-          load8(xv, i, xs);
-          ss = sumsq8(xs, ss);
-        }
-        inv_rms = inv_rms_of(ss);
-      }
-      for (int i = t; i < B * 4; i += T) {  // whole 4-thread groups stay together
-        float xs[8], as[8];
+    float inv_rms = 1.0f;
+    if (PRO && J.pro == kProRmsNorm) {
+      float ss = 0.0f;
+      for (int i = t; i < B * 4; i += T) {
+        float xs[8];
         load8(xv, i, xs);
+        ss = sumsq8(xs, ss);
+      }
+      inv_rms = inv_rms_of(ss);
+    }
+    for (int i = t; i < B * 4; i += T) {  // whole 4-thread groups stay together
+      float xs[8];
+      load8(xv, i, xs);
+      if constexpr (PRO) {
+        float as[8];
         if (J.pro != kProNone) load8(av, i, as);
         prologue(xs, as, inv_rms);
-        convert(i, xs);
       }
+      convert(i, xs);
     }
     __syncthreads();
     const int kb = t % B;
@@ -543,7 +531,7 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
   };
 
   // One step: close the chunk / switch job when due (uniform branches),
-  // refill the ring slot with the step kDepth ahead (returned), decode this
+  // refill the ring slot with the step three ahead (returned), decode this
   // lane's block and park its 8-lane group sum.
   auto step = [&](int ss, const Slot sl) -> Slot {
     if (ss == seg_end) {
@@ -619,26 +607,32 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
 }
 
 __global__ void __launch_bounds__(1024) q4_0_gemv_jobs_kernel(GemvLaunch L) {
-  gemv_jobs_body<kFmtQ4_0>(L);
+  gemv_jobs_body<kFmtQ4_0, false>(L);
+}
+
+__global__ void __launch_bounds__(1024) q4_0_gemv_jobs_pro_kernel(GemvLaunch L) {
+  gemv_jobs_body<kFmtQ4_0, true>(L);
 }
 
 __global__ void __launch_bounds__(1024) q8_0_gemv_jobs_kernel(GemvLaunch L) {
-  gemv_jobs_body<kFmtQ8_0>(L);
+  gemv_jobs_body<kFmtQ8_0, false>(L);
 }
 
-static bool g_lds_attr_set[2] = {false, false};
+static bool g_lds_attr_set[3] = {false, false, false};
 
 hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
                                   const GemvJob& job0, int njobs, int total_steps, int num_cus,
                                   hipStream_t s) {
   const bool q8 = g.fmt == kFmtQ8_0;
-  const void* kern = q8 ? reinterpret_cast<const void*>(q8_0_gemv_jobs_kernel)
-                        : reinterpret_cast<const void*>(q4_0_gemv_jobs_kernel);
-  if (!g_lds_attr_set[q8]) {
+  const int which = q8 ? 2 : (g.pro ? 1 : 0);
+  const void* kern = which == 2   ? reinterpret_cast<const void*>(q8_0_gemv_jobs_kernel)
+                     : which == 1 ? reinterpret_cast<const void*>(q4_0_gemv_jobs_pro_kernel)
+                                  : reinterpret_cast<const void*>(q4_0_gemv_jobs_kernel);
+  if (!g_lds_attr_set[which]) {
     hipError_t e =
         hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
     if (e != hipSuccess) return e;
-    g_lds_attr_set[q8] = true;
+    g_lds_attr_set[which] = true;
   }
   // As many work-groups as can be resident at once (registers and LDS).
   int per_cu = 0;
@@ -668,8 +662,10 @@ hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
   L.njobs = njobs;
   L.total_steps = total_steps;
   L.S = g.S;
-  if (q8)
+  if (which == 2)
     hipLaunchKernelGGL(q8_0_gemv_jobs_kernel, dim3(grid), dim3(g.T), g.lds, s, L);
+  else if (which == 1)
+    hipLaunchKernelGGL(q4_0_gemv_jobs_pro_kernel, dim3(grid), dim3(g.T), g.lds, s, L);
   else
     hipLaunchKernelGGL(q4_0_gemv_jobs_kernel, dim3(grid), dim3(g.T), g.lds, s, L);
   return hipGetLastError();
