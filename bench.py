@@ -418,10 +418,30 @@ def q8_0_decode(torch, lib):
         us = time_calls_graph(torch, issue, reps=copies * 4)
         out[f"{name}_M1"] = {"us": round(us, 2), "weight_gbs": round(nb / us / 1e3, 1),
                              "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
+        if name == "gate_up":
+            # prefill: weights expanded to fp16 once per call, fp16 MFMA GEMM
+            M = 512
+            xm = torch.randn(M, m, generator=gen, device="cuda")
+            ym = torch.empty(M, n, device="cuda")
+            xmp, ymp = ctypes.c_void_p(xm.data_ptr()), ctypes.c_void_p(ym.data_ptr())
+
+            def issue_m(sp, i, base=base, nb=nb, n=n, m=m):
+                rc = lib.lib.hypno_hip_matmul_q8_0_dev(ymp, ctypes.c_void_p(base), nb, xmp,
+                                                       None, n, m, M, sp)
+                if rc:
+                    lib.check(rc, "matmul_q8_0 M=512")
+
+            us = time_calls_graph(torch, issue_m, reps=5)
+            out[f"{name}_M{M}"] = {"us": round(us, 2),
+                                   "tflops": round(2.0 * M * n * m / us / 1e6, 2),
+                                   "frac_fp16_peak": round(2.0 * M * n * m / us / 1e6 /
+                                                           FP16_PEAK_TFLOPS, 4)}
+            del xm, ym
         del arena, x, y
         torch.cuda.empty_cache()
     return {"workload": "Q8_0 Mistral-7B projections, M = 1, one call per matrix, rotating "
-                        ">= 512 MB of weight copies", "results": out}
+                        ">= 512 MB of weight copies; gate/up also at M = 512 (prefill: fp16 "
+                        "expansion + fp16 GEMM, per call)", "results": out}
 
 
 def col_major(torch, lib):

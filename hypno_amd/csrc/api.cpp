@@ -179,7 +179,9 @@ int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
 
 // Q8_0 (ops.rs:33-36, turbo.rs:334-341): the reference dequantises the
 // whole tensor and slices rows of it, so a buffer shorter than n*m elements
-// is a panic there (EINVAL here).  Tokens go one by one through the GEMV.
+// is a panic there (EINVAL here).  From 16 tokens the fp16 GEMM path runs
+// (weights expanded to fp16 once per call); fewer go token by token through
+// the GEMV.
 int q8_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const float* bias,
              size_t n, size_t m, size_t batch, hipStream_t s) {
   if (n == 0 || batch == 0) return HYPNO_HIP_OK;
@@ -199,6 +201,22 @@ int q8_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
     cus = ds->cus;
   }
   hipError_t e;
+  if (batch >= kGemmMinBatch && q8_0_gemm_ok(n, m, batch)) {
+    void* ws = nullptr;
+    {
+      std::lock_guard<std::mutex> g(g_mu);
+      DeviceState* ds = nullptr;
+      int st = device_state(&ds);
+      if (st) return st;
+      DevBuf& b = ds->workspaces[s];
+      e = ensure(b, q8_0_gemm_workspace_bytes(batch, n, m, cus), s);
+      if (e != hipSuccess) return hip_fail(e, "Q8_0 GEMM workspace");
+      ws = b.p;
+    }
+    e = launch_q8_0_gemm(y, w, x, bias, n, m, batch, ws, cus, s);
+    if (e != hipSuccess) return hip_fail(e, "q8_0 GEMM launch");
+    return HYPNO_HIP_OK;
+  }
   if (q8_0_gemv_fast_ok(w, w_len, n, m) && aligned16(x)) {
     for (size_t t = 0; t < batch; t++) {
       e = launch_q8_0_gemv_fast(y + t * n, w, x + t * m, bias, n, m, cus, s);

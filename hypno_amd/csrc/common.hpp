@@ -154,6 +154,12 @@ hipError_t launch_quantize_q8_0(uint8_t* out, const float* src, size_t n_blocks,
 hipError_t launch_dequantize_q8_0(float* out, const uint8_t* q, size_t n_blocks, hipStream_t s);
 hipError_t launch_q8_0_generic(float* y, const uint8_t* w, const float* x, const float* bias,
                                size_t n, size_t m, size_t batch, hipStream_t s);
+// Q8_0 prefill through fp16 weights and the fp16 GEMM (gemm_q8_0.hip).
+bool q8_0_gemm_ok(size_t n, size_t m, size_t batch);
+size_t q8_0_gemm_workspace_bytes(size_t batch, size_t n, size_t m, int num_cus);
+hipError_t launch_q8_0_gemm(float* y, const uint8_t* w, const float* x, const float* bias,
+                            size_t n, size_t m, size_t batch, void* ws, int num_cus,
+                            hipStream_t s);
 // Q8_0 (34-byte blocks), same conditions with w_len >= n*m/32*34.
 bool q8_0_gemv_fast_ok(const uint8_t* w, size_t w_len, size_t n, size_t m);
 hipError_t launch_q8_0_gemv_fast(float* y, const uint8_t* w, const float* x, const float* bias,

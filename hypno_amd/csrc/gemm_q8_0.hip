@@ -1,0 +1,113 @@
+// Q8_0 prefill (turbo.rs:334-341 dequantises the tensor to fp32 and runs one
+// matmul_f32 per token).  Here, for M >= 16 tokens: the weights are expanded
+// once per call to fp16 in a workspace and the DMA-fed fp16 MFMA GEMM runs on
+// them (gemm_q4.hip), with the activations rounded to fp16 as on the other
+// GEMM paths.
+//
+// Each row n is expanded as (u - 128) * (d / D_n), D_n = the row's largest
+// |d|: every value then lies in [-128, 128], so none overflows fp16 (a plain
+// (u - 128) * d would for |w| > 65504), and each weight is rounded to fp16
+// once (relative 2^-11).  The GEMM output is rescaled by D_n, then the bias
+// added.  A row whose largest |d| is 0 or not finite keeps D_n = 1.
+#include "common.hpp"
+
+namespace hypno {
+
+namespace {
+
+// D[n] = max |d| over the row's blocks (one wave per row).
+__global__ void __launch_bounds__(256)
+q8_0_row_scale_kernel(float* __restrict__ D, const uint8_t* __restrict__ w, size_t n, int bpr) {
+  const size_t row = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (row >= n) return;  // wave-uniform
+  const uint8_t* base = w + row * (size_t)bpr * kQ8BlockBytes;
+  float mx = 0.0f;
+  for (int b = lane; b < bpr; b += 64) {
+    const uint8_t* blk = base + (size_t)b * kQ8BlockBytes;
+    mx = fmaxf(mx, fabsf(f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8))));
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if (lane == 0) D[row] = (mx > 0.0f && mx <= 3.0e38f) ? mx : 1.0f;
+}
+
+// out[row][32 b + i] = fp16((u_i - 128) * (d_b / D[row])), one thread per block.
+__global__ void __launch_bounds__(256)
+q8_0_to_f16_kernel(_Float16* __restrict__ out, const uint8_t* __restrict__ w,
+                   const float* __restrict__ D, size_t n_blocks, int bpr) {
+  const size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= n_blocks) return;
+  const uint8_t* blk = w + g * kQ8BlockBytes;
+  const float d = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+  const float r = d / D[g / bpr];
+  uint32_t p[kBlockElems / 2];
+#pragma unroll
+  for (int i = 0; i < kBlockElems / 2; i++) {
+    const _Float16 lo = (_Float16)((float)((int)blk[2 + 2 * i] - 128) * r);
+    const _Float16 hi = (_Float16)((float)((int)blk[3 + 2 * i] - 128) * r);
+    p[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+  }
+  u32x4* o = reinterpret_cast<u32x4*>(out + g * kBlockElems);  // 64 B per block, 16-aligned
+#pragma unroll
+  for (int q = 0; q < 4; q++) o[q] = u32x4{p[4 * q], p[4 * q + 1], p[4 * q + 2], p[4 * q + 3]};
+}
+
+// y[t][j] = y[t][j] * D[j] (+ bias[j]).
+__global__ void __launch_bounds__(256)
+q8_0_rescale_kernel(float* __restrict__ y, const float* __restrict__ D,
+                    const float* __restrict__ bias, size_t n, size_t total) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t j = i % n;
+    y[i] = y[i] * D[j] + (bias ? bias[j] : 0.0f);
+  }
+}
+
+size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+
+bool mul_overflows_sz(size_t a, size_t b) { return a != 0 && b > SIZE_MAX / 2 / a; }
+
+}  // namespace
+
+bool q8_0_gemm_ok(size_t n, size_t m, size_t batch) {
+  // The fp16 copy sits at the start of a 256-byte-aligned workspace (the
+  // address passed only stands for that alignment); K a multiple of the
+  // GEMM's 64-column stage, so rows hold whole blocks.
+  return m % 64 == 0 && !mul_overflows_sz(n, m) &&
+         f16_gemm_v2_ok(reinterpret_cast<const uint8_t*>((uintptr_t)256), n, m, batch);
+}
+
+size_t q8_0_gemm_workspace_bytes(size_t batch, size_t n, size_t m, int num_cus) {
+  return round256(n * m * 2) + round256(n * 4) + f16_gemm_v2_workspace_bytes(batch, n, m, num_cus);
+}
+
+hipError_t launch_q8_0_gemm(float* y, const uint8_t* w, const float* x, const float* bias,
+                            size_t n, size_t m, size_t batch, void* ws, int num_cus,
+                            hipStream_t s) {
+  uint8_t* base = static_cast<uint8_t*>(ws);
+  _Float16* w16 = reinterpret_cast<_Float16*>(base);
+  float* D = reinterpret_cast<float*>(base + round256(n * m * 2));
+  void* gemm_ws = base + round256(n * m * 2) + round256(n * 4);
+  const int bpr = (int)(m / kBlockElems);
+  hipLaunchKernelGGL(q8_0_row_scale_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, D, w,
+                     n, bpr);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const size_t nblk = n * (size_t)bpr;
+  hipLaunchKernelGGL(q8_0_to_f16_kernel, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, s,
+                     w16, w, D, nblk, bpr);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  e = launch_f16_gemm_v2(y, reinterpret_cast<const uint8_t*>(w16), x, nullptr, n, m, batch,
+                         gemm_ws, num_cus, s);
+  if (e != hipSuccess) return e;
+  const size_t total = n * batch;
+  size_t grid = (total + 255) / 256;
+  if (grid > 8192) grid = 8192;
+  hipLaunchKernelGGL(q8_0_rescale_kernel, dim3((unsigned)grid), dim3(256), 0, s, y, D, bias, n,
+                     total);
+  return hipGetLastError();
+}
+
+}  // namespace hypno

@@ -208,3 +208,50 @@ def test_q8_0_batch_and_host_paths(torch, hk, orc):
         hk.matmul_q8_0(torch.empty(n, device="cuda"), torch.from_numpy(wq[:-34]).cuda(),
                        torch.from_numpy(x[:m]).cuda(), None, n, m)
     assert e.value.status == 22
+
+
+GEMM_TOL = 2e-3  # rel-L2 over all M x N (north_star: MFMA prefill, fp16 activations)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batch,n,m", [(16, 512, 256), (64, 1000, 1024), (128, 4096, 4096),
+                                       (512, 2048, 2048), (20, 3, 64)])
+def test_q8_0_gemm(torch, hk, orc, batch, n, m):
+    """M >= 16 runs the fp16 GEMM on weights expanded to fp16 (per-row
+    normalised): against the per-token fp32 reference on the unrounded x
+    (turbo.rs:334-341 semantics; the fp16 rounding of x and of the weights
+    both count against the tolerance), and the bias on the device path."""
+    print(f"q8_0 gemm batch={batch} n={n} m={m}", flush=True)
+    wq = _q8(orc, batch + n + m, n, m)
+    x = orc.normal_f32(batch * 7 + m, batch * m, 1.0).reshape(batch, m)
+    bias = orc.normal_f32(n + 5, n, 1.0)
+    w64 = orc.dequantize_q8_0(wq)[: n * m].reshape(n, m).astype(np.float64)
+    ref = x.astype(np.float64) @ w64.T + bias           # fp64 of the reference's product
+    for t in (0, batch - 1):                             # and its own per-token form
+        assert orc.rel_l2(orc.matmul_q8_0(wq, x[t], bias, n, m), ref[t]) <= 1e-5
+    y = torch.empty(batch * n, device="cuda")
+    import ctypes
+    from hypno_amd import _lib
+    dw, dx, db = (torch.from_numpy(a).cuda() for a in (wq, np.ascontiguousarray(x), bias))
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _lib.check(_lib.load().hypno_hip_matmul_q8_0_dev(
+        ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(dw.data_ptr()), wq.size,
+        ctypes.c_void_p(dx.data_ptr()), ctypes.c_void_p(db.data_ptr()), n, m, batch, st),
+        "matmul_q8_0_dev")
+    got = y.cpu().numpy().reshape(batch, n)
+    err = orc.rel_l2(got, ref)
+    assert err <= GEMM_TOL, f"rel L2 {err:.3e}"
+    # a weight row with one huge block scale: per-row normalisation keeps the
+    # fp16 expansion finite (|w| up to 127 * 60000 > fp16 max)
+    if (batch, n, m) == (16, 512, 256):
+        big = wq.copy().reshape(-1, 34)
+        big[0, 0:2] = np.frombuffer(np.float16(60000.0).tobytes(), np.uint8)
+        big = big.ravel()
+        refb = x.astype(np.float64) @ orc.dequantize_q8_0(big)[: n * m].reshape(n, m).astype(
+            np.float64).T
+        yb = torch.empty(batch * n, device="cuda")
+        hk.batch_matmul(yb, torch.from_numpy(big).cuda(), hk.DType.Q8_0, dx.reshape(-1), n, m,
+                        batch)
+        gb = yb.cpu().numpy().reshape(batch, n)
+        assert np.all(np.isfinite(gb))
+        assert orc.rel_l2(gb, refb) <= GEMM_TOL
