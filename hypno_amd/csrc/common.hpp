@@ -229,11 +229,13 @@ hipError_t launch_q4_0_gemm(float* y, const uint8_t* w, const float* x, const fl
 hipError_t launch_x_f16_permuted(const float* x, size_t batch, size_t m, void* ws,
                                  hipStream_t s);
 
-// MFMA prefill GEMM, 512-thread 128x128 tiles with K-groups (gemm_q4.hip).
-// Requires m % 128 == 0, w 4-byte aligned, w_len full.  `workspace` as above.
+// MFMA prefill GEMM, 512-thread 128x128 tiles with K-groups (gemm_q4.hip),
+// weights rounded to fp16 after a per-row power-of-two normalisation.
+// Requires m % 256 == 0, w 16-byte aligned, w_len full.
 bool q4_0_gemm_v3_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t batch);
-// Workspace of launch_q4_0_gemm_v3: the fp16 activations, then the K-split
-// partial planes when the tile grid is too small for the chip.
+// Workspace of launch_q4_0_gemm_v3: the fp16 activations, the K-split
+// partial planes when the tile grid is too small for the chip, the per-row
+// scale exponents.
 size_t gemm_v3_workspace_bytes(size_t batch, size_t n, size_t m, int num_cus);
 hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const float* bias,
                                size_t n, size_t m, size_t batch, void* workspace, int num_cus,

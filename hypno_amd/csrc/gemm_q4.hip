@@ -1,13 +1,16 @@
 // Q4_0 batched-prefill GEMM for gfx950: Y[M][N] = X[M][K] . W[N][K]^T (+ bias)
 // with W in hypno's Q4_0 blocks (quant.rs:10-22) and X rounded to fp16.
 //
-// The integer nibbles (nib - 8) go to the matrix cores as exact fp16 values;
-// each 32-column block is one v_mfma_f32_16x16x32_f16 into a zeroed
-// accumulator, and the block's partial sum is scaled by the block's fp32
-// scale into fp32 accumulators (acc += d * partial).  That scale FMA is one
-// VALU op per output per block -- as much issue time as the MFMA itself -- so
-// the kernel keeps other VALU work small and overlaps the FMAs with the
-// matrix pipe:
+// Each weight goes to the matrix cores as fp16 (nib - 8) * (d / D_n), with
+// D_n a power of two just above the largest |d| of weight row n (a pre-pass,
+// q4_0_row_exp_kernel, writes its exponent): every such value lies in
+// (-8, 8), so none overflows fp16, the block scale is applied before the
+// MFMA (one packed fp16 multiply per pair of weights), the MFMAs accumulate
+// straight into fp32 accumulators across blocks, and the output column is
+// multiplied by D_n at the end (exact: a power of two).  Each weight is
+// rounded to fp16 once (relative 2^-11).  Scaling each block's partial sum
+// in fp32 instead costs one VALU FMA per output per block -- as much issue
+// time as the MFMA itself.
 //
 //  * Work-group = 512 threads (8 waves) on a 128 x 128 tile of Y, one per CU,
 //    two waves per SIMD.  A stage is 64 columns of K (two Q4_0 blocks); waves
@@ -28,9 +31,10 @@
 //        row's 36 stage bytes -- a block's scale and 8 nibble bytes, or the
 //        other 8 -- in a two-deep register double buffer.
 //  * Two stages ahead, every thread unpacks its 16 nibbles into exact fp16
-//    (nib - 8) with one and-or op and one packed fp16 op per pair of weights
-//    and writes them, with the block scale as fp32, to a 2-slot B ring in
-//    LDS.  The expansion is shared by all 128 rows of X.
+//    (nib - 8) with one and-or op and one packed fp16 op per pair of weights,
+//    multiplies them by fp16(d / D_n) (one packed fp16 op per pair) and
+//    writes them to a 2-slot B ring in LDS.  The expansion is shared by all
+//    128 rows of X.
 //  * Each MFMA operand register is reloaded from LDS for the next stage
 //    right after its last MFMA of this stage, so LDS latency hides behind
 //    the matrix work.  One barrier per stage.
@@ -61,11 +65,9 @@ constexpr int kARing = kPrefetch;       // stage s+1 read while s+2..s+4 land
 constexpr int kBRing = 2;               // stage s+1 read while s+2 is written
 constexpr int kRowBytes = BK * 2;           // 128 B: one fp16 tile row
 constexpr int kTileBytes = BM * kRowBytes;  // 16 KB
-constexpr int kScaleBytes = 2 * BN * 4;     // 1 KB
 constexpr int kOffA = 0;
 constexpr int kOffB = kOffA + kARing * kTileBytes;
-constexpr int kOffS = kOffB + kBRing * kTileBytes;
-constexpr int kLdsBytes = kOffS + kBRing * kScaleBytes;  // 98 KB (< 160 KB)
+constexpr int kLdsBytes = kOffB + kBRing * kTileBytes;  // 96 KB (< 160 KB)
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 static_assert(4 * 64 * 64 * 4 <= kARing * kTileBytes, "K-group reduction fits in the A ring");
 
@@ -120,7 +122,28 @@ struct Args {
   int xcd_map;        // 1: blockIdx -> tile mapping groups tiles per XCD
   int splits;         // K split over blockIdx.y; > 1: fp32 partials to `part`
   float* part;        // [splits][M][N] partial sums (splits > 1)
+  const int* rowexp;  // [N]: D_n = 2^rowexp[n]
 };
+
+// rowexp[n] = e with 2^(e-1) <= max |d| < 2^e over weight row n's blocks (0
+// when that maximum is 0 or not finite), one wave per row.
+__global__ void __launch_bounds__(256)
+q4_0_row_exp_kernel(int* __restrict__ rowexp, const uint8_t* __restrict__ w, int n, int bpr) {
+  const int row = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= n) return;  // wave-uniform
+  const uint8_t* base = w + (size_t)row * bpr * kBlockBytes;
+  float mx = 0.0f;
+  for (int b = lane; b < bpr; b += 64) {
+    const uint8_t* blk = base + (size_t)b * kBlockBytes;
+    mx = fmaxf(mx, fabsf(f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8))));
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  int e = 0;
+  if (mx > 0.0f && mx <= 3.0e38f) frexpf(mx, &e);
+  if (lane == 0) rowexp[row] = e;
+}
 
 __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a) {
   extern __shared__ __align__(16) uint8_t smem[];
@@ -184,7 +207,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   const uint8_t* erow = a.w + (size_t)min(n0 + er, a.N - 1) * w_row + 16 * eb + 8 * eh;
   const uint32_t boff0 = tile_off(er, 4 * eb + 2 * eh);
   const uint32_t boff1 = tile_off(er, 4 * eb + 2 * eh + 1);
-  const uint32_t soff = (((eb * 2 + (er >> 6)) * 16 + (er & 15)) * 4 + ((er & 63) >> 4)) * 4;
+  const int eexp = evalid ? a.rowexp[n0 + er] : 0;
   using RawW = u32x3;
   auto raw_load = [&](int s) -> RawW {  // stage min(s, steps-1) of this range
     const int g = s0 + (s < steps ? s : steps - 1);
@@ -192,41 +215,47 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   };
   struct Expanded {
     u32x4 lo, hi;
-    float scale;
   };
   auto expand_unpack = [&](const RawW& r) -> Expanded {
+    // fp16(d / D_n): exact while d / D_n is a normal fp16 number (d is fp16,
+    // D_n a power of two); rows past N get 0.  Only the eh = 0 thread's words
+    // hold the block's scale; its eh = 1 partner (the next lane) takes it
+    // with a DPP lane move (quad_perm 0,0,2,2).
+    const uint32_t own = (r.x >> (eb ? 16 : 0)) & 0xFFFFu;
+    const uint32_t dbits = (uint32_t)__builtin_amdgcn_mov_dpp((int)own, 0xA0, 0xF, 0xF, false);
+    const _Float16 h = evalid ? (_Float16)ldexpf(f16_bits_to_f32(dbits), -eexp) : (_Float16)0.0f;
+    const half2v hh = {h, h};
+    const u32x4 lo = unpack8(__builtin_amdgcn_perm(r.y, r.x, esel));
+    const u32x4 hi = unpack8(__builtin_amdgcn_perm(r.z, r.y, esel));
+    // (__builtin_bit_cast of a vector element reads element 0 under this
+    // compiler, so each word is copied to a scalar first.)
     Expanded e;
-    e.lo = unpack8(__builtin_amdgcn_perm(r.y, r.x, esel));
-    e.hi = unpack8(__builtin_amdgcn_perm(r.z, r.y, esel));
-    const uint32_t dbits = (r.x >> (eb ? 16 : 0)) & 0xFFFFu;
-    e.scale = evalid ? f16_bits_to_f32(dbits) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t wl = lo[i], wh = hi[i];
+      e.lo[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, wl) * hh);
+      e.hi[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, wh) * hh);
+    }
     return e;
   };
   auto expand_write = [&](int s, const Expanded& e) {
     uint8_t* bt = smem + kOffB + (s % kBRing) * kTileBytes;
     *reinterpret_cast<u32x4*>(bt + boff0) = e.lo;
     *reinterpret_cast<u32x4*>(bt + boff1) = e.hi;
-    if (eh == 0)
-      *reinterpret_cast<float*>(smem + kOffS + (s % kBRing) * kScaleBytes + soff) = e.scale;
   };
   auto expand = [&](int s, const RawW& r) { expand_write(s, expand_unpack(r)); };
 
   // MFMA operands of this wave's block (kb = kgrp) of one stage: one
   // register set for A and one for B, each operand reloaded in place for the
-  // next stage right after its last MFMA of this stage; the block scales are
-  // double-buffered.
+  // next stage right after its last MFMA of this stage.
   const uint32_t fchunk = ((4 * kgrp + lq) ^ ((lr >> 1) & 7)) << 4;
   const uint32_t fa_off = (wm * 64 + lr) * kRowBytes + fchunk;
   const uint32_t fb_off = (wn * 64 + lr) * kRowBytes + fchunk;
-  const uint32_t fs_off = ((kgrp * 2 + wn) * 16 + lr) * 16;
   auto a_addr = [&](int s, int i) -> uint32_t {
     return (uint32_t)(kOffA + (s % kARing) * kTileBytes) + fa_off + i * 16 * kRowBytes;
   };
   auto b_addr = [&](int s, int j) -> uint32_t {
     return (uint32_t)(kOffB + (s % kBRing) * kTileBytes) + fb_off + j * 16 * kRowBytes;
-  };
-  auto read_sc = [&](int s) -> floatx4 {
-    return *reinterpret_cast<const floatx4*>(smem + kOffS + (s % kBRing) * kScaleBytes + fs_off);
   };
 
   floatx4 acc[4][4];
@@ -235,54 +264,30 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // Stage s's MFMAs.  MFMA q = 4i + j; its partial is scaled in after MFMA
-  // q + kLag has been issued, so the FMAs do not wait on the matrix pipe and
-  // at most kLag + 2 partials are live.  The order is pinned by one empty
-  // asm statement per step (the default schedule would issue all MFMAs first
-  // and hold every partial at once, or scale a partial right behind its own
-  // MFMA and stall): statement q comes after MFMA q (it reads partial q),
-  // after the FMAs of partial q - kLag - 1 (it passes that accumulator
-  // through), and before the FMAs of partial q - kLag and MFMA q + 1 (it
-  // passes their operands through).  The scheduling groups then place up to
-  // six VALU ops after each MFMA -- the scale FMAs plus the weight unpack.
-  // A operand i is reloaded for stage `nx` right after MFMA 4i+3 and B
-  // operand j right after MFMA 12+j, from one base address per tile that
-  // also passes through the statements (which orders the loads); the
-  // unpacked weights of stage `xs` (W words `rw`) go to LDS early.
-  constexpr int kLag = 3;
-  auto mma = [&](half8 (&fa)[4], half8 (&fb)[4], const floatx4& sc, int nx, const RawW& rw,
-                 int xs) {
-    floatx4 part[16];
+  // Stage s's MFMAs, each accumulating into its own accumulator.  A operand
+  // i is reloaded for stage `nx` right after MFMA 4i+3 and B operand j right
+  // after MFMA 12+j, from one base address per tile; one empty asm statement
+  // per MFMA passes the next MFMA's A operand and the base addresses
+  // through, which keeps each reload behind the last MFMA that reads the
+  // register it overwrites.  The unpacked weights of stage `xs` (W words
+  // `rw`) go to LDS early; the scheduling groups place up to three VALU ops
+  // (the unpack) after each MFMA.
+  auto mma = [&](half8 (&fa)[4], half8 (&fb)[4], int nx, const RawW& rw, int xs) {
     uint32_t abase = a_addr(nx, 0);
     uint32_t bbase = b_addr(nx, 0);
 #pragma unroll
-    for (int q = 0; q < 16 + kLag; q++) {
-      const int u = q - kLag;
-      if (q < 16) {
-        part[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[q >> 2], fb[q & 3],
-                                                         floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-        const int i1 = (q + 1 < 16) ? (q + 1) >> 2 : 3;
-        if (u >= 1)
-          asm volatile("" : "+v"(fa[i1]), "+v"(part[u]), "+v"(acc[(u - 1) >> 2][(u - 1) & 3]),
-                       "+v"(abase), "+v"(bbase) : "v"(part[q]));
-        else if (u == 0)
-          asm volatile("" : "+v"(fa[i1]), "+v"(part[u]), "+v"(abase), "+v"(bbase)
-                       : "v"(part[q]));
-        else
-          asm volatile("" : "+v"(fa[i1]), "+v"(abase), "+v"(bbase) : "v"(part[q]));
-        if ((q & 3) == 3)
-          fa[q >> 2] = *reinterpret_cast<const half8*>(smem + abase + (q >> 2) * 16 * kRowBytes);
-        if (q >= 12)
-          fb[q & 3] = *reinterpret_cast<const half8*>(smem + bbase + (q & 3) * 16 * kRowBytes);
-      }
-      if (u >= 0) {
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-          acc[u >> 2][u & 3][r] = fmaf(sc[u & 3], part[u][r], acc[u >> 2][u & 3][r]);
-      }
+    for (int q = 0; q < 16; q++) {
+      acc[q >> 2][q & 3] =
+          __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[q >> 2], fb[q & 3], acc[q >> 2][q & 3], 0, 0, 0);
+      const int i1 = (q + 1 < 16) ? (q + 1) >> 2 : 3;
+      asm volatile("" : "+v"(fa[i1]), "+v"(abase), "+v"(bbase));
+      if ((q & 3) == 3)
+        fa[q >> 2] = *reinterpret_cast<const half8*>(smem + abase + (q >> 2) * 16 * kRowBytes);
+      if (q >= 12)
+        fb[q & 3] = *reinterpret_cast<const half8*>(smem + bbase + (q & 3) * 16 * kRowBytes);
       if (q == 2) expand_write(xs, expand_unpack(rw));
-      if (q < 16) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
     }
   };
 
@@ -305,11 +310,10 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
     fa[i] = *reinterpret_cast<const half8*>(smem + a_addr(0, i));
     fb[i] = *reinterpret_cast<const half8*>(smem + b_addr(0, i));
   }
-  floatx4 sc0 = read_sc(0), sc1;
   stage_barrier();
 
-  // Stage s (operands of s and W words of s+2 already in registers): LDS
-  // read of stage s+1's scales; MFMAs of stage s with the reloads of stage
+  // Stage s (operands of s and W words of s+2 already in registers): MFMAs
+  // of stage s with the reloads of stage
   // s+1's operands and the unpack/writes of stage s+2's B tile woven in; X
   // DMA of stage s+4 and W read of stage s+4 (into the register slot just
   // used); then wait for everything but stage s+4's reads, and barrier.
@@ -321,14 +325,12 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   // The stage's global reads are issued after its MFMAs (a scheduling
   // barrier keeps them there).
   for (int s = 0; s < steps; s += 2) {
-    sc1 = read_sc(s + 1);
-    mma(fa, fb, sc0, s + 1, rwa, s + 2);
+    mma(fa, fb, s + 1, rwa, s + 2);
     __builtin_amdgcn_sched_barrier(0);
     issue(s + kPrefetch);
     rwa = raw_load(s + 4);
     stage_barrier(rwb);  // covers rwb, read one stage earlier
-    sc0 = read_sc(s + 2);
-    mma(fa, fb, sc1, s + 2, rwb, s + 3);
+    mma(fa, fb, s + 2, rwb, s + 3);
     __builtin_amdgcn_sched_barrier(0);
     issue(s + 1 + kPrefetch);
     rwb = raw_load(s + 5);
@@ -351,8 +353,9 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   }
   __syncthreads();
   if (kgrp == 0) {
-    // split K: this range's sum goes to its partial plane, the bias is added
-    // by the reduction
+    // Output column n is scaled by D_n = 2^rowexp[n] (exact).  Split K:
+    // this range's sum goes to its partial plane, the bias is added by the
+    // reduction.
     float* dst = a.splits > 1 ? a.part + (size_t)z * a.M * a.N : a.y;
     const float* bias = a.splits > 1 ? nullptr : a.bias;
 #pragma unroll
@@ -360,11 +363,13 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
       const int n = n0 + wn * 64 + 16 * j + lr;
       const bool nok = n < a.N;
       const float bv = (bias && nok) ? bias[n] : 0.0f;
+      const int en = nok ? a.rowexp[n] : 0;
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          const float v = acc[i][j][r] + red[((wig * 64 + (i * 4 + j) * 4 + r) * 64) + lane];
+          const float v =
+              ldexpf(acc[i][j][r] + red[((wig * 64 + (i * 4 + j) * 4 + r) * 64) + lane], en);
           const int m = m0 + wm * 64 + 16 * i + 4 * lq + r;
           if (nok && m < a.M) dst[(size_t)m * a.N + n] = v + bv;
         }
@@ -536,11 +541,14 @@ size_t round256(size_t v) { return (v + 255) / 256 * 256; }
 
 }  // namespace
 
+// Workspace of the Q4_0 GEMM: fp16 X, then the K-split partial planes (if
+// any), then the row exponents.
 size_t gemm_v3_workspace_bytes(size_t batch, size_t n, size_t m, int num_cus) {
   const size_t tiles = ((n + BN - 1) / BN) * ((batch + BM - 1) / BM);
   const int splits = pick_splits(tiles, m, num_cus);
   const size_t xb = round256(gemm_workspace_bytes(batch, m));
-  return splits > 1 ? xb + (size_t)splits * batch * n * 4 : xb;
+  const size_t pb = splits > 1 ? round256((size_t)splits * batch * n * 4) : 0;
+  return xb + pb + round256(n * 4);
 }
 
 bool q4_0_gemm_v3_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t batch) {
@@ -633,6 +641,12 @@ hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const
   a.splits = pick_splits((size_t)tiles, m, num_cus);
   a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) +
                                     round256(gemm_workspace_bytes(batch, m)));
+  int* rowexp = reinterpret_cast<int*>(
+      static_cast<uint8_t*>(ws) + gemm_v3_workspace_bytes(batch, n, m, num_cus) - round256(n * 4));
+  a.rowexp = rowexp;
+  hipLaunchKernelGGL(q4_0_row_exp_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, rowexp, w,
+                     (int)n, (int)(m / kBlockElems));
+  if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL(q4_0_gemm_v3_kernel, dim3(tiles, a.splits), dim3(kThreads), kLdsBytes, s,
                      a);
   e = hipGetLastError();

@@ -387,6 +387,32 @@ def test_gemm_q4_0(torch, hk, orc, batch, n, m):
         assert orc.rel_l2(got[t], r32) <= GEMM_TOL
 
 
+def test_gemm_q4_0_scale_range(torch, hk, orc):
+    """The GEMM rounds each weight to fp16 after dividing its row by a power
+    of two above the row's largest block scale: rows of huge scales (whose
+    weights overflow fp16 unnormalised), tiny scales, mixed scales and zero
+    scales each stay within the GEMM bar column by column."""
+    batch, n, m = 96, 300, 512
+    q = _q4(orc, n, m, seed=41)
+    blk = q.reshape(n, m // 32, 18)
+    def set_d(rows, vals):
+        bits = np.asarray(vals, np.float16).view(np.uint8).reshape(-1, 2)
+        blk[rows, :, 0] = bits[:, 0]
+        blk[rows, :, 1] = bits[:, 1]
+    set_d(0, np.full(m // 32, 60000.0))                         # |w| up to 480000
+    set_d(1, np.full(m // 32, 1e-6))                            # fp16 subnormal scales
+    set_d(2, np.where(np.arange(m // 32) % 2 == 0, 1e3, 1e-3))  # 1e6 apart in one row
+    set_d(3, np.zeros(m // 32))
+    set_d(299, np.full(m // 32, 65504.0))                       # largest fp16, tail tile
+    x = orc.normal_f32(42, (batch, m))
+    got = _run_q4(torch, hk, _gpu(torch, q), _gpu(torch, x), None, n, m, batch)
+    ref = _gemm_ref(orc, q, x, n, m)
+    assert np.all(got[:, 3] == 0.0)
+    for j in [c for c in range(n) if c != 3]:
+        err = orc.rel_l2(got[:, j], ref[:, j])
+        assert err <= GEMM_TOL, (j, err)
+
+
 @pytest.mark.parametrize("m", [320, 384])
 def test_gemm_bias_and_tails(torch, hk, orc, m):
     # M and N tails with a bias; m = 320 takes the 64-column kernel, m = 384
