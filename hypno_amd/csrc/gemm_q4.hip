@@ -1,16 +1,21 @@
 // Q4_0 batched-prefill GEMM for gfx950: Y[M][N] = X[M][K] . W[N][K]^T (+ bias)
 // with W in hypno's Q4_0 blocks (quant.rs:10-22) and X rounded to fp16.
 //
-// Each weight goes to the matrix cores as fp16 (nib - 8) * (d / D_n), with
-// D_n a power of two just above the largest |d| of weight row n (a pre-pass,
-// q4_0_row_exp_kernel, writes its exponent): every such value lies in
-// (-8, 8), so none overflows fp16, the block scale is applied before the
-// MFMA (one packed fp16 multiply per pair of weights), the MFMAs accumulate
-// straight into fp32 accumulators across blocks, and the output column is
-// multiplied by D_n at the end (exact: a power of two).  Each weight is
-// rounded to fp16 once (relative 2^-11).  Scaling each block's partial sum
-// in fp32 instead costs one VALU FMA per output per block -- as much issue
-// time as the MFMA itself.
+// Two ways to apply the per-block scale d, one kernel template:
+//
+//  * kFold (M >= kFoldMinBatch): each weight goes to the matrix cores as fp16
+//    (nib - 8) * (d / D_n), with D_n a power of two just above the largest
+//    |d| of weight row n (a pre-pass, q4_0_row_exp_kernel, writes its
+//    exponent): every such value lies in (-8, 8), so none overflows fp16;
+//    the MFMAs accumulate straight into fp32 accumulators across blocks, and
+//    the output column is multiplied by D_n at the end (exact: a power of
+//    two).  Each weight is rounded to fp16 once (relative 2^-11).
+//  * exact (smaller M, where the pre-pass's extra read of W costs more than
+//    folding saves): the integer nibbles go to the matrix cores as exact fp16
+//    values, each block is one MFMA into a zeroed accumulator, and the
+//    block's partial sum is scaled by d into the fp32 accumulators
+//    (acc += d * partial) -- one VALU FMA per output per block, as much issue
+//    time as the MFMA itself.
 //
 //  * Work-group = 512 threads (8 waves) on a 128 x 128 tile of Y, one per CU,
 //    two waves per SIMD.  A stage is 64 columns of K (two Q4_0 blocks); waves
@@ -32,9 +37,9 @@
 //        other 8 -- in a two-deep register double buffer.
 //  * Two stages ahead, every thread unpacks its 16 nibbles into exact fp16
 //    (nib - 8) with one and-or op and one packed fp16 op per pair of weights,
-//    multiplies them by fp16(d / D_n) (one packed fp16 op per pair) and
-//    writes them to a 2-slot B ring in LDS.  The expansion is shared by all
-//    128 rows of X.
+//    and either multiplies them by fp16(d / D_n) (kFold: one packed fp16 op
+//    per pair) or writes the block scale as fp32 beside them, into a 2-slot
+//    B ring in LDS.  The expansion is shared by all 128 rows of X.
 //  * Each MFMA operand register is reloaded from LDS for the next stage
 //    right after its last MFMA of this stage, so LDS latency hides behind
 //    the matrix work.  One barrier per stage.
@@ -65,9 +70,13 @@ constexpr int kARing = kPrefetch;       // stage s+1 read while s+2..s+4 land
 constexpr int kBRing = 2;               // stage s+1 read while s+2 is written
 constexpr int kRowBytes = BK * 2;           // 128 B: one fp16 tile row
 constexpr int kTileBytes = BM * kRowBytes;  // 16 KB
+constexpr int kScaleBytes = 2 * BN * 4;     // 1 KB (exact variant)
 constexpr int kOffA = 0;
 constexpr int kOffB = kOffA + kARing * kTileBytes;
-constexpr int kLdsBytes = kOffB + kBRing * kTileBytes;  // 96 KB (< 160 KB)
+constexpr int kOffS = kOffB + kBRing * kTileBytes;
+constexpr int kLdsBytes = kOffS + kBRing * kScaleBytes;  // 98 KB (< 160 KB)
+// From this many tokens the folded-scale variant runs.
+constexpr size_t kFoldMinBatch = 256;
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 static_assert(4 * 64 * 64 * 4 <= kARing * kTileBytes, "K-group reduction fits in the A ring");
 
@@ -122,7 +131,7 @@ struct Args {
   int xcd_map;        // 1: blockIdx -> tile mapping groups tiles per XCD
   int splits;         // K split over blockIdx.y; > 1: fp32 partials to `part`
   float* part;        // [splits][M][N] partial sums (splits > 1)
-  const int* rowexp;  // [N]: D_n = 2^rowexp[n]
+  const int* rowexp;  // [N]: D_n = 2^rowexp[n] (kFold)
 };
 
 // rowexp[n] = e with 2^(e-1) <= max |d| < 2^e over weight row n's blocks (0
@@ -145,6 +154,7 @@ q4_0_row_exp_kernel(int* __restrict__ rowexp, const uint8_t* __restrict__ w, int
   if (lane == 0) rowexp[row] = e;
 }
 
+template <bool kFold>
 __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int t = threadIdx.x;
@@ -207,7 +217,8 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   const uint8_t* erow = a.w + (size_t)min(n0 + er, a.N - 1) * w_row + 16 * eb + 8 * eh;
   const uint32_t boff0 = tile_off(er, 4 * eb + 2 * eh);
   const uint32_t boff1 = tile_off(er, 4 * eb + 2 * eh + 1);
-  const int eexp = evalid ? a.rowexp[n0 + er] : 0;
+  const uint32_t soff = (((eb * 2 + (er >> 6)) * 16 + (er & 15)) * 4 + ((er & 63) >> 4)) * 4;
+  const int eexp = (kFold && evalid) ? a.rowexp[n0 + er] : 0;
   using RawW = u32x3;
   auto raw_load = [&](int s) -> RawW {  // stage min(s, steps-1) of this range
     const int g = s0 + (s < steps ? s : steps - 1);
@@ -215,8 +226,17 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   };
   struct Expanded {
     u32x4 lo, hi;
+    float scale;  // exact variant
   };
   auto expand_unpack = [&](const RawW& r) -> Expanded {
+    if constexpr (!kFold) {
+      Expanded e;
+      e.lo = unpack8(__builtin_amdgcn_perm(r.y, r.x, esel));
+      e.hi = unpack8(__builtin_amdgcn_perm(r.z, r.y, esel));
+      const uint32_t dbits = (r.x >> (eb ? 16 : 0)) & 0xFFFFu;
+      e.scale = evalid ? f16_bits_to_f32(dbits) : 0.0f;  // used by the eh = 0 thread
+      return e;
+    }
     // fp16(d / D_n): exact while d / D_n is a normal fp16 number (d is fp16,
     // D_n a power of two); rows past N get 0.  Only the eh = 0 thread's words
     // hold the block's scale; its eh = 1 partner (the next lane) takes it
@@ -236,26 +256,36 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
       e.lo[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, wl) * hh);
       e.hi[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, wh) * hh);
     }
+    e.scale = 0.0f;
     return e;
   };
   auto expand_write = [&](int s, const Expanded& e) {
     uint8_t* bt = smem + kOffB + (s % kBRing) * kTileBytes;
     *reinterpret_cast<u32x4*>(bt + boff0) = e.lo;
     *reinterpret_cast<u32x4*>(bt + boff1) = e.hi;
+    if constexpr (!kFold) {
+      if (eh == 0)
+        *reinterpret_cast<float*>(smem + kOffS + (s % kBRing) * kScaleBytes + soff) = e.scale;
+    }
   };
   auto expand = [&](int s, const RawW& r) { expand_write(s, expand_unpack(r)); };
 
   // MFMA operands of this wave's block (kb = kgrp) of one stage: one
   // register set for A and one for B, each operand reloaded in place for the
-  // next stage right after its last MFMA of this stage.
+  // next stage right after its last MFMA of this stage; the block scales
+  // (exact variant) are double-buffered.
   const uint32_t fchunk = ((4 * kgrp + lq) ^ ((lr >> 1) & 7)) << 4;
   const uint32_t fa_off = (wm * 64 + lr) * kRowBytes + fchunk;
   const uint32_t fb_off = (wn * 64 + lr) * kRowBytes + fchunk;
+  const uint32_t fs_off = ((kgrp * 2 + wn) * 16 + lr) * 16;
   auto a_addr = [&](int s, int i) -> uint32_t {
     return (uint32_t)(kOffA + (s % kARing) * kTileBytes) + fa_off + i * 16 * kRowBytes;
   };
   auto b_addr = [&](int s, int j) -> uint32_t {
     return (uint32_t)(kOffB + (s % kBRing) * kTileBytes) + fb_off + j * 16 * kRowBytes;
+  };
+  auto read_sc = [&](int s) -> floatx4 {
+    return *reinterpret_cast<const floatx4*>(smem + kOffS + (s % kBRing) * kScaleBytes + fs_off);
   };
 
   floatx4 acc[4][4];
@@ -264,7 +294,58 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // Stage s's MFMAs, each accumulating into its own accumulator.  A operand
+  // Exact variant, stage s's MFMAs.  MFMA q = 4i + j; its partial is scaled in after MFMA
+  // q + kLag has been issued, so the FMAs do not wait on the matrix pipe and
+  // at most kLag + 2 partials are live.  The order is pinned by one empty
+  // asm statement per step (the default schedule would issue all MFMAs first
+  // and hold every partial at once, or scale a partial right behind its own
+  // MFMA and stall): statement q comes after MFMA q (it reads partial q),
+  // after the FMAs of partial q - kLag - 1 (it passes that accumulator
+  // through), and before the FMAs of partial q - kLag and MFMA q + 1 (it
+  // passes their operands through).  The scheduling groups then place up to
+  // six VALU ops after each MFMA -- the scale FMAs plus the weight unpack.
+  // A operand i is reloaded for stage `nx` right after MFMA 4i+3 and B
+  // operand j right after MFMA 12+j, from one base address per tile that
+  // also passes through the statements (which orders the loads); the
+  // unpacked weights of stage `xs` (W words `rw`) go to LDS early.
+  constexpr int kLag = 3;
+  auto mma_exact = [&](half8 (&fa)[4], half8 (&fb)[4], const floatx4& sc, int nx, const RawW& rw,
+                 int xs) {
+    floatx4 part[16];
+    uint32_t abase = a_addr(nx, 0);
+    uint32_t bbase = b_addr(nx, 0);
+#pragma unroll
+    for (int q = 0; q < 16 + kLag; q++) {
+      const int u = q - kLag;
+      if (q < 16) {
+        part[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[q >> 2], fb[q & 3],
+                                                         floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        const int i1 = (q + 1 < 16) ? (q + 1) >> 2 : 3;
+        if (u >= 1)
+          asm volatile("" : "+v"(fa[i1]), "+v"(part[u]), "+v"(acc[(u - 1) >> 2][(u - 1) & 3]),
+                       "+v"(abase), "+v"(bbase) : "v"(part[q]));
+        else if (u == 0)
+          asm volatile("" : "+v"(fa[i1]), "+v"(part[u]), "+v"(abase), "+v"(bbase)
+                       : "v"(part[q]));
+        else
+          asm volatile("" : "+v"(fa[i1]), "+v"(abase), "+v"(bbase) : "v"(part[q]));
+        if ((q & 3) == 3)
+          fa[q >> 2] = *reinterpret_cast<const half8*>(smem + abase + (q >> 2) * 16 * kRowBytes);
+        if (q >= 12)
+          fb[q & 3] = *reinterpret_cast<const half8*>(smem + bbase + (q & 3) * 16 * kRowBytes);
+      }
+      if (u >= 0) {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          acc[u >> 2][u & 3][r] = fmaf(sc[u & 3], part[u][r], acc[u >> 2][u & 3][r]);
+      }
+      if (q == 2) expand_write(xs, expand_unpack(rw));
+      if (q < 16) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    }
+  };
+
+  // Folded variant, stage s's MFMAs, each accumulating into its own accumulator.  A operand
   // i is reloaded for stage `nx` right after MFMA 4i+3 and B operand j right
   // after MFMA 12+j, from one base address per tile; one empty asm statement
   // per MFMA passes the next MFMA's A operand and the base addresses
@@ -272,7 +353,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   // register it overwrites.  The unpacked weights of stage `xs` (W words
   // `rw`) go to LDS early; the scheduling groups place up to three VALU ops
   // (the unpack) after each MFMA.
-  auto mma = [&](half8 (&fa)[4], half8 (&fb)[4], int nx, const RawW& rw, int xs) {
+  auto mma_fold = [&](half8 (&fa)[4], half8 (&fb)[4], int nx, const RawW& rw, int xs) {
     uint32_t abase = a_addr(nx, 0);
     uint32_t bbase = b_addr(nx, 0);
 #pragma unroll
@@ -310,10 +391,13 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
     fa[i] = *reinterpret_cast<const half8*>(smem + a_addr(0, i));
     fb[i] = *reinterpret_cast<const half8*>(smem + b_addr(0, i));
   }
+  floatx4 sc0 = {}, sc1 = {};
+  if constexpr (!kFold) sc0 = read_sc(0);
   stage_barrier();
 
-  // Stage s (operands of s and W words of s+2 already in registers): MFMAs
-  // of stage s with the reloads of stage
+  // Stage s (operands of s and W words of s+2 already in registers): LDS
+  // read of stage s+1's scales (exact variant); MFMAs of stage s with the
+  // reloads of stage
   // s+1's operands and the unpack/writes of stage s+2's B tile woven in; X
   // DMA of stage s+4 and W read of stage s+4 (into the register slot just
   // used); then wait for everything but stage s+4's reads, and barrier.
@@ -325,12 +409,22 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   // The stage's global reads are issued after its MFMAs (a scheduling
   // barrier keeps them there).
   for (int s = 0; s < steps; s += 2) {
-    mma(fa, fb, s + 1, rwa, s + 2);
+    if constexpr (kFold) {
+      mma_fold(fa, fb, s + 1, rwa, s + 2);
+    } else {
+      sc1 = read_sc(s + 1);
+      mma_exact(fa, fb, sc0, s + 1, rwa, s + 2);
+    }
     __builtin_amdgcn_sched_barrier(0);
     issue(s + kPrefetch);
     rwa = raw_load(s + 4);
     stage_barrier(rwb);  // covers rwb, read one stage earlier
-    mma(fa, fb, s + 2, rwb, s + 3);
+    if constexpr (kFold) {
+      mma_fold(fa, fb, s + 2, rwb, s + 3);
+    } else {
+      sc0 = read_sc(s + 2);
+      mma_exact(fa, fb, sc1, s + 2, rwb, s + 3);
+    }
     __builtin_amdgcn_sched_barrier(0);
     issue(s + 1 + kPrefetch);
     rwb = raw_load(s + 5);
@@ -353,7 +447,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   }
   __syncthreads();
   if (kgrp == 0) {
-    // Output column n is scaled by D_n = 2^rowexp[n] (exact).  Split K:
+    // Output column n is scaled by D_n = 2^rowexp[n] (kFold; exact).  Split K:
     // this range's sum goes to its partial plane, the bias is added by the
     // reduction.
     float* dst = a.splits > 1 ? a.part + (size_t)z * a.M * a.N : a.y;
@@ -363,7 +457,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
       const int n = n0 + wn * 64 + 16 * j + lr;
       const bool nok = n < a.N;
       const float bv = (bias && nok) ? bias[n] : 0.0f;
-      const int en = nok ? a.rowexp[n] : 0;
+      const int en = (kFold && nok) ? a.rowexp[n] : 0;
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -621,11 +715,14 @@ hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const
   if (e != hipSuccess) return e;
   static bool attr_set = false;
   if (!attr_set) {
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(q4_0_gemm_v3_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-    if (e != hipSuccess) return e;
+    for (const void* k : {reinterpret_cast<const void*>(q4_0_gemm_v3_kernel<true>),
+                          reinterpret_cast<const void*>(q4_0_gemm_v3_kernel<false>)}) {
+      e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+      if (e != hipSuccess) return e;
+    }
     attr_set = true;
   }
+  const bool fold = batch >= kFoldMinBatch;
   Args a;
   a.y = y;
   a.w = w;
@@ -644,11 +741,16 @@ hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const
   int* rowexp = reinterpret_cast<int*>(
       static_cast<uint8_t*>(ws) + gemm_v3_workspace_bytes(batch, n, m, num_cus) - round256(n * 4));
   a.rowexp = rowexp;
-  hipLaunchKernelGGL(q4_0_row_exp_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, rowexp, w,
-                     (int)n, (int)(m / kBlockElems));
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(q4_0_gemm_v3_kernel, dim3(tiles, a.splits), dim3(kThreads), kLdsBytes, s,
-                     a);
+  if (fold) {
+    hipLaunchKernelGGL(q4_0_row_exp_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, rowexp,
+                       w, (int)n, (int)(m / kBlockElems));
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(q4_0_gemm_v3_kernel<true>, dim3(tiles, a.splits), dim3(kThreads), kLdsBytes,
+                       s, a);
+  } else {
+    hipLaunchKernelGGL(q4_0_gemm_v3_kernel<false>, dim3(tiles, a.splits), dim3(kThreads),
+                       kLdsBytes, s, a);
+  }
   e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
   const size_t mn = batch * n;

@@ -387,12 +387,14 @@ def test_gemm_q4_0(torch, hk, orc, batch, n, m):
         assert orc.rel_l2(got[t], r32) <= GEMM_TOL
 
 
-def test_gemm_q4_0_scale_range(torch, hk, orc):
-    """The GEMM rounds each weight to fp16 after dividing its row by a power
-    of two above the row's largest block scale: rows of huge scales (whose
+@pytest.mark.parametrize("batch", [96, 300])
+def test_gemm_q4_0_scale_range(torch, hk, orc, batch):
+    """From 256 tokens the GEMM rounds each weight to fp16 after dividing its
+    row by a power of two above the row's largest block scale (below that it
+    scales each block's partial sum in fp32): rows of huge scales (whose
     weights overflow fp16 unnormalised), tiny scales, mixed scales and zero
     scales each stay within the GEMM bar column by column."""
-    batch, n, m = 96, 300, 512
+    n, m = 300, 512
     q = _q4(orc, n, m, seed=41)
     blk = q.reshape(n, m // 32, 18)
     def set_d(rows, vals):
