@@ -97,6 +97,44 @@ __device__ __forceinline__ u32x4 unpack8(uint32_t q) {
   return r;
 }
 
+// Group idx (row idx / (K/8), columns 8g..8g+7) of X fp32 [M][K] -> Xh fp16
+// [Mp][K], rows M..Mp-1 zero; with kPermute each group's 8 columns go in the
+// Q4_0 nibble-unpack order e0,e4,e1,e5,e2,e6,e3,e7.
+template <bool kPermute>
+__device__ __forceinline__ void x_to_f16_group(u32x4* __restrict__ xh, const float* __restrict__ x,
+                                               int M, int Mp, int K, size_t idx) {
+  const size_t groups = (size_t)K / 8;
+  if (idx >= (size_t)Mp * groups) return;
+  const size_t row = idx / groups;
+  float v[8];
+  if (row < (size_t)M) {
+    const float* src = x + idx * 8;  // row * K + g * 8
+    if (((uintptr_t)src & 15) == 0) {
+      const float4 a = load_global<float4>(src);
+      const float4 b = load_global<float4>(src + 4);
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = src[i];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = 0.0f;
+  }
+  constexpr int perm_q4[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+  u32x4 packed;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int a = kPermute ? perm_q4[2 * j] : 2 * j;
+    const int b = kPermute ? perm_q4[2 * j + 1] : 2 * j + 1;
+    const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)v[a]);
+    const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)v[b]);
+    packed[j] = lo | (hi << 16);
+  }
+  xh[idx] = packed;
+}
+
 // Wave-wide sum (wave64) with xor butterflies; every lane gets the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -50,46 +50,17 @@ bool q4_0_gemm_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t bat
 }
 
 // X fp32 [M][K] -> Xh fp16 [Mp][K] (zero rows M..Mp-1); optionally zero Y.
-// One thread per 8-column group.
+// One thread per 8-column group (x_to_f16_group).
 template <bool kPermute>
 __global__ void __launch_bounds__(256)
 x_to_f16_kernel(u32x4* __restrict__ xh, const float* __restrict__ x, int M, int Mp, int K,
                 float* __restrict__ y_zero, size_t y_elems) {
-  const size_t groups = (size_t)K / 8;
   const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (y_zero) {
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = idx; i < y_elems; i += stride) y_zero[i] = 0.0f;
   }
-  if (idx >= (size_t)Mp * groups) return;
-  const size_t row = idx / groups;
-  float v[8];
-  if (row < (size_t)M) {
-    const float* src = x + idx * 8;  // row * K + g * 8
-    if (((uintptr_t)src & 15) == 0) {
-      const float4 a = load_global<float4>(src);
-      const float4 b = load_global<float4>(src + 4);
-      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; i++) v[i] = src[i];
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = 0.0f;
-  }
-  constexpr int perm_q4[8] = {0, 4, 1, 5, 2, 6, 3, 7};
-  u32x4 packed;
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int a = kPermute ? perm_q4[2 * j] : 2 * j;
-    const int b = kPermute ? perm_q4[2 * j + 1] : 2 * j + 1;
-    const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)v[a]);
-    const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)v[b]);
-    packed[j] = lo | (hi << 16);
-  }
-  xh[idx] = packed;
+  x_to_f16_group<kPermute>(xh, x, M, Mp, K, idx);
 }
 
 // One packed nibble dword (elements e0..e7, byte i = e[2i] | e[2i+1] << 4)

@@ -5,8 +5,9 @@
 //
 //  * kFold (M >= kFoldMinBatch): each weight goes to the matrix cores as fp16
 //    (nib - 8) * (d / D_n), with D_n a power of two just above the largest
-//    |d| of weight row n (a pre-pass, q4_0_row_exp_kernel, writes its
-//    exponent): every such value lies in (-8, 8), so none overflows fp16;
+//    |d| of weight row n (the pre-pass that converts X, q4_0_prepass_kernel,
+//    also writes that exponent): every such value lies in (-8, 8), so none
+//    overflows fp16;
 //    the MFMAs accumulate straight into fp32 accumulators across blocks, and
 //    the output column is multiplied by D_n at the end (exact: a power of
 //    two).  Each weight is rounded to fp16 once (relative 2^-11).
@@ -134,18 +135,33 @@ struct Args {
   const int* rowexp;  // [N]: D_n = 2^rowexp[n] (kFold)
 };
 
-// rowexp[n] = e with 2^(e-1) <= max |d| < 2^e over weight row n's blocks (0
-// when that maximum is 0 or not finite), one wave per row.
+// One launch before the folded-scale GEMM.  Work-groups [0, gx) round X to
+// fp16 (x_to_f16_group, permuted); the rest write rowexp[n] = e with
+// 2^(e-1) <= max |d| < 2^e over weight row n's blocks (0 when that maximum
+// is 0 or not finite), one wave per row, its scale loads four deep.
 __global__ void __launch_bounds__(256)
-q4_0_row_exp_kernel(int* __restrict__ rowexp, const uint8_t* __restrict__ w, int n, int bpr) {
-  const int row = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+q4_0_prepass_kernel(u32x4* __restrict__ xh, const float* __restrict__ x, int M, int Mp, int K,
+                    unsigned gx, int* __restrict__ rowexp, const uint8_t* __restrict__ w, int n) {
+  if (blockIdx.x < gx) {
+    x_to_f16_group<true>(xh, x, M, Mp, K, (size_t)blockIdx.x * blockDim.x + threadIdx.x);
+    return;
+  }
+  const int row = (int)(((blockIdx.x - gx) * blockDim.x + threadIdx.x) >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= n) return;  // wave-uniform
+  const int bpr = K / kBlockElems;
   const uint8_t* base = w + (size_t)row * bpr * kBlockBytes;
   float mx = 0.0f;
-  for (int b = lane; b < bpr; b += 64) {
-    const uint8_t* blk = base + (size_t)b * kBlockBytes;
-    mx = fmaxf(mx, fabsf(f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8))));
+  for (int b0 = lane; b0 < bpr; b0 += 256) {
+    float d[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int b = b0 + 64 * u;
+      const uint8_t* blk = base + (size_t)b * kBlockBytes;
+      d[u] = b < bpr ? f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8)) : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) mx = fmaxf(mx, fabsf(d[u]));
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
@@ -711,8 +727,7 @@ hipError_t launch_f16_gemm_v2(float* y, const uint8_t* w, const float* x, const 
 hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const float* bias,
                                size_t n, size_t m, size_t batch, void* ws, int num_cus,
                                hipStream_t s) {
-  hipError_t e = launch_x_f16_permuted(x, batch, m, ws, s);
-  if (e != hipSuccess) return e;
+  hipError_t e;
   static bool attr_set = false;
   if (!attr_set) {
     for (const void* k : {reinterpret_cast<const void*>(q4_0_gemm_v3_kernel<true>),
@@ -742,12 +757,15 @@ hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const
       static_cast<uint8_t*>(ws) + gemm_v3_workspace_bytes(batch, n, m, num_cus) - round256(n * 4));
   a.rowexp = rowexp;
   if (fold) {
-    hipLaunchKernelGGL(q4_0_row_exp_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, rowexp,
-                       w, (int)n, (int)(m / kBlockElems));
+    const size_t mp = (batch + BM - 1) / BM * BM;
+    const unsigned gx = (unsigned)((mp * (m / 8) + 255) / 256);
+    hipLaunchKernelGGL(q4_0_prepass_kernel, dim3(gx + (unsigned)((n + 3) / 4)), dim3(256), 0, s,
+                       static_cast<u32x4*>(ws), x, (int)batch, (int)mp, (int)m, gx, rowexp, w, (int)n);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(q4_0_gemm_v3_kernel<true>, dim3(tiles, a.splits), dim3(kThreads), kLdsBytes,
                        s, a);
   } else {
+    if ((e = launch_x_f16_permuted(x, batch, m, ws, s)) != hipSuccess) return e;
     hipLaunchKernelGGL(q4_0_gemm_v3_kernel<false>, dim3(tiles, a.splits), dim3(kThreads),
                        kLdsBytes, s, a);
   }
