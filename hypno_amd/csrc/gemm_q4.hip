@@ -536,6 +536,7 @@ struct F16Args {
   int xcd_map;
   int splits;
   float* part;
+  const float* colscale;  // optional: output column n multiplied by colscale[n]
 };
 
 __device__ __forceinline__ void dma16_nt(const void* src, uint8_t* lds_wave_base) {
@@ -625,12 +626,13 @@ __global__ void __launch_bounds__(F16Geom<NW>::kThreads, 1) f16_gemm_v2_kernel(c
     const int n = n0 + wn * 64 + 16 * j + lr;
     if (n >= a.N) continue;
     const float bv = (a.splits == 1 && a.bias) ? a.bias[n] : 0.0f;
+    const float cs = a.colscale ? a.colscale[n] : 1.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int m = m0 + wm * 64 + 16 * i + 4 * lq + r;
-        if (m < a.M) out[(size_t)m * a.N + n] = acc[i][j][r] + bv;
+        if (m < a.M) out[(size_t)m * a.N + n] = acc[i][j][r] * cs + bv;
       }
   }
 }
@@ -688,7 +690,7 @@ bool f16_gemm_v2_ok(const uint8_t* w, size_t n, size_t m, size_t batch) {
 
 hipError_t launch_f16_gemm_v2(float* y, const uint8_t* w, const float* x, const float* bias,
                               size_t n, size_t m, size_t batch, void* ws, int num_cus,
-                              hipStream_t s) {
+                              hipStream_t s, const float* colscale) {
   using G = F16Geom<kF16NW>;
   hipError_t e = launch_x_f16_plain(x, batch, m, ws, s);
   if (e != hipSuccess) return e;
@@ -714,6 +716,7 @@ hipError_t launch_f16_gemm_v2(float* y, const uint8_t* w, const float* x, const 
   a.splits = pick_splits((size_t)tiles, m, num_cus);
   a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) +
                                     round256(gemm_workspace_bytes(batch, m)));
+  a.colscale = colscale;
   hipLaunchKernelGGL(f16_gemm_v2_kernel<kF16NW>, dim3(tiles, a.splits), dim3(G::kThreads), G::kLds,
                      s, a);
   e = hipGetLastError();

@@ -7,40 +7,22 @@
 // Each row n is expanded as (u - 128) * (d / D_n), D_n = the row's largest
 // |d|: every value then lies in [-128, 128], so none overflows fp16 (a plain
 // (u - 128) * d would for |w| > 65504), and each weight is rounded to fp16
-// once (relative 2^-11).  The GEMM output is rescaled by D_n, then the bias
-// added.  A row whose largest |d| is 0 or not finite keeps D_n = 1.
+// once (relative 2^-11).  The GEMM's epilogue multiplies output column n by
+// D_n and adds the bias.  A row whose largest |d| is 0 or not finite keeps
+// D_n = 1.
 #include "common.hpp"
 
 namespace hypno {
 
 namespace {
 
-// D[n] = max |d| over the row's blocks (one wave per row).
-__global__ void __launch_bounds__(256)
-q8_0_row_scale_kernel(float* __restrict__ D, const uint8_t* __restrict__ w, size_t n, int bpr) {
-  const size_t row = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  const int lane = threadIdx.x & 63;
-  if (row >= n) return;  // wave-uniform
-  const uint8_t* base = w + row * (size_t)bpr * kQ8BlockBytes;
-  float mx = 0.0f;
-  for (int b = lane; b < bpr; b += 64) {
-    const uint8_t* blk = base + (size_t)b * kQ8BlockBytes;
-    mx = fmaxf(mx, fabsf(f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8))));
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-  if (lane == 0) D[row] = (mx > 0.0f && mx <= 3.0e38f) ? mx : 1.0f;
-}
-
-// out[row][32 b + i] = fp16((u_i - 128) * (d_b / D[row])), one thread per block.
-__global__ void __launch_bounds__(256)
-q8_0_to_f16_kernel(_Float16* __restrict__ out, const uint8_t* __restrict__ w,
-                   const float* __restrict__ D, size_t n_blocks, int bpr) {
-  const size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (g >= n_blocks) return;
+// out[g][i] = fp16((u_i - 128) * (d / D)) for Q8_0 block g (32 values).
+__device__ __forceinline__ void q8_0_block_to_f16(_Float16* __restrict__ out,
+                                                  const uint8_t* __restrict__ w, size_t g,
+                                                  float D) {
   const uint8_t* blk = w + g * kQ8BlockBytes;
   const float d = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-  const float r = d / D[g / bpr];
+  const float r = d / D;
   uint32_t p[kBlockElems / 2];
 #pragma unroll
   for (int i = 0; i < kBlockElems / 2; i++) {
@@ -54,15 +36,27 @@ q8_0_to_f16_kernel(_Float16* __restrict__ out, const uint8_t* __restrict__ w,
   for (int q = 0; q < 4; q++) o[q] = u32x4{p[4 * q], p[4 * q + 1], p[4 * q + 2], p[4 * q + 3]};
 }
 
-// y[t][j] = y[t][j] * D[j] (+ bias[j]).
+// One wave per weight row: D[row] = max |d| over the row's blocks (1 when
+// that is 0 or not finite), then the row's blocks to fp16, one lane per
+// block.  The row's bytes are read from HBM once: the conversion finds them
+// in the caches the scale pass filled.
 __global__ void __launch_bounds__(256)
-q8_0_rescale_kernel(float* __restrict__ y, const float* __restrict__ D,
-                    const float* __restrict__ bias, size_t n, size_t total) {
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (size_t)gridDim.x * blockDim.x) {
-    const size_t j = i % n;
-    y[i] = y[i] * D[j] + (bias ? bias[j] : 0.0f);
+q8_0_rows_to_f16_kernel(_Float16* __restrict__ out, float* __restrict__ D,
+                        const uint8_t* __restrict__ w, size_t n, int bpr) {
+  const size_t row = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (row >= n) return;  // wave-uniform
+  const uint8_t* base = w + row * (size_t)bpr * kQ8BlockBytes;
+  float mx = 0.0f;
+  for (int b = lane; b < bpr; b += 64) {
+    const uint8_t* blk = base + (size_t)b * kQ8BlockBytes;
+    mx = fmaxf(mx, fabsf(f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8))));
   }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  const float dr = (mx > 0.0f && mx <= 3.0e38f) ? mx : 1.0f;
+  if (lane == 0) D[row] = dr;
+  for (int b = lane; b < bpr; b += 64) q8_0_block_to_f16(out, w, row * (size_t)bpr + b, dr);
 }
 
 size_t round256(size_t b) { return (b + 255) / 256 * 256; }
@@ -91,23 +85,13 @@ hipError_t launch_q8_0_gemm(float* y, const uint8_t* w, const float* x, const fl
   float* D = reinterpret_cast<float*>(base + round256(n * m * 2));
   void* gemm_ws = base + round256(n * m * 2) + round256(n * 4);
   const int bpr = (int)(m / kBlockElems);
-  hipLaunchKernelGGL(q8_0_row_scale_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, D, w,
-                     n, bpr);
+  hipLaunchKernelGGL(q8_0_rows_to_f16_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, w16,
+                     D, w, n, bpr);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const size_t nblk = n * (size_t)bpr;
-  hipLaunchKernelGGL(q8_0_to_f16_kernel, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, s,
-                     w16, w, D, nblk, bpr);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  e = launch_f16_gemm_v2(y, reinterpret_cast<const uint8_t*>(w16), x, nullptr, n, m, batch,
-                         gemm_ws, num_cus, s);
-  if (e != hipSuccess) return e;
-  const size_t total = n * batch;
-  size_t grid = (total + 255) / 256;
-  if (grid > 8192) grid = 8192;
-  hipLaunchKernelGGL(q8_0_rescale_kernel, dim3((unsigned)grid), dim3(256), 0, s, y, D, bias, n,
-                     total);
-  return hipGetLastError();
+  // the fp16 GEMM's epilogue multiplies output column n by D[n] and adds the bias
+  return launch_f16_gemm_v2(y, reinterpret_cast<const uint8_t*>(w16), x, bias, n, m, batch,
+                            gemm_ws, num_cus, s, D);
 }
 
 }  // namespace hypno
