@@ -16,29 +16,30 @@ namespace hypno {
 
 namespace {
 
-// out[g][i] = fp16((u_i - 128) * (d / D)) for Q8_0 block g (32 values).
-__device__ __forceinline__ void q8_0_block_to_f16(_Float16* __restrict__ out,
-                                                  const uint8_t* __restrict__ w, size_t g,
-                                                  float D) {
+// out[g][8k + i] = fp16((u_{8k+i} - 128) * (d / D)), i < 8: quarter k of
+// Q8_0 block g, read as four 2-byte loads (the block's bytes are 2-byte
+// aligned) and written as one 16-byte store.
+__device__ __forceinline__ void q8_0_quarter_to_f16(_Float16* __restrict__ out,
+                                                    const uint8_t* __restrict__ w, size_t g, int k,
+                                                    float D) {
   const uint8_t* blk = w + g * kQ8BlockBytes;
-  const float d = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+  const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk));
   const float r = d / D;
-  uint32_t p[kBlockElems / 2];
+  const uint16_t* q = reinterpret_cast<const uint16_t*>(blk + 2 + 8 * k);
+  u32x4 o;
 #pragma unroll
-  for (int i = 0; i < kBlockElems / 2; i++) {
-    const _Float16 lo = (_Float16)((float)((int)blk[2 + 2 * i] - 128) * r);
-    const _Float16 hi = (_Float16)((float)((int)blk[3 + 2 * i] - 128) * r);
-    p[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+  for (int i = 0; i < 4; i++) {
+    const uint32_t two = q[i];
+    const _Float16 lo = (_Float16)((float)((int)(two & 0xFFu) - 128) * r);
+    const _Float16 hi = (_Float16)((float)((int)(two >> 8) - 128) * r);
+    o[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
            ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
   }
-  u32x4* o = reinterpret_cast<u32x4*>(out + g * kBlockElems);  // 64 B per block, 16-aligned
-#pragma unroll
-  for (int q = 0; q < 4; q++) o[q] = u32x4{p[4 * q], p[4 * q + 1], p[4 * q + 2], p[4 * q + 3]};
+  *reinterpret_cast<u32x4*>(out + g * kBlockElems + 8 * k) = o;  // 16-aligned
 }
 
 // One wave per weight row: D[row] = max |d| over the row's blocks (1 when
-// that is 0 or not finite), then the row's blocks to fp16, one lane per
-// block.  The row's bytes are read from HBM once: the conversion finds them
+// that is 0 or not finite), then the row's blocks to fp16.  The row's bytes are read from HBM once: the conversion finds them
 // in the caches the scale pass filled.
 __global__ void __launch_bounds__(256)
 q8_0_rows_to_f16_kernel(_Float16* __restrict__ out, float* __restrict__ D,
@@ -56,7 +57,9 @@ q8_0_rows_to_f16_kernel(_Float16* __restrict__ out, float* __restrict__ D,
   for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
   const float dr = (mx > 0.0f && mx <= 3.0e38f) ? mx : 1.0f;
   if (lane == 0) D[row] = dr;
-  for (int b = lane; b < bpr; b += 64) q8_0_block_to_f16(out, w, row * (size_t)bpr + b, dr);
+  // four lanes per block, consecutive lanes on consecutive 16-byte outputs
+  for (int gi = lane; gi < 4 * bpr; gi += 64)
+    q8_0_quarter_to_f16(out, w, row * (size_t)bpr + (gi >> 2), gi & 3, dr);
 }
 
 size_t round256(size_t b) { return (b + 255) / 256 * 256; }
