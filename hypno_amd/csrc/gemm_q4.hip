@@ -361,14 +361,13 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
     }
   };
 
-  // Folded variant, stage s's MFMAs, each accumulating into its own accumulator.  A operand
-  // i is reloaded for stage `nx` right after MFMA 4i+3 and B operand j right
-  // after MFMA 12+j, from one base address per tile; one empty asm statement
-  // per MFMA passes the next MFMA's A operand and the base addresses
-  // through, which keeps each reload behind the last MFMA that reads the
-  // register it overwrites.  The unpacked weights of stage `xs` (W words
-  // `rw`) go to LDS early; the scheduling groups place up to three VALU ops
-  // (the unpack) after each MFMA.
+  // Folded variant, stage s's MFMAs, each accumulating into its own
+  // accumulator.  A operand i is reloaded for stage `nx` after MFMA 4i+3 and
+  // B operand j after MFMA 12+j (the reloads read the other ring slot, so
+  // their order against the MFMAs is free); the unpacked weights of stage
+  // `xs` (W words `rw`) go to LDS.  The compiler schedules all of it: asm
+  // statements pinning the reloads behind their MFMAs, and scheduling groups
+  // pinning three VALU ops after each MFMA, were each 1-3% slower.
   auto mma_fold = [&](half8 (&fa)[4], half8 (&fb)[4], int nx, const RawW& rw, int xs) {
     uint32_t abase = a_addr(nx, 0);
     uint32_t bbase = b_addr(nx, 0);
@@ -377,14 +376,12 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
       acc[q >> 2][q & 3] =
           __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[q >> 2], fb[q & 3], acc[q >> 2][q & 3], 0, 0, 0);
       const int i1 = (q + 1 < 16) ? (q + 1) >> 2 : 3;
-      asm volatile("" : "+v"(fa[i1]), "+v"(abase), "+v"(bbase));
       if ((q & 3) == 3)
         fa[q >> 2] = *reinterpret_cast<const half8*>(smem + abase + (q >> 2) * 16 * kRowBytes);
       if (q >= 12)
         fb[q & 3] = *reinterpret_cast<const half8*>(smem + bbase + (q & 3) * 16 * kRowBytes);
       if (q == 2) expand_write(xs, expand_unpack(rw));
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+
     }
   };
 
