@@ -3,14 +3,14 @@
 //
 // Two ways to apply the per-block scale d, one kernel template:
 //
-//  * kFold (M >= kFoldMinBatch): each weight goes to the matrix cores as fp16
-//    (nib - 8) * (d / D_n), with D_n a power of two just above the largest
-//    |d| of weight row n (the pre-pass that converts X, q4_0_prepass_kernel,
-//    also writes that exponent): every such value lies in (-8, 8), so none
-//    overflows fp16;
-//    the MFMAs accumulate straight into fp32 accumulators across blocks, and
-//    the output column is multiplied by D_n at the end (exact: a power of
-//    two).  Each weight is rounded to fp16 once (relative 2^-11).
+//  * kFold (M >= 256, or >= 128 for W up to 64 MB): each weight goes to the
+//    matrix cores as fp16 (nib - 8) * (d / D_n), with D_n a power of two
+//    just above the largest |d| of weight row n (the pre-pass that converts
+//    X, q4_0_prepass_kernel, also writes that exponent): every such value
+//    lies in (-8, 8), so none overflows fp16; the MFMAs accumulate straight
+//    into fp32 accumulators across blocks, and the output column is
+//    multiplied by D_n at the end (exact: a power of two).  Each weight is
+//    rounded to fp16 once (relative 2^-11).
 //  * exact (smaller M, where the pre-pass's extra read of W costs more than
 //    folding saves): the integer nibbles go to the matrix cores as exact fp16
 //    values, each block is one MFMA into a zeroed accumulator, and the
@@ -76,8 +76,13 @@ constexpr int kOffA = 0;
 constexpr int kOffB = kOffA + kARing * kTileBytes;
 constexpr int kOffS = kOffB + kBRing * kTileBytes;
 constexpr int kLdsBytes = kOffS + kBRing * kScaleBytes;  // 98 KB (< 160 KB)
-// From this many tokens the folded-scale variant runs.
+// The folded-scale variant runs from kFoldMinBatch tokens, and from
+// kFoldMinBatchSmallW when W is at most kFoldSmallWBytes (its pre-pass reads
+// every block scale, i.e. all of W once more; for a 295 MB lm_head at 128
+// tokens that costs more than folding saves, for a 33 MB matrix it does not).
 constexpr size_t kFoldMinBatch = 256;
+constexpr size_t kFoldMinBatchSmallW = 128;
+constexpr size_t kFoldSmallWBytes = (size_t)64 << 20;
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 static_assert(4 * 64 * 64 * 4 <= kARing * kTileBytes, "K-group reduction fits in the A ring");
 
@@ -737,7 +742,9 @@ hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const
     }
     attr_set = true;
   }
-  const bool fold = batch >= kFoldMinBatch;
+  const size_t wbytes = n * (m / kBlockElems) * kBlockBytes;
+  const bool fold = batch >= kFoldMinBatch ||
+                    (batch >= kFoldMinBatchSmallW && wbytes <= kFoldSmallWBytes);
   Args a;
   a.y = y;
   a.w = w;

@@ -389,9 +389,10 @@ def test_gemm_q4_0(torch, hk, orc, batch, n, m):
 
 @pytest.mark.parametrize("batch", [96, 300])
 def test_gemm_q4_0_scale_range(torch, hk, orc, batch):
-    """From 256 tokens the GEMM rounds each weight to fp16 after dividing its
-    row by a power of two above the row's largest block scale (below that it
-    scales each block's partial sum in fp32): rows of huge scales (whose
+    """From 128 tokens (this W is small) the GEMM rounds each weight to fp16
+    after dividing its row by a power of two above the row's largest block
+    scale (below that it scales each block's partial sum in fp32): rows of
+    huge scales (whose
     weights overflow fp16 unnormalised), tiny scales, mixed scales and zero
     scales each stay within the GEMM bar column by column."""
     n, m = 300, 512
