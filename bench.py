@@ -1,30 +1,39 @@
 #!/usr/bin/env python3
 """Q4_0 matmul benchmark on one MI355X.
 
-Headline workload: the full TinyLlama-1.1B decode
-step weight stream, M = 1, Q4_0, 22 layers x {q, k, v, o, gate, up, down}
-(544,997,376 weight bytes, larger than the 256 MB Infinity Cache, so every
-step streams from HBM).  One step = the 154 GEMVs as one multi-GEMV plan
-launch; steps are launched back to back on one stream and timed with HIP
-events on that stream.  value = weight bytes / step time (GB/s).
+Headline workload (BASELINE.json configs[3] at M = 1, the 7B shapes the
+metric and the north star quote): the Mistral-7B decode-step weight stream,
+32 layers x {q, k, v, o, gate, up, down} Q4_0 GEMVs (3,925,868,544 weight
+bytes, fifteen times the 256 MB Infinity Cache, so every step streams from
+HBM).  One step = the 224 GEMVs as one multi-GEMV plan launch; steps are
+launched back to back on one stream and timed with HIP events on that
+stream.  value = weight bytes / step time (GB/s).
 
 Also reported, in the same JSON line:
   roofline      the decode GEMV kernel's weight bytes per launch / its average
-                launch duration over the timed region, against the 8 TB/s HBM
-                peak; traffic = measured HBM bytes per launch (rocprofv3 --pmc,
-                read from the committed profile summary);
+                launch duration over the timed region (HIP events on the
+                launch stream), against the 8 TB/s HBM peak, with the
+                first-launches ("burst") and last-launches ("sustained")
+                averages; traffic = measured HBM bytes per launch (rocprofv3
+                --pmc, read from the committed profile summary);
   cpu_baseline  the CPU restatement of hypno's AVX2 kernel (oracle/) on this
-                host, on a bounded sample (layer 0's seven matrices);
+                host, on the same 224-matrix stream: the host's CPU share
+                and 8 threads, OMP_PROC_BIND=close, 3 warm-ups + 10 timed
+                passes, median (bench.rs:115-133);
   secondary     every other BASELINE config, GPU-timed (graph replay):
-                configs[0] the single 2048x2048 GEMV, configs[2] the prefill
-                GEMM at Llama-3.2-3B MLP shapes (M = 512), configs[3] the
-                Mistral-7B decode stream (224 GEMVs, one plan launch) and the
-                M-sweep {1, 8, 64, 512, 2048}, configs[4] the lm_head in Q4_0
-                and FP16 at M = 1 and 128; model_load: a TinyLlama-shaped
-                .hypno file opened with its payloads uploaded to HBM
-                (pipelined pinned upload, against a pageable copy and the
-                reference's host-only open); q8_0_decode and col_major: the
-                Q8_0 and column-major Q4_0 GEMVs at the Mistral shapes.
+                configs[0] the single 2048x2048 GEMV, configs[1] the
+                TinyLlama decode stream (with its own roofline block, and as
+                grouped / fused / per-call decode steps), configs[2] the
+                prefill GEMM at Llama-3.2-3B MLP shapes (M = 512), configs[3]
+                the Mistral M-sweep {1, 8, 64, 512, 2048}, configs[4] the
+                lm_head in Q4_0 and FP16 at M = 1 and 128; prefill GEMMs also
+                in the exact-nibble arithmetic (hypno_hip_set_gemm_numerics);
+                model_load, q8_0_decode, col_major.
+Every workload's output is checked once, untimed, against an fp64 reference
+computed here from the same packed bytes (sampled rows or columns; GEMV
+bar 1e-4 normwise, GEMM bar 2e-3 relative L2): each carries "checked".
+Each result also carries the reference bench's fields (bench.rs:14-16,35-46):
+time_ms, gflops, bandwidth_gbps (weight bytes / time).
 
 Inputs are synthetic: weights N(0, 0.02) from a seeded torch generator,
 quantised on the GPU by the bit-exact Q4_0 quantizer; activations N(0, 1).
@@ -33,8 +42,10 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import glob
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -45,17 +56,112 @@ if ROOT not in sys.path:
 METRIC = "Q4_0 GEMV weight GB/s (% HBM peak); prefill GEMM TFLOPS at 7B shapes"
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
+GEMV_TOL = 1e-4
+GEMM_TOL = 2e-3
 
-# TinyLlama-1.1B per-layer projections (n = output rows, m = input dim)
+# (name, n = output rows, m = input dim) per layer
 TINYLLAMA = [("q", 2048, 2048), ("k", 256, 2048), ("v", 256, 2048), ("o", 2048, 2048),
              ("gate", 5632, 2048), ("up", 5632, 2048), ("down", 2048, 5632)]
-LAYERS = 22
+TINYLLAMA_LAYERS = 22
+MISTRAL = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+           ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+MISTRAL_LAYERS = 32
+MISTRAL_SHAPES = [("q_o", 4096, 4096), ("k_v", 1024, 4096), ("gate_up", 14336, 4096),
+                  ("down", 4096, 14336)]
 ALIGN = 64  # .hypno tensor alignment (format.rs:10)
+X_OF = {"q": "attn", "k": "attn", "v": "attn", "o": "o", "gate": "mlp", "up": "mlp",
+        "down": "down"}
 
 
 def q4_bytes(n, m):
     return n * m // 32 * 18
 
+
+# --- fp64 reference checks (untimed; numpy over the packed bytes) ---------------------
+
+def q4_rows_f64(raw):
+    """Q4_0 rows [r, B*18] -> weights [r, B*32] in fp64: byte i of a block holds
+    element 2i (low nibble) and 2i+1 (high); w = (nibble - 8) * d."""
+    import numpy as np
+    r = raw.shape[0]
+    blk = raw.reshape(r, -1, 18)
+    d = blk[:, :, :2].copy().view(np.float16).astype(np.float64)  # [r, B, 1]
+    qs = blk[:, :, 2:].astype(np.int16)
+    vals = np.stack([(qs & 15) - 8, (qs >> 4) - 8], axis=-1).reshape(r, -1, 32)
+    return (vals * d).reshape(r, -1)
+
+
+def q8_rows_f64(raw):
+    """Q8_0 rows [r, B*34] -> fp64 weights: w = (u - 128) * d."""
+    import numpy as np
+    r = raw.shape[0]
+    blk = raw.reshape(r, -1, 34)
+    d = blk[:, :, :2].copy().view(np.float16).astype(np.float64)
+    return ((blk[:, :, 2:].astype(np.float64) - 128.0) * d).reshape(r, -1)
+
+
+def sample_idx(n, count, seed):
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    s = set(rng.choice(n, size=min(n, count), replace=False).tolist())
+    s.update({0, n - 1})
+    return np.array(sorted(s))
+
+
+def gather_rows(torch, buf, off, n, row_bytes, rows):
+    """Bytes of weight rows `rows` of the matrix at buf[off:] (rows of
+    row_bytes bytes), gathered on the device and copied to the host."""
+    mat = buf[off:off + n * row_bytes].view(n, row_bytes)
+    return mat[torch.as_tensor(rows, device=buf.device)].cpu().numpy()
+
+
+def normwise(got, ref):
+    import numpy as np
+    den = float(np.max(np.abs(ref)))
+    err = float(np.max(np.abs(got.astype(np.float64) - ref)))
+    return err / den if den > 0 else err
+
+
+def rel_l2(got, ref):
+    import numpy as np
+    den = float(np.linalg.norm(ref))
+    err = float(np.linalg.norm(got.astype(np.float64) - ref))
+    return err / den if den > 0 else err
+
+
+def check_q4(torch, buf, off, n, m, x, y, M, seed, count=64):
+    """y [M][n] from W at buf[off:] and x [M][m] (device) against fp64 over
+    sampled weight rows (GEMV: normwise; M > 16: relative L2 over all tokens of
+    the sampled columns)."""
+    cols = sample_idx(n, count, seed)
+    w = q4_rows_f64(gather_rows(torch, buf, off, n, m // 32 * 18, cols))
+    xh = x.reshape(M, m).cpu().numpy().astype("float64")
+    ref = xh @ w.T
+    got = y.reshape(M, n)[:, torch.as_tensor(cols, device=y.device)].cpu().numpy()
+    if M <= 16:
+        err = max(normwise(got[t], ref[t]) for t in range(M))
+        return {"checked": err <= GEMV_TOL, "max_err": float(f"{err:.3g}"), "bar": "normwise 1e-4",
+                "sampled_cols": len(cols)}
+    err = rel_l2(got, ref)
+    return {"checked": err <= GEMM_TOL, "max_err": float(f"{err:.3g}"), "bar": "rel-L2 2e-3",
+            "sampled_cols": len(cols)}
+
+
+def merge_checks(checks):
+    """One check record for a workload made of several outputs."""
+    checks = list(checks)
+    return {"checked": all(c["checked"] for c in checks),
+            "max_err": max(c["max_err"] for c in checks), "bar": checks[0]["bar"],
+            "outputs_checked": len(checks)}
+
+
+def ref_fields(us, flops, nbytes):
+    """The reference bench's BenchResult fields (bench.rs:14-16)."""
+    return {"time_ms": round(us * 1e-3, 6), "gflops": round(flops / us * 1e-3, 1),
+            "bandwidth_gbps": round(nbytes / us * 1e-3, 1)}
+
+
+# --- library and inputs ----------------------------------------------------------------
 
 class Lib:
     def __init__(self):
@@ -115,70 +221,143 @@ def time_graph(torch, fn, steps, warmup):
 
 
 def time_launches(torch, fn, steps, warmup):
-    """Average ms per call of `fn` over `steps` back-to-back calls on the
-    current stream, bracketed by HIP events on that stream."""
+    """Back-to-back calls of `fn` (one kernel launch each) on the current
+    stream: an event before every launch and after the last, all on that
+    stream.  Returns (average ms over the timed region, per-launch ms)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record()
+    for i in range(steps):
         fn()
-    e1.record()
+        ev[i + 1].record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    return ev[0].elapsed_time(ev[steps]) / steps, per
 
 
-def decode_stream(torch, lib, steps, warmup, value_only=False):
-    """22 layers x 7 Q4_0 GEMVs.  Each matrix has its own output
-    buffer; each layer has its own activation vectors (x for q/k/v/gate/up
-    and for o share m = 2048, down has m = 5632)."""
-    import hypno_amd as hk
+def launch_stats(per_ms, bytes_per_launch):
+    k = max(1, min(5, len(per_ms) // 4))
+    first, last = per_ms[:k], per_ms[-k:]
+    us = lambda v: round(v * 1e3, 2)  # noqa: E731
+    gbs = lambda ms: round(bytes_per_launch / (ms * 1e-3) / 1e9, 1)  # noqa: E731
+    return {"launches": len(per_ms), "median_us": us(statistics.median(per_ms)),
+            "min_us": us(min(per_ms)), "max_us": us(max(per_ms)),
+            f"burst_first{k}_us": us(sum(first) / k), f"sustained_last{k}_us": us(sum(last) / k),
+            f"burst_first{k}_gbs": gbs(sum(first) / k),
+            f"sustained_last{k}_gbs": gbs(sum(last) / k)}
+
+
+# --- decode-step weight streams (configs[1], configs[3] at M = 1) -----------------------
+
+def build_stream(torch, lib, per_layer, layers, seed):
+    """All layers' Q4_0 matrices in one arena, one output per matrix and, per
+    layer, one activation vector per input kind (q/k/v and gate/up share)."""
     stream0 = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    shapes = [(n, m) for _ in range(LAYERS) for (_, n, m) in TINYLLAMA]
-    arena, offs = make_q4_arena(torch, lib, shapes, seed=1234, stream=stream0)
-    gen = torch.Generator(device="cuda").manual_seed(99)
-    xs = [{"attn": torch.randn(2048, generator=gen, device="cuda"),
-           "o": torch.randn(2048, generator=gen, device="cuda"),
-           "mlp": torch.randn(2048, generator=gen, device="cuda"),
-           "down": torch.randn(5632, generator=gen, device="cuda")} for _ in range(LAYERS)]
-    x_of = {"q": "attn", "k": "attn", "v": "attn", "o": "o", "gate": "mlp", "up": "mlp",
-            "down": "down"}
+    shapes = [(n, m) for _ in range(layers) for (_, n, m) in per_layer]
+    arena, offs = make_q4_arena(torch, lib, shapes, seed=seed, stream=stream0)
+    gen = torch.Generator(device="cuda").manual_seed(seed + 1)
+    dm = {"attn": per_layer[0][2], "o": per_layer[3][2], "mlp": per_layer[4][2],
+          "down": per_layer[6][2]}
+    xs = [{k: torch.randn(v, generator=gen, device="cuda") for k, v in dm.items()}
+          for _ in range(layers)]
     ys = [torch.empty(n, device="cuda") for n, _ in shapes]
-    jobs = []  # (layer, name, y, w view, x, n, m)
+    jobs = []  # (layer, name, y, offset, x, n, m)
     for i, ((n, m), (off, nb)) in enumerate(zip(shapes, offs)):
-        layer, (name, _, _) = divmod(i, len(TINYLLAMA))[0], TINYLLAMA[i % len(TINYLLAMA)]
-        jobs.append((layer, name, ys[i], arena[off:off + nb], xs[layer][x_of[name]], n, m))
-    weight_bytes = sum(nb for _, nb in offs)
+        layer, name = i // len(per_layer), per_layer[i % len(per_layer)][0]
+        jobs.append((layer, name, ys[i], off, xs[layer][X_OF[name]], n, m))
+    return arena, offs, xs, jobs
 
-    # (a) the whole weight stream as one plan: one launch per step (the value),
-    # launched back to back on the current stream
-    plan_all = hk.GemvPlan([(y, w, x, None, n, m) for _, _, y, w, x, n, m in jobs])
-    ms_all = time_launches(torch, plan_all.run, steps, warmup)
-    res = {"ms": ms_all, "weight_bytes": weight_bytes, "launches": plan_all.launches}
-    host_sample = [w.cpu().numpy() for _, _, _, w, _, _, _ in jobs[:len(TINYLLAMA)]]
-    res["sample"] = host_sample
-    res["x_host"] = {m: jobs[0][4].cpu().numpy() if m == 2048 else jobs[6][4].cpu().numpy()
-                     for m in (2048, 5632)}
-    if value_only:
-        return res
-    # (b) dependency-respecting decode step: per layer [q,k,v] [o] [gate,up] [down]
-    groups = []
-    for layer in range(LAYERS):
-        lj = [j for j in jobs if j[0] == layer]
-        for names in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",)):
-            groups.append(hk.GemvPlan([(y, w, x, None, n, m)
-                                       for _, nm, y, w, x, n, m in lj if nm in names]))
+
+def check_jobs(torch, arena, jobs, seed, count=16):
+    return merge_checks(check_q4(torch, arena, off, n, m, x, y, 1, seed + i, count)
+                        for i, (_, _, y, off, x, n, m) in enumerate(jobs))
+
+
+def plan_of(hk, arena, jobs, names=None, layer=None, pro=None):
+    sel = [j for j in jobs if (names is None or j[1] in names) and (layer is None or j[0] == layer)]
+    return hk.GemvPlan([(y, arena[off:off + q4_bytes(n, m)], x, None, n, m) +
+                        ((pro(name),) if pro else ())
+                        for _, name, y, off, x, n, m in sel])
+
+
+def mistral_stream(torch, lib, steps, warmup):
+    """The value: Mistral-7B's 224 Q4_0 GEMVs as one plan launch per step."""
+    import hypno_amd as hk
+    arena, offs, xs, jobs = build_stream(torch, lib, MISTRAL, MISTRAL_LAYERS, seed=11)
+    plan = plan_of(hk, arena, jobs)
+    wb = sum(nb for _, nb in offs)
+    ms, per = time_launches(torch, plan.run, steps, warmup)
+    for _, _, y, *_ in jobs:
+        y.fill_(float("nan"))
+    plan.run()
+    torch.cuda.synchronize()
+    chk = check_jobs(torch, arena, jobs, seed=3)
+    res = {"ms": ms, "per": per, "weight_bytes": wb, "launches": plan.launches, "check": chk,
+           "arena": arena, "offs": offs, "jobs": jobs}
+    plan.close()
+    return res
+
+
+def tinyllama_stream(torch, lib, steps, warmup):
+    """TinyLlama's 154 GEMVs as one plan launch (with its own
+    roofline block), and the same weights as a real decode step runs them:
+    dependency-respecting plans per layer, those plans with RMS norm and
+    silu(gate)*up fused into their activation staging (beside the same work
+    as separate kernels), and one drop-in call per matrix."""
+    import numpy as np
+
+    import hypno_amd as hk
+    arena, offs, xs, jobs = build_stream(torch, lib, TINYLLAMA, TINYLLAMA_LAYERS, seed=1234)
+    wb = sum(nb for _, nb in offs)
+    out = {"workload": "configs[1] TinyLlama-1.1B decode-step Q4_0 weight stream: 22 layers x "
+                       "{q,k,v,o,gate,up,down}, M=1, 154 GEMVs as one plan launch, back to back",
+           "weight_bytes": wb}
+
+    def reset():
+        for _, _, y, *_ in jobs:
+            y.fill_(float("nan"))
+
+    plan = plan_of(hk, arena, jobs)
+    ms, per = time_launches(torch, plan.run, steps, warmup)
+    reset()
+    plan.run()
+    torch.cuda.synchronize()
+    out["check"] = check_jobs(torch, arena, jobs, seed=5)
+    gbs = wb / (ms * 1e-3) / 1e9
+    out.update({"us": round(ms * 1e3, 2), "weight_gbs": round(gbs, 1),
+                "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                "roofline": {"bound": "hbm", "kernel": "q4_0_gemv_jobs_kernel",
+                             "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(gbs / HBM_PEAK_GBS, 4),
+                             "traffic": stream_traffic(TINY_TRAFFIC_FILE),
+                             "per_launch": launch_stats(per, wb)},
+                **ref_fields(ms * 1e3, 2.0 * sum(n * m for *_, n, m in jobs), wb)})
+    plan.close()
+    # dependency-respecting decode step: per layer [q,k,v] [o] [gate,up] [down]
+    groups = [plan_of(hk, arena, jobs, names, layer)
+              for layer in range(TINYLLAMA_LAYERS)
+              for names in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",))]
 
     def run_groups():
         for p in groups:
             p.run()
 
-    ms_grp, g_grp = time_graph(torch, run_groups, steps, warmup)
-    # (c) the drop-in path: one matmul_q4_0 call per matrix (154 launches)
-    calls = [(ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(w.data_ptr()), w.numel(),
-              ctypes.c_void_p(x.data_ptr()), n, m) for _, _, y, w, x, n, m in jobs]
+    ms_grp, g = time_graph(torch, run_groups, steps, warmup)
+    reset()
+    g.replay()
+    torch.cuda.synchronize()
+    del g
+    out["decode_step_grouped"] = {
+        "desc": "dependency-respecting decode step: per layer [q,k,v], [o], [gate,up], [down] "
+                "plans, replayed as one HIP graph",
+        "launches": sum(p.launches for p in groups), "ms_per_step": round(ms_grp, 5),
+        "gbs": round(wb / (ms_grp * 1e-3) / 1e9, 2), "check": check_jobs(torch, arena, jobs, 7)}
+    # one drop-in call per matrix
+    calls = [(ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(arena.data_ptr() + off),
+              q4_bytes(n, m), ctypes.c_void_p(x.data_ptr()), n, m)
+             for _, _, y, off, x, n, m in jobs]
 
     def per_call():
         st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -187,42 +366,68 @@ def decode_stream(torch, lib, steps, warmup, value_only=False):
             if rc:
                 lib.check(rc, "decode GEMV")
 
-    ms_call, g_call = time_graph(torch, per_call, steps, warmup)
-    del g_grp, g_call
-    res.update({"ms_grouped": ms_grp, "launches_grouped": sum(p.launches for p in groups),
-                "ms_per_call": ms_call, "launches_per_call": len(calls)})
-    # (d) the same groups with the steps either side of the GEMVs: RMS norm
-    # before [q,k,v] and [gate,up], silu(gate)*up before [down] — fused into
-    # the GEMVs' staging, against the same work as separate kernels
+    ms_call, g = time_graph(torch, per_call, steps, warmup)
+    reset()
+    g.replay()
+    torch.cuda.synchronize()
+    del g
+    out["per_call"] = {
+        "desc": "drop-in path: one hypno_hip_matmul_q4_0_dev call per matrix, replayed as one "
+                "HIP graph", "launches": len(calls), "ms_per_step": round(ms_call, 5),
+        "gbs": round(wb / (ms_call * 1e-3) / 1e9, 2), "check": check_jobs(torch, arena, jobs, 9)}
+    # RMS norm before [q,k,v] and [gate,up], silu(gate)*up before [down], fused
     eps = 1e-5
+    gen = torch.Generator(device="cuda").manual_seed(77)
     norms = [(1.0 + 0.1 * torch.randn(2048, generator=gen, device="cuda"),
-              1.0 + 0.1 * torch.randn(2048, generator=gen, device="cuda")) for _ in range(LAYERS)]
-    ups = [torch.randn(5632, generator=gen, device="cuda") for _ in range(LAYERS)]
-    fused = []
-    for layer in range(LAYERS):
-        lj = {nm: (y, w, x, n, m) for lyr, nm, y, w, x, n, m in jobs if lyr == layer}
-        n1, n2 = norms[layer]
+              1.0 + 0.1 * torch.randn(2048, generator=gen, device="cuda"))
+             for _ in range(TINYLLAMA_LAYERS)]
+    ups = [torch.randn(5632, generator=gen, device="cuda") for _ in range(TINYLLAMA_LAYERS)]
 
-        def j(nm, pro):
-            y, w, x, n, m = lj[nm]
-            return (y, w, x, None, n, m, pro)
-        fused += [hk.GemvPlan([j(nm, ("rms_norm", n1, eps)) for nm in ("q", "k", "v")]),
-                  hk.GemvPlan([j("o", None)]),
-                  hk.GemvPlan([j(nm, ("rms_norm", n2, eps)) for nm in ("gate", "up")]),
-                  hk.GemvPlan([j("down", ("silu_mul", ups[layer]))])]
+    def pro_of(layer):
+        return lambda name: (("rms_norm", norms[layer][0], eps) if name in ("q", "k", "v") else
+                             ("rms_norm", norms[layer][1], eps) if name in ("gate", "up") else
+                             ("silu_mul", ups[layer]) if name == "down" else None)
+
+    fused = []
+    for layer in range(TINYLLAMA_LAYERS):
+        for names in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",)):
+            pf = pro_of(layer)
+            if names == ("o",):
+                fused.append(plan_of(hk, arena, jobs, names, layer))
+            else:
+                fused.append(plan_of(hk, arena, jobs, names, layer, pro=pf))
 
     def run_fused():
         for p in fused:
             p.run()
 
-    ms_fused, g_f = time_graph(torch, run_fused, steps, warmup)
-    # separate kernels write the GEMVs' inputs from the residual stream and
-    # the gate vector, as the reference's in-place norm and silu do
+    ms_fused, g = time_graph(torch, run_fused, steps, warmup)
+    reset()
+    g.replay()
+    torch.cuda.synchronize()
+    del g
+    # fp64 reference of the fused step: the GEMV of the normed / gated input
+    fchecks = []
+    for i, (layer, name, y, off, x, n, m) in enumerate(jobs):
+        if i % 7 == 0 or name in ("down", "gate"):  # a sample of the 154 jobs
+            xv = x.cpu().numpy().astype(np.float64)
+            if name in ("q", "k", "v", "gate", "up"):
+                nw = norms[layer][0 if name in ("q", "k", "v") else 1].cpu().numpy()
+                xv = xv / np.sqrt(np.mean(xv * xv) + eps) * nw
+            elif name == "down":
+                xv = xv / (1.0 + np.exp(-xv)) * ups[layer].cpu().numpy()
+            cols = sample_idx(n, 16, 100 + i)
+            wv = q4_rows_f64(gather_rows(torch, arena, off, n, m // 32 * 18, cols))
+            got = y[torch.as_tensor(cols, device="cuda")].cpu().numpy()
+            err = normwise(got, wv @ xv)
+            fchecks.append({"checked": err <= GEMV_TOL, "max_err": float(f"{err:.3g}"),
+                            "bar": "normwise 1e-4"})
+    # the same work as separate kernels (norm / silu write the GEMVs' inputs)
     hidden = torch.randn(2048, generator=gen, device="cuda")
     gate_v = torch.randn(5632, generator=gen, device="cuda")
 
     def run_separate():
-        for layer in range(LAYERS):
+        for layer in range(TINYLLAMA_LAYERS):
             x = xs[layer]
             hk.rms_norm(hidden, norms[layer][0], eps, out=x["attn"])
             groups[4 * layer].run()
@@ -232,16 +437,29 @@ def decode_stream(torch, lib, steps, warmup, value_only=False):
             hk.silu_mul(gate_v, ups[layer], out=x["down"])
             groups[4 * layer + 3].run()
 
-    ms_sep, g_s = time_graph(torch, run_separate, steps, warmup)
-    del g_f, g_s
-    res.update({"ms_fused": ms_fused, "launches_fused": sum(p.launches for p in fused),
-                "ms_separate": ms_sep,
-                "launches_separate": sum(p.launches for p in groups) + 3 * LAYERS})
-    return res
+    ms_sep, g = time_graph(torch, run_separate, steps, warmup)
+    reset()
+    g.replay()
+    torch.cuda.synchronize()
+    del g
+    out["decode_step_fused"] = {
+        "desc": "the grouped decode step with RMS norm before [q,k,v] and [gate,up] and "
+                "silu(gate)*up before [down] applied inside the GEMVs' activation staging",
+        "launches": sum(p.launches for p in fused), "ms_per_step": round(ms_fused, 5),
+        "vs_separate_kernels_ms": round(ms_sep, 5),
+        "separate_launches": sum(p.launches for p in groups) + 3 * TINYLLAMA_LAYERS,
+        "check": merge_checks(fchecks), "separate_check": check_jobs(torch, arena, jobs, 11)}
+    for p in groups + fused:
+        p.close()
+    del arena
+    torch.cuda.empty_cache()
+    return out
 
+
+# --- single calls (graph replay) -------------------------------------------------------
 
 def time_calls_graph(torch, issue, reps, replays=3):
-    """GPU time per iteration of `issue(stream_ptr)` (library calls on one
+    """GPU time per iteration of `issue(stream_ptr, i)` (library calls on one
     stream): one warm-up call, then `reps` iterations captured in a HIP graph
     and replayed `replays` times between HIP events, so host-side call
     overhead does not enter the figure."""
@@ -266,22 +484,28 @@ def time_calls_graph(torch, issue, reps, replays=3):
     return e0.elapsed_time(e1) / (replays * reps) * 1e3  # us
 
 
-def rotating_q4(torch, lib, n, m, seed, min_bytes=512 * 2**20):
-    """Distinct Q4_0 copies of one n x m matrix, >= min_bytes in total, so that
-    successive calls stream their weights from HBM, not from the 256 MB cache."""
-    nb = q4_bytes(n, m)
-    copies = max(2, -(-min_bytes // nb))
-    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    arena, offs = make_q4_arena(torch, lib, [(n, m)] * copies, seed=seed, stream=st)
-    return arena, [arena.data_ptr() + off for off, _ in offs], nb
+def result(us, M, n, m, nbytes):
+    flops = 2.0 * M * n * m
+    return {"us": round(us, 2), "weight_gbs": round(nbytes / us / 1e3, 1),
+            "tflops": round(flops / us / 1e6, 2),
+            "frac_hbm_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            "frac_fp16_peak": round(flops / us / 1e6 / FP16_PEAK_TFLOPS, 4),
+            **ref_fields(us, flops, nbytes)}
 
 
-def q4_case(torch, lib, n, m, M, seed, reps):
+def q4_case(torch, lib, n, m, M, seed, reps, exact_too=False):
     """GPU us per hypno_hip_matmul_q4_0_dev call of an M x m . (n x m)^T
-    product (rotating weight copies when the weights are small)."""
-    arena, ptrs, nb = rotating_q4(torch, lib, n, m, seed,
-                                  min_bytes=512 * 2**20 if M <= 64 else 1)
-    x = torch.randn(M, m, device="cuda")
+    product, over >= 512 MB of distinct weight copies when M <= 64 (so the
+    weights stream from HBM), checked once against fp64.  With exact_too, the
+    same call again in the exact-nibble GEMM arithmetic."""
+    import hypno_amd as hk
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    nb = q4_bytes(n, m)
+    copies = max(2, -(-(512 * 2**20) // nb)) if M <= 64 else 1
+    arena, offs = make_q4_arena(torch, lib, [(n, m)] * copies, seed=seed, stream=st)
+    ptrs = [arena.data_ptr() + off for off, _ in offs]
+    gen = torch.Generator(device="cuda").manual_seed(seed + 1)
+    x = torch.randn(M, m, generator=gen, device="cuda")
     y = torch.empty(M, n, device="cuda")
     xp, yp = ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr())
 
@@ -290,69 +514,63 @@ def q4_case(torch, lib, n, m, M, seed, reps):
         if rc:
             lib.check(rc, "matmul_q4_0")
 
-    us = time_calls_graph(torch, issue, reps)
+    def checked():
+        y.fill_(float("nan"))
+        issue(st, 0)
+        torch.cuda.synchronize()
+        return check_q4(torch, arena, offs[0][0], n, m, x, y, M, seed)
+
+    out = result(time_calls_graph(torch, issue, reps), M, n, m, nb)
+    out["check"] = checked()
+    if exact_too:
+        prev = hk.set_gemm_numerics(hk.GEMM_EXACT)
+        try:
+            ex = result(time_calls_graph(torch, issue, reps), M, n, m, nb)
+            ex["check"] = checked()
+        finally:
+            hk.set_gemm_numerics(prev)
+        out["exact_nibbles"] = ex
     del arena, x, y
     torch.cuda.empty_cache()
-    return {"us": round(us, 2), "weight_gbs": round(nb / us / 1e3, 1),
-            "tflops": round(2.0 * M * n * m / us / 1e6, 2),
-            "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4),
-            "frac_fp16_peak": round(2.0 * M * n * m / us / 1e6 / FP16_PEAK_TFLOPS, 4)}
+    return out
+
+
+def single_gemv(torch, lib):
+    """configs[0]: one 2048 x 2048 Q4_0 GEMV (TinyLlama q_proj), M = 1."""
+    r = q4_case(torch, lib, 2048, 2048, 1, seed=2048, reps=50)
+    r["workload"] = ("configs[0] 2048x2048 Q4_0 GEMV, M=1; GPU time per call, >= 512 MB "
+                     "of rotating weight copies")
+    return r
 
 
 def prefill_gemm(torch, lib):
     """M = 512 tokens, Llama-3.2-3B MLP: gate/up 8192 x 3072 and
-    down 3072 x 8192, activations N(0,1) with 1% of channels x20.  Each call =
-    fp16 activation pre-pass + MFMA GEMM."""
+    down 3072 x 8192.  Each call = fp16 activation pre-pass + MFMA GEMM (+ a
+    split-K reduction when the tile grid is small)."""
     out = {}
     for name, n, m in (("gate_up", 8192, 3072), ("down", 3072, 8192)):
-        out[name] = q4_case(torch, lib, n, m, 512, seed=7 + n, reps=20)
+        out[name] = q4_case(torch, lib, n, m, 512, seed=7 + n, reps=20, exact_too=True)
     return {"workload": "configs[2] Llama-3.2-3B MLP, M=512, Q4_0; GPU time per call incl. "
-                        "the fp16 activation pre-pass", "results": out}
-
-
-MISTRAL = [("q_o", 4096, 4096), ("k_v", 1024, 4096), ("gate_up", 14336, 4096),
-           ("down", 4096, 14336)]
-
-
-def mistral_stream(torch, lib, steps=10, warmup=3):
-    """configs[3] at M = 1 as a decode step streams it: the 224 Q4_0 GEMVs of
-    Mistral-7B (32 layers x q, k, v, o, gate, up, down; 3.93 GB) as one plan
-    launch, launched back to back."""
-    import hypno_amd as hk
-    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    per_layer = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096),
-                 (14336, 4096), (4096, 14336)]
-    shapes = per_layer * 32
-    arena, offs = make_q4_arena(torch, lib, shapes, seed=11, stream=st)
-    xs = {4096: torch.randn(4096, device="cuda"), 14336: torch.randn(14336, device="cuda")}
-    ys = [torch.empty(n, device="cuda") for n, _ in shapes]
-    plan = hk.GemvPlan([(ys[i], arena[o:o + nb], xs[m], None, n, m)
-                        for i, ((n, m), (o, nb)) in enumerate(zip(shapes, offs))])
-    wb = sum(nb for _, nb in offs)
-    ms = time_launches(torch, plan.run, steps, warmup)
-    plan.close()
-    del arena, ys
-    torch.cuda.empty_cache()
-    gbs = wb / (ms * 1e-3) / 1e9
-    return {"workload": "configs[3] M=1: Mistral-7B decode-step weight stream, 224 Q4_0 "
-                        "GEMVs as one plan launch", "weight_bytes": wb, "us": round(ms * 1e3, 1),
-            "weight_gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+                        "the fp16 activation pre-pass (the BASELINE outlier channels are "
+                        "exercised by the parity tests)", "results": out}
 
 
 def mistral_m_sweep(torch, lib):
     """Mistral-7B projections at M in {1, 8, 64, 512, 2048}."""
     out = {}
-    for name, n, m in MISTRAL:
+    for name, n, m in MISTRAL_SHAPES:
         for M in (1, 8, 64, 512, 2048):
             out[f"{name}_M{M}"] = q4_case(torch, lib, n, m, M, seed=n + m + M,
-                                          reps=20 if M <= 64 else 4)
+                                          reps=20 if M <= 64 else 4, exact_too=M >= 512)
     return {"workload": "configs[3] Mistral-7B q/o, k/v, gate/up, down at M in "
                         "{1,8,64,512,2048}; GPU time per call (graph replay); M <= 64 "
-                        "rotates >= 512 MB of weight copies", "results": out}
+                        "rotates >= 512 MB of weight copies; M >= 512 also in the "
+                        "exact-nibble arithmetic", "results": out}
 
 
 def lm_head(torch, lib):
     """K = 4096, N = 128256, M in {1, 128}, Q4_0 and FP16 weights."""
+    import numpy as np
     n, m = 128256, 4096
     out = {}
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -360,7 +578,7 @@ def lm_head(torch, lib):
     gen = torch.Generator(device="cuda").manual_seed(18)
     w16 = torch.randn(n * m, generator=gen, device="cuda").mul_(0.02).half()
     for M in (1, 128):
-        x = torch.randn(M, m, device="cuda")
+        x = torch.randn(M, m, generator=gen, device="cuda")
         y = torch.empty(M, n, device="cuda")
         xp, yp = ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr())
         for dt, nb in (("q4_0", offs[0][1]), ("f16", w16.numel() * 2)):
@@ -373,12 +591,24 @@ def lm_head(torch, lib):
                         yp, ctypes.c_void_p(w16.data_ptr()), nb, xp, None, n, m, M, sp)
                 if rc:
                     lib.check(rc, "lm_head")
-            us = time_calls_graph(torch, issue, reps=5)
-            out[f"{dt}_M{M}"] = {"us": round(us, 1), "weight_gbs": round(nb / us / 1e3, 1),
-                                 "tflops": round(2.0 * M * n * m / us / 1e6, 2),
-                                 "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4),
-                                 "frac_fp16_peak": round(2.0 * M * n * m / us / 1e6 /
-                                                         FP16_PEAK_TFLOPS, 4)}
+            r = result(time_calls_graph(torch, issue, reps=5), M, n, m, nb)
+            y.fill_(float("nan"))
+            issue(st, 0)
+            torch.cuda.synchronize()
+            if dt == "q4_0":
+                r["check"] = check_q4(torch, arena, 0, n, m, x, y, M, seed=M, count=256)
+            else:
+                cols = np.union1d(sample_idx(n, 256, M), np.arange(n - 64, n))
+                wv = w16.view(n, m)[torch.as_tensor(cols, device="cuda")].double().cpu().numpy()
+                ref = x.double().cpu().numpy() @ wv.T
+                got = y[:, torch.as_tensor(cols, device="cuda")].cpu().numpy()
+                err = (max(normwise(got[t], ref[t]) for t in range(M)) if M == 1
+                       else rel_l2(got, ref))
+                tol = GEMV_TOL if M == 1 else GEMM_TOL
+                r["check"] = {"checked": err <= tol, "max_err": float(f"{err:.3g}"),
+                              "bar": "normwise 1e-4" if M == 1 else "rel-L2 2e-3",
+                              "sampled_cols": len(cols)}
+            out[f"{dt}_M{M}"] = r
         del x, y
     del arena, w16
     torch.cuda.empty_cache()
@@ -394,8 +624,19 @@ def q8_0_decode(torch, lib):
     import hypno_amd as hk
     out = {}
     gen = torch.Generator(device="cuda").manual_seed(88)
-    for name, n, m in (("q_o", 4096, 4096), ("k_v", 1024, 4096), ("gate_up", 14336, 4096),
-                       ("down", 4096, 14336)):
+
+    def chk(arena, n, m, x, y, M, seed):
+        cols = sample_idx(n, 64, seed)
+        raw = gather_rows(torch, arena, 0, n, m // 32 * 34, cols)
+        ref = x.reshape(M, m).double().cpu().numpy() @ q8_rows_f64(raw).T
+        got = y.reshape(M, n)[:, torch.as_tensor(cols, device="cuda")].cpu().numpy()
+        err = normwise(got[0], ref[0]) if M == 1 else rel_l2(got, ref)
+        tol = GEMV_TOL if M == 1 else GEMM_TOL
+        return {"checked": err <= tol, "max_err": float(f"{err:.3g}"),
+                "bar": "normwise 1e-4" if M == 1 else "rel-L2 2e-3", "sampled_cols": len(cols)}
+
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for name, n, m in MISTRAL_SHAPES:
         nb = n * m // 32 * 34
         stride = (nb + 255) // 256 * 256
         copies = max(2, -(-(512 * 2**20) // nb))
@@ -415,9 +656,11 @@ def q8_0_decode(torch, lib):
             if rc:
                 lib.check(rc, "matmul_q8_0")
 
-        us = time_calls_graph(torch, issue, reps=copies * 4)
-        out[f"{name}_M1"] = {"us": round(us, 2), "weight_gbs": round(nb / us / 1e3, 1),
-                             "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
+        r = result(time_calls_graph(torch, issue, reps=copies * 4), 1, n, m, nb)
+        issue(st, 0)
+        torch.cuda.synchronize()
+        r["check"] = chk(arena, n, m, x, y, 1, n)
+        out[f"{name}_M1"] = r
         if name == "gate_up":
             # prefill: weights expanded to fp16 once per call, fp16 MFMA GEMM
             M = 512
@@ -431,11 +674,11 @@ def q8_0_decode(torch, lib):
                 if rc:
                     lib.check(rc, "matmul_q8_0 M=512")
 
-            us = time_calls_graph(torch, issue_m, reps=5)
-            out[f"{name}_M{M}"] = {"us": round(us, 2),
-                                   "tflops": round(2.0 * M * n * m / us / 1e6, 2),
-                                   "frac_fp16_peak": round(2.0 * M * n * m / us / 1e6 /
-                                                           FP16_PEAK_TFLOPS, 4)}
+            r = result(time_calls_graph(torch, issue_m, reps=5), M, n, m, nb)
+            issue_m(st, 0)
+            torch.cuda.synchronize()
+            r["check"] = chk(arena, n, m, xm, ym, M, n + 1)
+            out[f"{name}_M{M}"] = r
             del xm, ym
         del arena, x, y
         torch.cuda.empty_cache()
@@ -448,9 +691,14 @@ def col_major(torch, lib):
     """Column-major Q4_0 (kernels.rs:403-535) at the Mistral-7B shapes, M = 1:
     W_col[m][n] streamed once per call (plus the fixed-order split
     reduction), rotating >= 512 MB of weight copies."""
+    import numpy as np
     out = {}
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     for name, n, m in (("q_o", 4096, 4096), ("gate_up", 14336, 4096), ("down", 4096, 14336)):
-        arena, ptrs, nb = rotating_q4(torch, lib, m, n, seed=n + m)  # m columns of n outputs
+        nb = q4_bytes(m, n)  # m columns of n outputs
+        copies = max(2, -(-(512 * 2**20) // nb))
+        arena, offs = make_q4_arena(torch, lib, [(m, n)] * copies, seed=n + m, stream=st)
+        ptrs = [arena.data_ptr() + off for off, _ in offs]
         x = torch.randn(m, device="cuda")
         y = torch.empty(n, device="cuda")
         xp, yp = ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr())
@@ -461,9 +709,22 @@ def col_major(torch, lib):
             if rc:
                 lib.check(rc, "matmul_q4_0_col")
 
-        us = time_calls_graph(torch, issue, reps=len(ptrs) * 2)
-        out[f"{name}_M1"] = {"us": round(us, 2), "weight_gbs": round(nb / us / 1e3, 1),
-                             "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
+        r = result(time_calls_graph(torch, issue, reps=len(ptrs) * 2), 1, n, m, nb)
+        issue(st, 0)
+        torch.cuda.synchronize()
+        # outputs of a few block columns: block b of every input row k
+        nbk = n // 32
+        blocks = sample_idx(nbk, 8, n)
+        view = arena[:nb].view(m, nbk, 18)
+        raw = view[:, torch.as_tensor(blocks, device="cuda"), :].cpu().numpy()  # [m, b, 18]
+        w = q4_rows_f64(raw.reshape(m * len(blocks), 18)).reshape(m, len(blocks), 32)
+        ref = np.einsum("kbj,k->bj", w, x.double().cpu().numpy()).ravel()
+        cols = (blocks[:, None] * 32 + np.arange(32)[None, :]).ravel()
+        got = y[torch.as_tensor(cols, device="cuda")].cpu().numpy()
+        err = normwise(got, ref)
+        r["check"] = {"checked": err <= GEMV_TOL, "max_err": float(f"{err:.3g}"),
+                      "bar": "normwise 1e-4", "sampled_cols": len(cols)}
+        out[f"{name}_M1"] = r
         del arena, x, y
         torch.cuda.empty_cache()
     return {"workload": "column-major Q4_0 Mistral-7B projections, M = 1, rotating >= 512 MB "
@@ -517,7 +778,7 @@ def model_load(torch, lib):
 
     import hypno_amd as hk
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    shapes = [(n, m) for _ in range(LAYERS) for (_, n, m) in TINYLLAMA]
+    shapes = [(n, m) for _ in range(TINYLLAMA_LAYERS) for (_, n, m) in TINYLLAMA]
     arena, offs = make_q4_arena(torch, lib, shapes, seed=4321, stream=st)
     host = arena.cpu().numpy()
     del arena
@@ -537,17 +798,31 @@ def model_load(torch, lib):
     try:
         path = os.path.join(tmp, "tinyllama_q4_0.hypno")
         size = write_hypno(path, [("architecture", "LlamaForCausalLM"),
-                                  ("num_hidden_layers", str(LAYERS)),
+                                  ("num_hidden_layers", str(TINYLLAMA_LAYERS)),
                                   ("weight_layout", "row_major")], tensors)
         hk.HypnoModel.open(path, device=False).close()
         up, parse = [], []
-        for _ in range(3):
+        for it in range(3):
             t0 = time.perf_counter()
-            m = hk.HypnoModel.open(path)
+            mdl = hk.HypnoModel.open(path)
             up.append(time.perf_counter() - t0)
-            infos = m.manifest.tensors
+            infos = mdl.manifest.tensors
             span = infos[-1].offset + infos[-1].data_len - (infos[0].offset // ALIGN * ALIGN)
-            m.close()
+            if it == 0:  # the uploaded payloads are the file's bytes (a sample of tensors)
+                ok, picked = True, list(range(0, len(infos), 17)) + [len(infos) - 1]
+                for ti in picked:
+                    name = infos[ti].name
+                    ptr, nbytes, _ = mdl.device_tensor(name)
+                    dev = torch.empty(nbytes, dtype=torch.uint8)
+                    torch.cuda.synchronize()
+                    if hip_memcpy_d2h(dev.data_ptr(), ptr, nbytes) != 0:
+                        ok = False
+                        continue
+                    hb = np.frombuffer(mdl.get_tensor_data(name)[0], np.uint8)
+                    ok &= bool(np.array_equal(dev.numpy(), hb))
+                load_check = {"checked": ok, "bar": "uploaded bytes equal the file's",
+                              "tensors_compared": len(picked)}
+            mdl.close()
             t0 = time.perf_counter()
             hk.HypnoModel.open(path, device=False).close()
             parse.append(time.perf_counter() - t0)
@@ -578,15 +853,20 @@ def model_load(torch, lib):
             "upload_gbs": round(span / t_up / 1e9, 2),
             "frac_pcie_peak": round(span / t_up / 1e9 / PCIE_PEAK_GBS, 3),
             "host_only_open_ms": round(sorted(parse)[1] * 1e3, 3),
-            "pageable_copy_gbs": round(span / t_naive / 1e9, 2)}
+            "pageable_copy_gbs": round(span / t_naive / 1e9, 2), "check": load_check}
 
 
-def single_gemv(torch, lib):
-    """configs[0]: one 2048 x 2048 Q4_0 GEMV (TinyLlama q_proj), M = 1."""
-    r = q4_case(torch, lib, 2048, 2048, 1, seed=2048, reps=50)
-    r["workload"] = ("configs[0] 2048x2048 Q4_0 GEMV, M=1; GPU time per call, >= 512 MB "
-                     "of rotating weight copies")
-    return r
+def hip_memcpy_d2h(dst, src, nbytes):
+    """hipMemcpy device -> host through the HIP runtime that torch loaded."""
+    for name in ("libamdhip64.so", "libamdhip64.so.7", "libamdhip64.so.6",
+                 "/opt/rocm/lib/libamdhip64.so"):
+        try:
+            h = ctypes.CDLL(name)
+        except OSError:
+            continue
+        h.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        return h.hipMemcpy(ctypes.c_void_p(dst), ctypes.c_void_p(src), nbytes, 2)
+    return -1
 
 
 def copy_probe(torch, nbytes=1 << 30, reps=20):
@@ -595,21 +875,24 @@ def copy_probe(torch, nbytes=1 << 30, reps=20):
     src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
-    ms = time_launches(torch, lambda: dst.copy_(src), reps, 2)
+    ms, _ = time_launches(torch, lambda: dst.copy_(src), reps, 2)
     print(json.dumps({"copy_probe_bytes": nbytes, "ms": round(ms, 4),
                       "gbs_each_way": round(nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_0_gemv_jobs_kernel_tinyllama_stream_traffic.txt")
+MISTRAL_TRAFFIC_FILE = os.path.join(ROOT, "profiles",
+                                    "q4_0_gemv_jobs_kernel_mistral7b_stream_traffic.txt")
+TINY_TRAFFIC_FILE = os.path.join(ROOT, "profiles",
+                                 "q4_0_gemv_jobs_kernel_tinyllama_stream_traffic.txt")
 
 
-def stream_traffic():
-    """HBM bytes per launch of the decode-stream GEMV, from the committed
+def stream_traffic(path):
+    """HBM bytes per launch of a decode-stream GEMV, from a committed
     rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE per dispatch, each divided
     by the factor the same counter reads on a plain copy of known size)."""
     try:
         kv = {}
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             for ln in f:
                 if "=" in ln and not ln.startswith("#"):
                     k, v = ln.split("=", 1)
@@ -619,41 +902,92 @@ def stream_traffic():
         return None
 
 
-def cpu_baseline(sample, x_host, seconds):
-    """hypno's AVX2 Q4_0 kernel (restated in oracle/) on this host's cores."""
-    from oracle import oracle as orc
-    threads = max(1, min(16, os.cpu_count() or 1))
-    orc.set_threads(threads)
-    mats = list(zip(sample, TINYLLAMA))
-    for q, (_, n, m) in mats:  # warm-up (bench.rs:121)
-        orc.matmul_q4_0(q, x_host[m], None, n, m)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        for q, (_, n, m) in mats:
-            orc.matmul_q4_0(q, x_host[m], None, n, m)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and reps >= 3:
-            break
-    layer_bytes = sum(q.size for q in sample)
-    gbs = layer_bytes * reps / el / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "avx2": orc.have_avx2_fma(),
-            "sample": f"TinyLlama layer 0 (7 GEMVs, {layer_bytes} weight bytes) x {reps} reps "
-                      f"in {el:.1f} s, OpenMP row-parallel"}
+# --- CPU baseline -----------------------------------------------
 
+def host_description():
+    """nproc, CPU share, sockets, NUMA nodes and CPU model of this host."""
+    d = {"nproc": len(os.sched_getaffinity(0)), "host_cpus": os.cpu_count()}
+    try:
+        with open("/proc/cpuinfo") as f:
+            info = f.read()
+        models = {ln.split(":", 1)[1].strip() for ln in info.splitlines()
+                  if ln.startswith("model name")}
+        d["cpu_model"] = "; ".join(sorted(models))
+        sockets = {ln.split(":", 1)[1].strip() for ln in info.splitlines()
+                   if ln.startswith("physical id")}
+        d["sockets"] = len(sockets) or None
+    except OSError:
+        pass
+    d["numa_nodes"] = len(glob.glob("/sys/devices/system/node/node[0-9]*")) or None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, per = f.read().split()[:2]
+        d["cgroup_cpu_quota"] = None if q == "max" else round(int(q) / int(per), 2)
+    except (OSError, ValueError):
+        d["cgroup_cpu_quota"] = None
+    d["omp_num_threads_env"] = os.environ.get("OMP_NUM_THREADS")
+    return d
+
+
+def cpu_baseline(mats, x_host):
+    """hypno's AVX2 Q4_0 kernel (restated in oracle/, kernels.rs:270-359) on
+    this host, over the same 224-matrix Mistral-7B stream as the value: one
+    pass = one matmul_q4_0 call per matrix (row-parallel with OpenMP, as
+    rayon's par_iter_mut, kernels.rs:279).  Method of bench.rs:115-133: 3
+    warm-up passes, 10 timed, median; GB/s = weight bytes / time.  Runs on the
+    CPU share this process has (all host cores when nothing limits it) and on
+    8 threads (the published figures' thread count), threads bound
+    OMP_PROC_BIND=close, OMP_PLACES=cores (set before the oracle's OpenMP
+    runtime loads)."""
+    os.environ["OMP_PROC_BIND"] = "close"
+    os.environ["OMP_PLACES"] = "cores"
+    from oracle import oracle as orc
+    host = host_description()
+    share = host["nproc"]
+    if host.get("cgroup_cpu_quota"):
+        share = min(share, max(1, int(host["cgroup_cpu_quota"])))
+    if host.get("omp_num_threads_env", "").isdigit():
+        share = min(share, int(host["omp_num_threads_env"]))
+    total = sum(q.size for q, _, _ in mats)
+
+    def run(threads):
+        orc.set_threads(threads)
+        times = []
+        for it in range(13):
+            t0 = time.perf_counter()
+            for q, n, m in mats:
+                orc.matmul_q4_0(q, x_host[m], None, n, m)
+            if it >= 3:
+                times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        return {"threads": threads, "median_s": round(med, 4), "gbs": round(total / med / 1e9, 3),
+                "gflops": round(2.0 * sum(n * m for _, n, m in mats) / med / 1e9, 2)}
+
+    t0 = time.perf_counter()
+    share_run = run(share)
+    t8 = run(8) if share != 8 else share_run
+    elapsed = time.perf_counter() - t0
+    return {"value": share_run["gbs"], "unit": "GB/s", "cores": share, "kind": "port",
+            "avx2": orc.have_avx2_fma(), "threads_8": t8, "all_share": share_run,
+            "omp_proc_bind": "close", "omp_places": "cores", "host": host,
+            "sample": f"the full Mistral-7B decode stream ({len(mats)} matrices, {total} weight "
+                      f"bytes, above any host LLC) per pass; 3 warm-up + 10 timed passes per "
+                      f"thread count, median; {elapsed:.1f} s in all"}
+
+
+# --- main -------------------------------------------------------------------------------
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--value-only", action="store_true",
-                    help="time only the value's launches (no grouped/per-call variants, "
-                         "no secondary, no CPU baseline)")
+                    help="time only the value's launches (no secondary, no CPU baseline)")
+    ap.add_argument("--tinyllama-only", action="store_true",
+                    help="time only the TinyLlama stream plan (profiling its traffic)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run only a plain 1 GiB device copy, 20 times (HBM counter "
                          "calibration under rocprofv3 --pmc)")
@@ -662,7 +996,6 @@ def main():
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
               "(every GPU box here has one GPU)", file=sys.stderr)
         sys.exit(2)
-
     if args.value_only:
         args.no_secondary = args.no_cpu_baseline = True
 
@@ -673,45 +1006,27 @@ def main():
         copy_probe(torch)
         return
     lib = Lib()
+    if args.tinyllama_only:
+        import hypno_amd as hk
+        arena, offs, xs, jobs = build_stream(torch, lib, TINYLLAMA, TINYLLAMA_LAYERS, seed=1234)
+        plan = plan_of(hk, arena, jobs)
+        ms, _ = time_launches(torch, plan.run, args.steps, args.warmup)
+        print(json.dumps({"tinyllama_stream_ms": round(ms, 5)}), flush=True)
+        return
 
-    print("[bench] decode stream: building 545 MB of Q4_0 weights", file=sys.stderr, flush=True)
-    d = decode_stream(torch, lib, args.steps, args.warmup, value_only=args.value_only)
-    value = d["weight_bytes"] / (d["ms"] * 1e-3) / 1e9
-    print(f"[bench] decode stream {d['ms']:.4f} ms/step, {value:.1f} GB/s", file=sys.stderr,
+    print("[bench] Mistral-7B decode stream: building 3.93 GB of Q4_0 weights", file=sys.stderr,
           flush=True)
-    config = {
-        "workload": "TinyLlama-1.1B decode-step Q4_0 weight stream (configs[1]): 22 layers "
-                    "x {q,k,v,o,gate,up,down} GEMV, M=1, all 154 GEMVs as one "
-                    "multi-GEMV plan launch",
-        "weight_bytes": d["weight_bytes"],
-        "launches_per_step": d["launches"],
-        "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
-    }
-    if "ms_grouped" in d:
-        config["decode_step_grouped"] = {
-            "desc": "dependency-respecting decode step: per layer [q,k,v], [o], [gate,up], "
-                    "[down] plans, replayed as one HIP graph",
-            "launches": d["launches_grouped"],
-            "ms_per_step": round(d["ms_grouped"], 5),
-            "gbs": round(d["weight_bytes"] / (d["ms_grouped"] * 1e-3) / 1e9, 2)}
-        config["decode_step_fused"] = {
-            "desc": "the grouped decode step with RMS norm before [q,k,v] and [gate,up] and "
-                    "silu(gate)*up before [down] applied inside the GEMVs' activation staging",
-            "launches": d["launches_fused"],
-            "ms_per_step": round(d["ms_fused"], 5),
-            "vs_separate_kernels_ms": round(d["ms_separate"], 5),
-            "separate_launches": d["launches_separate"]}
-        config["per_call"] = {
-            "desc": "drop-in path: one hypno_hip_matmul_q4_0_dev call per matrix, "
-                    "replayed as one HIP graph",
-            "launches": d["launches_per_call"],
-            "ms_per_step": round(d["ms_per_call"], 5),
-            "gbs": round(d["weight_bytes"] / (d["ms_per_call"] * 1e-3) / 1e9, 2)}
+    d = mistral_stream(torch, lib, args.steps, args.warmup)
+    wb = d["weight_bytes"]
+    value = wb / (d["ms"] * 1e-3) / 1e9
+    print(f"[bench] decode stream {d['ms']:.4f} ms/step, {value:.1f} GB/s, checked "
+          f"{d['check']['checked']}", file=sys.stderr, flush=True)
     # One kernel launch per step: the launch's average duration over the timed
-    # region is the step time (it includes the few-microsecond gap between
-    # back-to-back launches).
+    # region is the step time (it includes the gap between back-to-back
+    # launches, a few microseconds).
     launch_ms = d["ms"] / d["launches"]
-    achieved = d["weight_bytes"] / d["launches"] / (launch_ms * 1e-3) / 1e9
+    achieved = wb / d["launches"] / (launch_ms * 1e-3) / 1e9
+    n_mats = len(d["jobs"])
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -723,33 +1038,67 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": "i4 weights x i19 activation limbs (i32 dots), f32 accumulate",
         "data": "synthetic: weights N(0,0.02) seeded, Q4_0-quantised on GPU; x N(0,1)",
-        "config": config,
+        "config": {
+            "workload": "Mistral-7B decode-step Q4_0 weight stream (configs[3] at M=1): 32 "
+                        "layers x {q,k,v,o,gate,up,down} GEMV, all 224 GEMVs as one "
+                        "multi-GEMV plan launch, launched back to back",
+            "weight_bytes": wb,
+            "matrices": n_mats,
+            "launches_per_step": d["launches"],
+            "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+            "check": d["check"],
+            **ref_fields(d["ms"] * 1e3, 2.0 * sum(n * m for *_, n, m in d["jobs"]), wb),
+        },
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": stream_traffic(),
+            "traffic": stream_traffic(MISTRAL_TRAFFIC_FILE),
             "kernel": "q4_0_gemv_jobs_kernel",
             "launch_us": round(launch_ms * 1e3, 2),
-            "bytes_per_launch": d["weight_bytes"] // d["launches"],
+            "bytes_per_launch": wb // d["launches"],
+            "per_launch": launch_stats(d["per"], wb),
         },
     }
+    cpu_mats = None
+    if not args.no_cpu_baseline:
+        arena = d["arena"]
+        cpu_mats = [(arena[off:off + nb].cpu().numpy(), n, m)
+                    for (off, nb), (_, _, _, _, _, n, m) in zip(d["offs"], d["jobs"])]
+        x_host = {m: x.cpu().numpy() for *_, x, n, m in d["jobs"][:7]}
+    del d
+    torch.cuda.empty_cache()
     if not args.no_secondary:
         sec = {}
-        for key, fn in (("c0_single_gemv", single_gemv), ("c2_prefill_gemm", prefill_gemm),
-                        ("c3_mistral_stream", mistral_stream), ("c3_m_sweep", mistral_m_sweep),
+        for key, fn in (("c0_single_gemv", single_gemv), ("c1_tinyllama_stream", None),
+                        ("c2_prefill_gemm", prefill_gemm), ("c3_m_sweep", mistral_m_sweep),
                         ("c4_lm_head", lm_head), ("model_load", model_load),
                         ("q8_0_decode", q8_0_decode), ("col_major", col_major)):
             print(f"[bench] secondary: {key}", file=sys.stderr, flush=True)
-            sec[key] = fn(torch, lib)
+            if fn is None:
+                sec[key] = tinyllama_stream(torch, lib, args.steps, args.warmup)
+            else:
+                sec[key] = fn(torch, lib)
         line["secondary"] = sec
-    if not args.no_cpu_baseline:
+        checks = []
+
+        def walk(o):
+            if isinstance(o, dict):
+                for k, v in o.items():
+                    if k in ("check", "separate_check") and isinstance(v, dict):
+                        checks.append(v.get("checked", False))
+                    else:
+                        walk(v)
+        walk(sec)
+        line["all_checked"] = bool(checks) and all(checks) and line["config"]["check"]["checked"]
+        line["checks_run"] = len(checks) + 1
+    if cpu_mats is not None:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        line["cpu_baseline"] = cpu_baseline(d["sample"], d["x_host"], args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(cpu_mats, x_host)
     print(json.dumps(line), flush=True)
 
 

@@ -5,6 +5,8 @@ C ABI of include/hypno_hip.h); this package is its Python face and mirrors
 the reference's function names (see hypno_amd.kernels).
 """
 from .kernels import (  # noqa: F401
+    GEMM_AUTO,
+    GEMM_EXACT,
     DType,
     GemvPlan,
     HypnoHipError,
@@ -25,6 +27,7 @@ from .kernels import (  # noqa: F401
     register_weight,
     rms_norm,
     rms_norm_in_place,
+    set_gemm_numerics,
     silu_mul,
     unregister_weight,
 )

@@ -5,11 +5,15 @@
 // weight-residency registry.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <mutex>
+#include <set>
 #include <string>
 #include <vector>
 
@@ -69,12 +73,22 @@ hipError_t ensure(DevBuf& b, size_t bytes, hipStream_t sync) {
   return hipSuccess;
 }
 
+// Workspace of one (device, stream).  Its mutex is held from the size check
+// through the last launch of a call, so two threads calling on one stream
+// neither free a buffer the other is about to launch with nor interleave
+// their multi-kernel sequences (pre-pass, GEMM, reduction); a buffer is only
+// replaced after the stream has drained.
+struct StreamWs {
+  std::mutex mu;
+  DevBuf buf;
+};
+
 struct DeviceState {
   bool init = false;
   int cus = 256;
   hipStream_t stream = nullptr;  // used by the host-slice entry points
   DevBuf w, x, y, bias;          // host-slice staging
-  std::map<hipStream_t, DevBuf> workspaces;
+  std::map<hipStream_t, std::unique_ptr<StreamWs>> workspaces;
 };
 
 struct Registered {
@@ -115,6 +129,48 @@ int device_state(DeviceState** out) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// A locked workspace: valid (and exclusively this caller's on its stream)
+// until the object goes out of scope.
+struct WsLock {
+  std::unique_lock<std::mutex> lk;
+  void* p = nullptr;
+};
+
+// Locks stream s's workspace on the device of `ds` and grows it to `bytes`.
+int lock_workspace(DeviceState* ds, hipStream_t s, size_t bytes, WsLock& out,
+                   const char* what) {
+  StreamWs* w = nullptr;
+  {
+    std::lock_guard<std::mutex> g(g_mu);
+    std::unique_ptr<StreamWs>& slot = ds->workspaces[s];
+    if (!slot) slot.reset(new StreamWs());
+    w = slot.get();
+  }
+  out.lk = std::unique_lock<std::mutex>(w->mu);
+  hipError_t e = ensure(w->buf, bytes, s);
+  if (e != hipSuccess) return hip_fail(e, what);
+  out.p = w->buf.p;
+  return HYPNO_HIP_OK;
+}
+
+// [a, a + na) and [b, b + nb) share a byte (empty ranges share none).
+bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
+  if (!a || !b || !na || !nb) return false;
+  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+  return x < y + nb && y < x + na;
+}
+
+// The output of a device call may not share memory with any of its inputs
+// (the reference takes `y: &mut [f32]` beside shared borrows of the rest,
+// which Rust keeps disjoint).
+int check_disjoint(const float* y, size_t ybytes, const void* w, size_t wbytes, const float* x,
+                   size_t xbytes, const float* bias, size_t bbytes) {
+  if (overlaps(y, ybytes, x, xbytes) || overlaps(y, ybytes, w, wbytes) ||
+      overlaps(y, ybytes, bias, bbytes))
+    return fail(HYPNO_HIP_EINVAL, "y overlaps an input buffer");
+  return HYPNO_HIP_OK;
+}
+
 bool mul_overflows(size_t a, size_t b) { return a != 0 && b > SIZE_MAX / a; }
 
 // --- dispatch on device pointers (caller holds no lock) ---------------------
@@ -126,42 +182,35 @@ int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
   if (!w && w_len) return fail(HYPNO_HIP_EINVAL, "w_q is NULL but w_len > 0");
   if (mul_overflows(n, batch) || mul_overflows(m, batch) || mul_overflows(n, m))
     return fail(HYPNO_HIP_EINVAL, "shape overflows size_t");
+  int st = check_disjoint(y, n * batch * 4, w, w_len, x, m * batch * 4, bias, bias ? n * 4 : 0);
+  if (st) return st;
   int cus = 256;
   DeviceState* ds = nullptr;
   {
     std::lock_guard<std::mutex> g(g_mu);
-    int st = device_state(&ds);
+    st = device_state(&ds);
     if (st) return st;
     cus = ds->cus;
   }
   hipError_t e;
   if (batch >= 2 && batch <= kSkinnyMaxBatch && q4_0_skinny_ok(w, w_len, n, m, batch, cus) &&
       aligned16(x)) {
-    void* ws = nullptr;
-    {
-      std::lock_guard<std::mutex> g(g_mu);
-      DevBuf& b = ds->workspaces[s];
-      e = ensure(b, skinny_workspace_bytes(batch, n, m, cus), s);
-      if (e != hipSuccess) return hip_fail(e, "skinny workspace");
-      ws = b.p;
-    }
-    e = launch_q4_0_skinny(y, w, x, bias, n, m, batch, ws, cus, s);
+    WsLock ws;
+    st = lock_workspace(ds, s, skinny_workspace_bytes(batch, n, m, cus), ws, "skinny workspace");
+    if (st) return st;
+    e = launch_q4_0_skinny(y, w, x, bias, n, m, batch, ws.p, cus, s);
     if (e != hipSuccess) return hip_fail(e, "q4_0 skinny launch");
     return HYPNO_HIP_OK;
   }
   const bool v3 = batch >= kGemmMinBatch && q4_0_gemm_v3_ok(w, w_len, n, m, batch);
   if (v3 || (batch >= kGemmMinBatch && q4_0_gemm_ok(w, w_len, n, m, batch))) {
-    void* ws = nullptr;
-    {
-      std::lock_guard<std::mutex> g(g_mu);
-      DevBuf& b = ds->workspaces[s];
-      e = ensure(b, v3 ? gemm_v3_workspace_bytes(batch, n, m, cus) : gemm_workspace_bytes(batch, m),
-                 s);
-      if (e != hipSuccess) return hip_fail(e, "GEMM workspace");
-      ws = b.p;
-    }
-    e = v3 ? launch_q4_0_gemm_v3(y, w, x, bias, n, m, batch, ws, cus, s)
-           : launch_q4_0_gemm(y, w, x, bias, n, m, batch, ws, cus, s);
+    WsLock ws;
+    st = lock_workspace(
+        ds, s, v3 ? gemm_v3_workspace_bytes(batch, n, m, cus) : gemm_workspace_bytes(batch, m),
+        ws, "GEMM workspace");
+    if (st) return st;
+    e = v3 ? launch_q4_0_gemm_v3(y, w, x, bias, n, m, batch, ws.p, cus, s)
+           : launch_q4_0_gemm(y, w, x, bias, n, m, batch, ws.p, cus, s);
     if (e != hipSuccess) return hip_fail(e, "q4_0 GEMM launch");
     return HYPNO_HIP_OK;
   }
@@ -192,28 +241,23 @@ int q8_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
     return fail(HYPNO_HIP_EINVAL, "Q8_0 weights: %zu bytes hold fewer than n*m = %zu elements",
                 w_len, n * m);
   if (!w && n * m) return fail(HYPNO_HIP_EINVAL, "w is NULL");
+  int st = check_disjoint(y, n * batch * 4, w, w_len, x, m * batch * 4, bias, bias ? n * 4 : 0);
+  if (st) return st;
   int cus = 256;
+  DeviceState* ds = nullptr;
   {
     std::lock_guard<std::mutex> g(g_mu);
-    DeviceState* ds = nullptr;
-    int st = device_state(&ds);
+    st = device_state(&ds);
     if (st) return st;
     cus = ds->cus;
   }
   hipError_t e;
   if (batch >= kGemmMinBatch && q8_0_gemm_ok(n, m, batch)) {
-    void* ws = nullptr;
-    {
-      std::lock_guard<std::mutex> g(g_mu);
-      DeviceState* ds = nullptr;
-      int st = device_state(&ds);
-      if (st) return st;
-      DevBuf& b = ds->workspaces[s];
-      e = ensure(b, q8_0_gemm_workspace_bytes(batch, n, m, cus), s);
-      if (e != hipSuccess) return hip_fail(e, "Q8_0 GEMM workspace");
-      ws = b.p;
-    }
-    e = launch_q8_0_gemm(y, w, x, bias, n, m, batch, ws, cus, s);
+    WsLock ws;
+    st = lock_workspace(ds, s, q8_0_gemm_workspace_bytes(batch, n, m, cus), ws,
+                        "Q8_0 GEMM workspace");
+    if (st) return st;
+    e = launch_q8_0_gemm(y, w, x, bias, n, m, batch, ws.p, cus, s);
     if (e != hipSuccess) return hip_fail(e, "q8_0 GEMM launch");
     return HYPNO_HIP_OK;
   }
@@ -239,26 +283,25 @@ int q4_0_col_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const
   if (mul_overflows(n, batch) || mul_overflows(m, batch) || m > 0x7FFFFFFF ||
       n / kBlockElems > 0x7FFFFFFF)
     return fail(HYPNO_HIP_EINVAL, "shape out of range");
+  int st = check_disjoint(y, n * batch * 4, w, w_len, x, m * batch * 4, bias, bias ? n * 4 : 0);
+  if (st) return st;
   int cus = 256;
   DeviceState* ds = nullptr;
   {
     std::lock_guard<std::mutex> g(g_mu);
-    int st = device_state(&ds);
+    st = device_state(&ds);
     if (st) return st;
     cus = ds->cus;
   }
-  void* ws = nullptr;
+  WsLock ws;
   const size_t wsb = q4_0_col_workspace_bytes(n, m, cus);
   hipError_t e;
   if (wsb) {
-    std::lock_guard<std::mutex> g(g_mu);
-    DevBuf& b = ds->workspaces[s];
-    e = ensure(b, wsb, s);
-    if (e != hipSuccess) return hip_fail(e, "column-major workspace");
-    ws = b.p;
+    st = lock_workspace(ds, s, wsb, ws, "column-major workspace");
+    if (st) return st;
   }
   for (size_t t = 0; t < batch; t++) {
-    e = launch_q4_0_col(y + t * n, w, w_len, x + t * m, bias, n, m, ws, cus, s);
+    e = launch_q4_0_col(y + t * n, w, w_len, x + t * m, bias, n, m, ws.p, cus, s);
     if (e != hipSuccess) return hip_fail(e, "column-major Q4_0 launch");
   }
   return HYPNO_HIP_OK;
@@ -275,25 +318,23 @@ int f16_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const floa
   if (w_len < 2 * n * m)
     return fail(HYPNO_HIP_EINVAL, "fp16 weights: w_len %zu < 2*n*m = %zu", w_len, 2 * n * m);
   if (!w && n * m) return fail(HYPNO_HIP_EINVAL, "w is NULL");
+  int st = check_disjoint(y, n * batch * 4, w, w_len, x, m * batch * 4, bias, bias ? n * 4 : 0);
+  if (st) return st;
   int cus = 256;
   DeviceState* ds = nullptr;
   {
     std::lock_guard<std::mutex> g(g_mu);
-    int st = device_state(&ds);
+    st = device_state(&ds);
     if (st) return st;
     cus = ds->cus;
   }
   hipError_t e;
   if (batch >= kGemmMinBatch && f16_gemm_v2_ok(w, n, m, batch)) {
-    void* ws = nullptr;
-    {
-      std::lock_guard<std::mutex> g(g_mu);
-      DevBuf& b = ds->workspaces[s];
-      e = ensure(b, f16_gemm_v2_workspace_bytes(batch, n, m, cus), s);
-      if (e != hipSuccess) return hip_fail(e, "GEMM workspace");
-      ws = b.p;
-    }
-    e = launch_f16_gemm_v2(y, w, x, bias, n, m, batch, ws, cus, s);
+    WsLock ws;
+    st = lock_workspace(ds, s, f16_gemm_v2_workspace_bytes(batch, n, m, cus), ws,
+                        "GEMM workspace");
+    if (st) return st;
+    e = launch_f16_gemm_v2(y, w, x, bias, n, m, batch, ws.p, cus, s);
     if (e != hipSuccess) return hip_fail(e, "f16 GEMM launch");
     return HYPNO_HIP_OK;
   }
@@ -397,6 +438,23 @@ int set_last_error(int status, const std::string& msg) {
 }
 
 int hip_status(hipError_t e, const char* what) { return hip_fail(e, what); }
+
+static std::atomic<uint32_t> g_gemm_numerics{HYPNO_HIP_GEMM_AUTO};
+
+bool gemm_force_exact() { return g_gemm_numerics.load() == HYPNO_HIP_GEMM_EXACT; }
+
+hipError_t set_lds_limit(const void* kernel, int bytes) {
+  static std::mutex mu;
+  static std::set<std::pair<const void*, int>> done;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> g(mu);
+  if (done.count({kernel, dev})) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done.insert({kernel, dev});
+  return e;
+}
 
 }  // namespace hypno
 
@@ -617,6 +675,48 @@ int close_group(hypno_hip_gemv_plan* pl, hypno_hip_gemv_plan::Group& grp,
   return HYPNO_HIP_OK;
 }
 
+// The jobs of a plan run concurrently in one launch: no job's y may share
+// memory with another job's y, nor with any job's inputs (x, w, bias and the
+// prologue operand aux).  Sorted write ranges make this O(count log count).
+int check_plan_disjoint(const hypno_hip_gemv_desc* descs, const hypno_hip_gemv_prologue* pros,
+                        size_t count) {
+  struct Range {
+    uintptr_t a, b;
+    size_t job;
+  };
+  std::vector<Range> writes, reads;
+  auto add = [](std::vector<Range>& v, const void* p, size_t bytes, size_t job) {
+    if (p && bytes) v.push_back({(uintptr_t)p, (uintptr_t)p + bytes, job});
+  };
+  for (size_t i = 0; i < count; i++) {
+    const hypno_hip_gemv_desc& d = descs[i];
+    if (d.n == 0) continue;
+    if (mul_overflows(d.n, 4) || mul_overflows(d.m, 4))
+      return fail(HYPNO_HIP_EINVAL, "plan_create: descriptor %zu shape overflows", i);
+    add(writes, d.y, d.n * 4, i);
+    add(reads, d.x, d.m * 4, i);
+    add(reads, d.w_q, d.w_len, i);
+    add(reads, d.bias, d.n * 4, i);
+    if (pros && pros[i].kind != HYPNO_HIP_PROLOGUE_NONE) add(reads, pros[i].aux, d.m * 4, i);
+  }
+  std::sort(writes.begin(), writes.end(),
+            [](const Range& p, const Range& q) { return p.a < q.a; });
+  for (size_t i = 1; i < writes.size(); i++)
+    if (writes[i].a < writes[i - 1].b)
+      return fail(HYPNO_HIP_EINVAL, "plan_create: y of descriptors %zu and %zu overlap",
+                  writes[i - 1].job, writes[i].job);
+  for (const Range& r : reads) {
+    // first write range ending after r starts (ends are sorted like starts)
+    auto it = std::lower_bound(writes.begin(), writes.end(), r.a,
+                               [](const Range& w, uintptr_t a) { return w.b <= a; });
+    if (it != writes.end() && it->a < r.b)
+      return fail(HYPNO_HIP_EINVAL,
+                  "plan_create: y of descriptor %zu overlaps an input of descriptor %zu", it->job,
+                  r.job);
+  }
+  return HYPNO_HIP_OK;
+}
+
 void free_plan(hypno_hip_gemv_plan* pl) {
   for (auto& g : pl->groups)
     if (g.d_jobs) (void)hipFree(g.d_jobs);
@@ -640,6 +740,10 @@ int hypno_hip_q4_0_gemv_plan_create_ex(const hypno_hip_gemv_desc* descs,
   if (!plan) return fail(HYPNO_HIP_EINVAL, "plan_create: NULL plan pointer");
   *plan = nullptr;
   if (!descs && count) return fail(HYPNO_HIP_EINVAL, "plan_create: NULL descriptors");
+  {
+    int st = check_plan_disjoint(descs, prologues, count);
+    if (st) return st;
+  }
   int cus = 256;
   {
     std::lock_guard<std::mutex> g(g_mu);
@@ -779,6 +883,14 @@ int hypno_hip_silu_mul_dev(float* out, const float* gate, const float* up, size_
   hipError_t e = launch_silu_mul(out, gate, up, n, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "silu_mul launch");
   return HYPNO_HIP_OK;
+}
+
+int hypno_hip_set_gemm_numerics(uint32_t mode) {
+  if (mode != HYPNO_HIP_GEMM_AUTO && mode != HYPNO_HIP_GEMM_EXACT) {
+    fail(HYPNO_HIP_EINVAL, "set_gemm_numerics: unknown mode %u", mode);
+    return -HYPNO_HIP_EINVAL;
+  }
+  return (int)g_gemm_numerics.exchange(mode);
 }
 
 int hypno_hip_stream_synchronize(void* stream) {

@@ -97,42 +97,72 @@ __device__ __forceinline__ u32x4 unpack8(uint32_t q) {
   return r;
 }
 
-// Group idx (row idx / (K/8), columns 8g..8g+7) of X fp32 [M][K] -> Xh fp16
-// [Mp][K], rows M..Mp-1 zero; with kPermute each group's 8 columns go in the
-// Q4_0 nibble-unpack order e0,e4,e1,e5,e2,e6,e3,e7.
+// Row r of X fp32 [M][K] -> row r of Xh fp16 [Mp][K], scaled by 2^sh with sh
+// chosen so that the row's largest |x| times 2^sh lies in [2^14, 2^15) (sh =
+// 0 for an all-zero row or one holding inf or NaN), and xexp[r] = -sh: the
+// consumer multiplies output row r by 2^xexp[r] (exact), so no token
+// overflows fp16 or sinks into fp16 subnormals because of its magnitude.
+// (Scaling by a power of two leaves the rounding of normal values unchanged.)
+// Rows M..Mp-1 are zero.  Called by a whole 256-thread work-group per row;
+// with kPermute each group of 8 columns goes in the Q4_0 nibble-unpack
+// order e0,e4,e1,e5,e2,e6,e3,e7.  K % 8 == 0.
 template <bool kPermute>
-__device__ __forceinline__ void x_to_f16_group(u32x4* __restrict__ xh, const float* __restrict__ x,
-                                               int M, int Mp, int K, size_t idx) {
-  const size_t groups = (size_t)K / 8;
-  if (idx >= (size_t)Mp * groups) return;
-  const size_t row = idx / groups;
-  float v[8];
-  if (row < (size_t)M) {
-    const float* src = x + idx * 8;  // row * K + g * 8
-    if (((uintptr_t)src & 15) == 0) {
-      const float4 a = load_global<float4>(src);
-      const float4 b = load_global<float4>(src + 4);
+__device__ __forceinline__ void x_row_to_f16(u32x4* __restrict__ xh, int* __restrict__ xexp,
+                                             const float* __restrict__ x, int M, int K, int r) {
+  __shared__ uint32_t red[4];
+  const int t = threadIdx.x;
+  const int groups = K / 8;
+  u32x4* dst = xh + (size_t)r * groups;
+  if (r >= M) {
+    for (int g = t; g < groups; g += 256) dst[g] = u32x4{0u, 0u, 0u, 0u};
+    if (t == 0) xexp[r] = 0;
+    return;
+  }
+  const float* src = x + (size_t)r * K;
+  const bool al = ((uintptr_t)src & 15) == 0;
+  auto load8 = [&](int g, float (&v)[8]) {
+    const float* p = src + (size_t)g * 8;
+    if (al) {
+      const float4 a = load_global<float4>(p);
+      const float4 b = load_global<float4>(p + 4);
       v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
       v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; i++) v[i] = src[i];
+      for (int i = 0; i < 8; i++) v[i] = p[i];
     }
-  } else {
+  };
+  uint32_t mb = 0;  // largest |x| by bit pattern (inf and NaN above every finite value)
+  for (int g = t; g < groups; g += 256) {
+    float v[8];
+    load8(g, v);
 #pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = 0.0f;
+    for (int i = 0; i < 8; i++) mb = max(mb, __float_as_uint(v[i]) & 0x7FFFFFFFu);
   }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, off, 64));
+  if ((t & 63) == 0) red[t >> 6] = mb;
+  __syncthreads();
+  mb = max(max(red[0], red[1]), max(red[2], red[3]));
+  const float amax = __uint_as_float(mb);
+  int sh = 0;
+  if (amax > 0.0f && amax < __builtin_inff()) sh = 15 - __builtin_amdgcn_frexp_expf(amax);
   constexpr int perm_q4[8] = {0, 4, 1, 5, 2, 6, 3, 7};
-  u32x4 packed;
+  for (int g = t; g < groups; g += 256) {
+    float v[8];
+    load8(g, v);
+    u32x4 packed;
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int a = kPermute ? perm_q4[2 * j] : 2 * j;
-    const int b = kPermute ? perm_q4[2 * j + 1] : 2 * j + 1;
-    const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)v[a]);
-    const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)v[b]);
-    packed[j] = lo | (hi << 16);
+    for (int j = 0; j < 4; j++) {
+      const int a = kPermute ? perm_q4[2 * j] : 2 * j;
+      const int b = kPermute ? perm_q4[2 * j + 1] : 2 * j + 1;
+      const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)ldexpf(v[a], sh));
+      const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)ldexpf(v[b], sh));
+      packed[j] = lo | (hi << 16);
+    }
+    dst[g] = packed;
   }
-  xh[idx] = packed;
+  if (t == 0) xexp[r] = -sh;
 }
 
 // Wave-wide sum (wave64) with xor butterflies; every lane gets the total.
@@ -257,13 +287,17 @@ hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
 // MFMA prefill GEMM.  Requires m % 64 == 0, w 4-byte aligned, w_len full.
 // `xh` is a device workspace of gemm_q4_0_workspace_bytes(batch, m) bytes.
 bool q4_0_gemm_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t batch);
+// Bytes of the fp16 activation copy [round_up(batch, 128)][m] followed by its
+// per-row exponents (x_row_to_f16), which gemm_x_exponents locates.
 size_t gemm_workspace_bytes(size_t batch, size_t m);
+int* gemm_x_exponents(void* ws, size_t batch, size_t m);
 hipError_t launch_q4_0_gemm(float* y, const uint8_t* w, const float* x, const float* bias,
                             size_t n, size_t m, size_t batch, void* workspace, int num_cus,
                             hipStream_t s);
 
 // X fp32 [batch][m] -> fp16 [round_up(batch,128)][m] workspace (zero pad
-// rows), each group of 8 columns permuted to the Q4_0 nibble-unpack order.
+// rows, each row scaled by its power of two, exponents after the rows), each
+// group of 8 columns permuted to the Q4_0 nibble-unpack order.
 hipError_t launch_x_f16_permuted(const float* x, size_t batch, size_t m, void* ws,
                                  hipStream_t s);
 
@@ -293,7 +327,12 @@ hipError_t launch_f16_generic(float* y, const uint8_t* w, const float* x, const 
 bool f16_gemv_fast_ok(const uint8_t* w, size_t n, size_t m);
 hipError_t launch_f16_gemv_fast(float* y, const uint8_t* w, const float* x, const float* bias,
                                 size_t n, size_t m, int num_cus, hipStream_t s);
-// X -> fp16 [Mp][K] in natural column order (FP16-weight GEMM pre-pass).
+// X fp32 [batch][m] -> `rows` (>= batch) fp16 rows at xh, per-row exponents
+// at xexp (x_row_to_f16; permuted or natural column order).
+hipError_t launch_x_rows_f16(const float* x, size_t batch, size_t rows, size_t m, void* xh,
+                            int* xexp, bool permute, hipStream_t s);
+// X -> fp16 [Mp][K] in natural column order, rows scaled as above
+// (FP16-weight GEMM pre-pass).
 hipError_t launch_x_f16_plain(const float* x, size_t batch, size_t m, void* ws, hipStream_t s);
 // DMA-fed FP16-weight GEMM (gemm_q4.hip).
 bool f16_gemm_v2_ok(const uint8_t* w, size_t n, size_t m, size_t batch);
@@ -322,5 +361,13 @@ hipError_t launch_silu_mul(float* out, const float* gate, const float* up, size_
 // to ENOMEM / EDEVICE the same way.
 int set_last_error(int status, const std::string& msg);
 int hip_status(hipError_t e, const char* what);
+
+// True when the caller asked for the exact-nibble GEMM arithmetic
+// (hypno_hip_set_gemm_numerics(HYPNO_HIP_GEMM_EXACT)).
+bool gemm_force_exact();
+
+// Raises `kernel`'s dynamic-LDS limit to `bytes` on the current device, once
+// per (kernel, device); safe to call from several threads (api.cpp).
+hipError_t set_lds_limit(const void* kernel, int bytes);
 
 }  // namespace hypno

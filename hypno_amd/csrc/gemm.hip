@@ -4,7 +4,8 @@
 // Y[M][N] = X[M][K] . W[N][K]^T (+ bias).
 //
 // Pre-pass: X (fp32) is rounded to fp16 into a workspace padded to a multiple
-// of the 128-row tile (float4 loads, one 16-byte store per 8 columns).  For
+// of the 128-row tile, each row scaled by a power of two (undone in the
+// epilogue) so that no token's magnitude takes it out of fp16's normal range.  For
 // Q4_0 weights each 8-column group is stored in the order [0,4,1,5,2,6,3,7],
 // the order in which one packed nibble dword unpacks into fp16 pairs (see
 // unpack_nib8), so both MFMA operands list the same columns in the same
@@ -40,7 +41,15 @@ constexpr int kTileHalves = kBM * kLdsRow;
 
 static size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-size_t gemm_workspace_bytes(size_t batch, size_t m) { return round_up(batch, kBM) * m * 2; }
+size_t gemm_workspace_bytes(size_t batch, size_t m) {
+  const size_t mp = round_up(batch, kBM);
+  return round_up(mp * m * 2, 256) + mp * 4;
+}
+
+int* gemm_x_exponents(void* ws, size_t batch, size_t m) {
+  return reinterpret_cast<int*>(static_cast<uint8_t*>(ws) +
+                                round_up(round_up(batch, kBM) * m * 2, 256));
+}
 
 bool q4_0_gemm_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t batch) {
   if (m == 0 || m % kBK != 0 || n == 0 || batch == 0) return false;
@@ -49,18 +58,18 @@ bool q4_0_gemm_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t bat
   return w_len / kBlockBytes >= n * (m / kBlockElems);
 }
 
-// X fp32 [M][K] -> Xh fp16 [Mp][K] (zero rows M..Mp-1); optionally zero Y.
-// One thread per 8-column group (x_to_f16_group).
+// X fp32 [M][K] -> Xh fp16 [Mp][K] with per-row exponents (x_row_to_f16),
+// one work-group per row; optionally zero Y (grid-stride over all of them).
 template <bool kPermute>
 __global__ void __launch_bounds__(256)
-x_to_f16_kernel(u32x4* __restrict__ xh, const float* __restrict__ x, int M, int Mp, int K,
-                float* __restrict__ y_zero, size_t y_elems) {
-  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+x_rows_to_f16_kernel(u32x4* __restrict__ xh, int* __restrict__ xexp, const float* __restrict__ x,
+                     int M, int K, float* __restrict__ y_zero, size_t y_elems) {
   if (y_zero) {
     const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t i = idx; i < y_elems; i += stride) y_zero[i] = 0.0f;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < y_elems; i += stride)
+      y_zero[i] = 0.0f;
   }
-  x_to_f16_group<kPermute>(xh, x, M, Mp, K, idx);
+  x_row_to_f16<kPermute>(xh, xexp, x, M, K, (int)blockIdx.x);
 }
 
 // One packed nibble dword (elements e0..e7, byte i = e[2i] | e[2i+1] << 4)
@@ -89,7 +98,8 @@ struct StepRegs {
 
 __global__ void __launch_bounds__(256, 2)
 gemm_kernel(float* __restrict__ y, const uint8_t* __restrict__ w, const u32x4* __restrict__ xh,
-            const float* __restrict__ bias, int M, int N, int K, int ksplit) {
+            const int* __restrict__ xexp, const float* __restrict__ bias, int M, int N, int K,
+            int ksplit) {
   extern __shared__ __align__(16) uint8_t smem[];
   // LDS: 2 x {A tile, B tile} fp16 + 2 x scales [2 blocks][128]
   _Float16* As0 = reinterpret_cast<_Float16*>(smem);
@@ -213,10 +223,11 @@ gemm_kernel(float* __restrict__ y, const uint8_t* __restrict__ w, const u32x4* _
         const int mrow = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + r;
         if (mrow >= M) continue;
         float* dst = y + (size_t)mrow * N + n;
+        const float v = ldexpf(acc[i][j][r], xexp[mrow]);
         if (ksplit == 1)
-          *dst = acc[i][j][r] + bv;
+          *dst = v + bv;
         else
-          atomicAdd(dst, acc[i][j][r] + bv);
+          atomicAdd(dst, v + bv);
       }
   }
 }
@@ -230,14 +241,24 @@ static int pick_ksplit(size_t tiles, size_t m, int num_cus) {
 static hipError_t launch_x_prepass(const float* x, size_t batch, size_t m, void* ws, bool permute,
                                    float* y_zero, size_t y_elems, hipStream_t s) {
   const size_t mp = round_up(batch, kBM);
-  const size_t work = mp * (m / 8);
-  const size_t grid = (work + 255) / 256;
+  int* xexp = gemm_x_exponents(ws, batch, m);
   if (permute)
-    hipLaunchKernelGGL(x_to_f16_kernel<true>, dim3((unsigned)grid), dim3(256), 0, s,
-                       (u32x4*)ws, x, (int)batch, (int)mp, (int)m, y_zero, y_elems);
+    hipLaunchKernelGGL(x_rows_to_f16_kernel<true>, dim3((unsigned)mp), dim3(256), 0, s,
+                       (u32x4*)ws, xexp, x, (int)batch, (int)m, y_zero, y_elems);
   else
-    hipLaunchKernelGGL(x_to_f16_kernel<false>, dim3((unsigned)grid), dim3(256), 0, s,
-                       (u32x4*)ws, x, (int)batch, (int)mp, (int)m, y_zero, y_elems);
+    hipLaunchKernelGGL(x_rows_to_f16_kernel<false>, dim3((unsigned)mp), dim3(256), 0, s,
+                       (u32x4*)ws, xexp, x, (int)batch, (int)m, y_zero, y_elems);
+  return hipGetLastError();
+}
+
+hipError_t launch_x_rows_f16(const float* x, size_t batch, size_t rows, size_t m, void* xh,
+                            int* xexp, bool permute, hipStream_t s) {
+  if (permute)
+    hipLaunchKernelGGL(x_rows_to_f16_kernel<true>, dim3((unsigned)rows), dim3(256), 0, s,
+                       (u32x4*)xh, xexp, x, (int)batch, (int)m, nullptr, (size_t)0);
+  else
+    hipLaunchKernelGGL(x_rows_to_f16_kernel<false>, dim3((unsigned)rows), dim3(256), 0, s,
+                       (u32x4*)xh, xexp, x, (int)batch, (int)m, nullptr, (size_t)0);
   return hipGetLastError();
 }
 
@@ -260,16 +281,12 @@ hipError_t launch_q4_0_gemm(float* y, const uint8_t* w, const float* x, const fl
                                   ksplit > 1 ? n * batch : 0, s);
   if (e != hipSuccess) return e;
   const size_t lds = 2 * ((size_t)2 * kTileHalves * 2 + 2 * kBN * 4);
-  static bool attr_set = false;
-  if (!attr_set) {
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  e = set_lds_limit(reinterpret_cast<const void*>(gemm_kernel), (int)lds);
+  if (e != hipSuccess) return e;
   const dim3 grid((unsigned)tiles_n, (unsigned)tiles_m, (unsigned)ksplit);
-  hipLaunchKernelGGL(gemm_kernel, grid, dim3(256), lds, s, y, w, (const u32x4*)ws, bias,
-                     (int)batch, (int)n, (int)m, ksplit);
+  hipLaunchKernelGGL(gemm_kernel, grid, dim3(256), lds, s, y, w, (const u32x4*)ws,
+                     (const int*)gemm_x_exponents(ws, batch, m), bias, (int)batch, (int)n, (int)m,
+                     ksplit);
   return hipGetLastError();
 }
 

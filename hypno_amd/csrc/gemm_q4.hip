@@ -138,20 +138,23 @@ struct Args {
   int splits;         // K split over blockIdx.y; > 1: fp32 partials to `part`
   float* part;        // [splits][M][N] partial sums (splits > 1)
   const int* rowexp;  // [N]: D_n = 2^rowexp[n] (kFold)
+  const int* xexp;    // [Mp]: row m of xh holds X row m times 2^-xexp[m]
 };
 
-// One launch before the folded-scale GEMM.  Work-groups [0, gx) round X to
-// fp16 (x_to_f16_group, permuted); the rest write rowexp[n] = e with
-// 2^(e-1) <= max |d| < 2^e over weight row n's blocks (0 when that maximum
-// is 0 or not finite), one wave per row, its scale loads four deep.
+// One launch before the folded-scale GEMM.  Work-groups [0, Mp) round X to
+// fp16, one row each (x_row_to_f16, permuted, per-row exponents); the rest
+// write rowexp[n] = e with 2^(e-1) <= max |d| < 2^e over weight row n's
+// blocks (0 when that maximum is 0 or not finite), one wave per row, its
+// scale loads four deep.
 __global__ void __launch_bounds__(256)
-q4_0_prepass_kernel(u32x4* __restrict__ xh, const float* __restrict__ x, int M, int Mp, int K,
-                    unsigned gx, int* __restrict__ rowexp, const uint8_t* __restrict__ w, int n) {
-  if (blockIdx.x < gx) {
-    x_to_f16_group<true>(xh, x, M, Mp, K, (size_t)blockIdx.x * blockDim.x + threadIdx.x);
+q4_0_prepass_kernel(u32x4* __restrict__ xh, int* __restrict__ xexp, const float* __restrict__ x,
+                    int M, int Mp, int K, int* __restrict__ rowexp,
+                    const uint8_t* __restrict__ w, int n) {
+  if ((int)blockIdx.x < Mp) {
+    x_row_to_f16<true>(xh, xexp, x, M, K, (int)blockIdx.x);
     return;
   }
-  const int row = (int)(((blockIdx.x - gx) * blockDim.x + threadIdx.x) >> 6);
+  const int row = (int)(((blockIdx.x - Mp) * blockDim.x + threadIdx.x) >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= n) return;  // wave-uniform
   const int bpr = K / kBlockElems;
@@ -380,7 +383,6 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
     for (int q = 0; q < 16; q++) {
       acc[q >> 2][q & 3] =
           __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[q >> 2], fb[q & 3], acc[q >> 2][q & 3], 0, 0, 0);
-      const int i1 = (q + 1 < 16) ? (q + 1) >> 2 : 3;
       if ((q & 3) == 3)
         fa[q >> 2] = *reinterpret_cast<const half8*>(smem + abase + (q >> 2) * 16 * kRowBytes);
       if (q >= 12)
@@ -465,9 +467,9 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   }
   __syncthreads();
   if (kgrp == 0) {
-    // Output column n is scaled by D_n = 2^rowexp[n] (kFold; exact).  Split K:
-    // this range's sum goes to its partial plane, the bias is added by the
-    // reduction.
+    // Output column n is scaled by D_n = 2^rowexp[n] (kFold) and row m by
+    // 2^xexp[m] (both exact).  Split K: this range's sum goes to its partial
+    // plane, the bias is added by the reduction.
     float* dst = a.splits > 1 ? a.part + (size_t)z * a.M * a.N : a.y;
     const float* bias = a.splits > 1 ? nullptr : a.bias;
 #pragma unroll
@@ -480,9 +482,9 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          const float v =
-              ldexpf(acc[i][j][r] + red[((wig * 64 + (i * 4 + j) * 4 + r) * 64) + lane], en);
           const int m = m0 + wm * 64 + 16 * i + 4 * lq + r;
+          const float v = ldexpf(acc[i][j][r] + red[((wig * 64 + (i * 4 + j) * 4 + r) * 64) + lane],
+                                 en + a.xexp[m]);
           if (nok && m < a.M) dst[(size_t)m * a.N + n] = v + bv;
         }
     }
@@ -539,6 +541,7 @@ struct F16Args {
   int splits;
   float* part;
   const float* colscale;  // optional: output column n multiplied by colscale[n]
+  const int* xexp;        // [Mp]: row m of xh holds X row m times 2^-xexp[m]
 };
 
 __device__ __forceinline__ void dma16_nt(const void* src, uint8_t* lds_wave_base) {
@@ -634,7 +637,7 @@ __global__ void __launch_bounds__(F16Geom<NW>::kThreads, 1) f16_gemm_v2_kernel(c
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int m = m0 + wm * 64 + 16 * i + 4 * lq + r;
-        if (m < a.M) out[(size_t)m * a.N + n] = acc[i][j][r] * cs + bv;
+        if (m < a.M) out[(size_t)m * a.N + n] = ldexpf(acc[i][j][r], a.xexp[m]) * cs + bv;
       }
   }
 }
@@ -696,13 +699,8 @@ hipError_t launch_f16_gemm_v2(float* y, const uint8_t* w, const float* x, const 
   using G = F16Geom<kF16NW>;
   hipError_t e = launch_x_f16_plain(x, batch, m, ws, s);
   if (e != hipSuccess) return e;
-  static bool attr_set = false;
-  if (!attr_set) {
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(f16_gemm_v2_kernel<kF16NW>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, G::kLds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  e = set_lds_limit(reinterpret_cast<const void*>(f16_gemm_v2_kernel<kF16NW>), G::kLds);
+  if (e != hipSuccess) return e;
   F16Args a;
   a.y = y;
   a.w = w;
@@ -719,6 +717,7 @@ hipError_t launch_f16_gemm_v2(float* y, const uint8_t* w, const float* x, const 
   a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) +
                                     round256(gemm_workspace_bytes(batch, m)));
   a.colscale = colscale;
+  a.xexp = gemm_x_exponents(ws, batch, m);
   hipLaunchKernelGGL(f16_gemm_v2_kernel<kF16NW>, dim3(tiles, a.splits), dim3(G::kThreads), G::kLds,
                      s, a);
   e = hipGetLastError();
@@ -733,18 +732,15 @@ hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const
                                size_t n, size_t m, size_t batch, void* ws, int num_cus,
                                hipStream_t s) {
   hipError_t e;
-  static bool attr_set = false;
-  if (!attr_set) {
-    for (const void* k : {reinterpret_cast<const void*>(q4_0_gemm_v3_kernel<true>),
-                          reinterpret_cast<const void*>(q4_0_gemm_v3_kernel<false>)}) {
-      e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-      if (e != hipSuccess) return e;
-    }
-    attr_set = true;
+  for (const void* k : {reinterpret_cast<const void*>(q4_0_gemm_v3_kernel<true>),
+                        reinterpret_cast<const void*>(q4_0_gemm_v3_kernel<false>)}) {
+    e = set_lds_limit(k, kLdsBytes);
+    if (e != hipSuccess) return e;
   }
   const size_t wbytes = n * (m / kBlockElems) * kBlockBytes;
-  const bool fold = batch >= kFoldMinBatch ||
-                    (batch >= kFoldMinBatchSmallW && wbytes <= kFoldSmallWBytes);
+  const bool fold = !gemm_force_exact() &&
+                    (batch >= kFoldMinBatch ||
+                     (batch >= kFoldMinBatchSmallW && wbytes <= kFoldSmallWBytes));
   Args a;
   a.y = y;
   a.w = w;
@@ -763,11 +759,12 @@ hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const
   int* rowexp = reinterpret_cast<int*>(
       static_cast<uint8_t*>(ws) + gemm_v3_workspace_bytes(batch, n, m, num_cus) - round256(n * 4));
   a.rowexp = rowexp;
+  a.xexp = gemm_x_exponents(ws, batch, m);
   if (fold) {
     const size_t mp = (batch + BM - 1) / BM * BM;
-    const unsigned gx = (unsigned)((mp * (m / 8) + 255) / 256);
-    hipLaunchKernelGGL(q4_0_prepass_kernel, dim3(gx + (unsigned)((n + 3) / 4)), dim3(256), 0, s,
-                       static_cast<u32x4*>(ws), x, (int)batch, (int)mp, (int)m, gx, rowexp, w, (int)n);
+    hipLaunchKernelGGL(q4_0_prepass_kernel, dim3((unsigned)mp + (unsigned)((n + 3) / 4)),
+                       dim3(256), 0, s, static_cast<u32x4*>(ws), gemm_x_exponents(ws, batch, m), x,
+                       (int)batch, (int)mp, (int)m, rowexp, w, (int)n);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(q4_0_gemm_v3_kernel<true>, dim3(tiles, a.splits), dim3(kThreads), kLdsBytes,
                        s, a);

@@ -618,8 +618,6 @@ __global__ void __launch_bounds__(1024) q8_0_gemv_jobs_kernel(GemvLaunch L) {
   gemv_jobs_body<kFmtQ8_0, false>(L);
 }
 
-static bool g_lds_attr_set[3] = {false, false, false};
-
 hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
                                   const GemvJob& job0, int njobs, int total_steps, int num_cus,
                                   hipStream_t s) {
@@ -628,11 +626,9 @@ hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
   const void* kern = which == 2   ? reinterpret_cast<const void*>(q8_0_gemv_jobs_kernel)
                      : which == 1 ? reinterpret_cast<const void*>(q4_0_gemv_jobs_pro_kernel)
                                   : reinterpret_cast<const void*>(q4_0_gemv_jobs_kernel);
-  if (!g_lds_attr_set[which]) {
-    hipError_t e =
-        hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+  {
+    hipError_t e = set_lds_limit(kern, (int)kMaxLds);
     if (e != hipSuccess) return e;
-    g_lds_attr_set[which] = true;
   }
   // As many work-groups as can be resident at once (registers and LDS).
   int per_cu = 0;

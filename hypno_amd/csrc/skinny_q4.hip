@@ -24,7 +24,9 @@
 //        adds (acc_hi + acc_lo) / s to y_t: an fp32-accurate result, as the
 //        GEMV path gives.  (Per-stage scales keep the pre-pass one pass over
 //        X with a work-group per stage.)
-//      - 16 < M <= 64: one fp16 row per token (the prefill GEMM's rounding).
+//      - 16 < M <= 64: one fp16 row per token (the prefill GEMM's rounding),
+//        scaled by a power of two per token (x_row_to_f16) that the epilogue
+//        undoes.
 //
 // Requirements (q4_0_skinny_ok): K % 256 == 0, w 16-byte aligned (row
 // segments of a stage are then 16-byte aligned), W and X under 4 GB, w
@@ -147,6 +149,7 @@ struct SkinnyArgs {
   const uint8_t* w;
   const uint8_t* xa;
   const float* inv_s;
+  const int* xexp;    // without SPLIT: token t's row holds x_t times 2^-xexp[t]
   const float* bias;
   int M, N, K;
   int split;          // hi/lo rows
@@ -329,7 +332,7 @@ __global__ void __launch_bounds__(64 * kSkWaves) q4_0_skinny_kernel(const Skinny
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int tkn = 16 * f + 4 * g + i;
-        if (nvalid && tkn < a.M) out[(size_t)tkn * a.N + n] = acc[f][i] + bv;
+        if (nvalid && tkn < a.M) out[(size_t)tkn * a.N + n] = ldexpf(acc[f][i], a.xexp[tkn]) + bv;
       }
   }
 }
@@ -387,14 +390,9 @@ int skinny_splits(size_t n, size_t m, size_t batch, int num_cus) {
 
 template <int MF, bool SPLIT>
 hipError_t launch_mf(const SkinnyArgs& a, dim3 grid, hipStream_t s) {
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(q4_0_skinny_kernel<MF, SPLIT>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       SkGeom<MF>::kLds);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
+  hipError_t e = set_lds_limit(reinterpret_cast<const void*>(q4_0_skinny_kernel<MF, SPLIT>),
+                               SkGeom<MF>::kLds);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((q4_0_skinny_kernel<MF, SPLIT>), grid, dim3(64 * kSkWaves), SkGeom<MF>::kLds,
                      s, a);
   return hipGetLastError();
@@ -414,10 +412,12 @@ bool q4_0_skinny_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t b
 
 static size_t round256(size_t v) { return (v + 255) / 256 * 256; }
 
+// Workspace: A rows, the split mode's 1/s table, the plain mode's per-token
+// exponents (64 ints), the K-split partial planes.
 size_t skinny_workspace_bytes(size_t batch, size_t n, size_t m, int num_cus) {
   const SkinnyShape sh = skinny_shape(batch);
   const int sp = skinny_splits(n, m, batch, num_cus);
-  size_t b = round256((size_t)sh.rows * m * 2) + round256(m / kSkStageK * 16 * 4);
+  size_t b = round256((size_t)sh.rows * m * 2) + round256(m / kSkStageK * 16 * 4) + 256;
   if (sp > 1) b += (size_t)sp * batch * n * 4;
   return b;
 }
@@ -428,13 +428,18 @@ hipError_t launch_q4_0_skinny(float* y, const uint8_t* w, const float* x, const 
   const SkinnyShape sh = skinny_shape(batch);
   uint8_t* xa = static_cast<uint8_t*>(ws);
   float* inv_s = reinterpret_cast<float*>(xa + round256((size_t)sh.rows * m * 2));
-  float* part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(inv_s) +
-                                         round256(m / kSkStageK * 16 * 4));
-  const int hi_rows = sh.split ? sh.mh : sh.rows;
-  const int stages = (int)(m / kSkStageK);
-  hipLaunchKernelGGL(x_skinny_kernel, dim3((unsigned)((stages + 7) / 8), (unsigned)hi_rows),
-                     dim3(256), 0, s, xa, inv_s, x, (int)batch, (int)m, sh.mh, sh.split);
-  hipError_t e = hipGetLastError();
+  int* xexp = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(inv_s) +
+                                     round256(m / kSkStageK * 16 * 4));
+  float* part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(xexp) + 256);
+  hipError_t e;
+  if (sh.split) {
+    const int stages = (int)(m / kSkStageK);
+    hipLaunchKernelGGL(x_skinny_kernel, dim3((unsigned)((stages + 7) / 8), (unsigned)sh.mh),
+                       dim3(256), 0, s, xa, inv_s, x, (int)batch, (int)m, sh.mh, sh.split);
+    e = hipGetLastError();
+  } else {
+    e = launch_x_rows_f16(x, batch, (size_t)sh.rows, m, xa, xexp, true, s);
+  }
   if (e != hipSuccess) return e;
   const int sp = skinny_splits(n, m, batch, num_cus);
   SkinnyArgs a;
@@ -443,6 +448,7 @@ hipError_t launch_q4_0_skinny(float* y, const uint8_t* w, const float* x, const 
   a.w = w;
   a.xa = xa;
   a.inv_s = inv_s;
+  a.xexp = xexp;
   a.bias = bias;
   a.M = (int)batch;
   a.N = (int)n;

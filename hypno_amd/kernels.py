@@ -32,8 +32,21 @@ __all__ = [
     "matmul_vec_f16", "matmul_vec_auto", "batch_matmul", "quantize_f32_to_q4_0",
     "dequantize_q4_0", "register_weight", "unregister_weight", "device_count", "GemvPlan",
     "rms_norm", "rms_norm_in_place", "silu_mul", "matmul_q8_0", "quantize_f32_to_q8_0",
-    "dequantize_q8_0", "matmul_q4_0_col", "matmul_vec_col",
+    "dequantize_q8_0", "matmul_q4_0_col", "matmul_vec_col", "set_gemm_numerics",
+    "GEMM_AUTO", "GEMM_EXACT",
 ]
+
+GEMM_AUTO, GEMM_EXACT = 0, 1  # HYPNO_HIP_GEMM_AUTO / _EXACT
+
+
+def set_gemm_numerics(mode: int) -> int:
+    """Q4_0 prefill GEMM arithmetic: GEMM_AUTO (fastest per shape) or
+    GEMM_EXACT (integer nibbles, each block's scale applied in fp32).
+    Process-wide; returns the previous mode."""
+    prev = int(load().hypno_hip_set_gemm_numerics(int(mode)))
+    if prev < 0:
+        check(-prev, "set_gemm_numerics")
+    return prev
 
 
 class DType(enum.IntEnum):

@@ -14,15 +14,39 @@
  *     (kernels.rs:362-400).
  *   - A weight buffer shorter than the tensor is not an error: a block whose
  *     18 bytes lie past w_len contributes nothing (kernels.rs:275-277, :374).
- *   - y is fully overwritten; bias may be NULL (kernels.rs:356).
- *   - Results: fp32 accumulation for M = 1..15 tokens; for M >= 16 the Q4_0
- *     and FP16 paths round activations to fp16 and run on MFMA (the scale of
- *     each 32-block is applied to the MFMA partial in fp32).
+ *   - y is fully overwritten; bias may be NULL (kernels.rs:356).  y may not
+ *     share memory with any input (EINVAL; Rust's &mut y rules it out too).
+ *   - Arithmetic by path (M = tokens):
+ *       Q4_0, M = 1, m % 256 == 0 (the streaming decode GEMV): each block of
+ *         32 activations becomes exact integers of 19 significant bits
+ *         relative to the block's largest |x| (rounding <= 2^-18 of that
+ *         value), products with the nibbles are exact in int32, each block's
+ *         sum is scaled by d in fp32 and blocks accumulate in fp32.  Other
+ *         shapes: fp32 FMAs.  Bar: max|y - r| / max|r| <= 1e-4.
+ *       Q4_0, M = 2..16: fp16 hi/lo activation pairs per 256-column stage
+ *         (to ~2^-22), exact nibble products on MFMA, fp32 block scale; the
+ *         same 1e-4 bar per token.
+ *       Q4_0, M = 17..64, and M >= 65 (prefill GEMM): activations rounded to
+ *         fp16 after a power-of-two scale per token (undone exactly on the
+ *         output), fp32 accumulation on MFMA.  Weights: exact nibbles with
+ *         each block's d applied to its partial in fp32, except from 256
+ *         tokens (from 128 when W is at most 64 MB), where each weight goes
+ *         to the MFMA as fp16 (nibble - 8) * d / 2^E_n (one rounding,
+ *         relative 2^-11; 2^E_n just above row n's largest |d|).  Bar:
+ *         ||Y - R||_2 / ||R||_2 <= 2e-3.
+ *       FP16: M < 16 fp32 FMAs; M >= 16 as the Q4_0 GEMM with fp16 weights.
+ *       Q8_0: M < 16 token by token, activations as three exact int8 digit
+ *         planes per block (to 2^-23); M >= 16 weights expanded once to fp16
+ *         (row-normalised, relative 2^-11) and the FP16 GEMM.
  *   - Every function returns a status (HYPNO_HIP_OK on success) and never
  *     aborts the process.  hypno_hip_last_error() describes the last failure
  *     on the calling thread.
  *   - All functions are thread-safe.  Device-pointer ("_dev") entry points are
- *     asynchronous on the given stream (NULL = the default stream).
+ *     asynchronous on the given stream (NULL = the default stream).  Calls
+ *     from several threads on one stream are serialised for the span of
+ *     their launches (each stream has its own workspace); a call needing a
+ *     larger workspace than its stream holds synchronises that stream first,
+ *     so make the first call of each size before capturing a HIP graph.
  */
 #ifndef HYPNO_HIP_H
 #define HYPNO_HIP_H
@@ -187,8 +211,8 @@ int hypno_hip_dequantize_q4_0_dev(float* out, const uint8_t* q, size_t q_len, vo
  * them as one launch removes the per-launch cost (about 1.6 us per kernel in
  * a HIP graph on MI355X) and keeps HBM busy across matrix boundaries.
  * Each descriptor has the semantics of hypno_hip_matmul_q4_0_dev with
- * batch = 1.  Jobs must be independent: no job's y may overlap another job's
- * x, w or y.  Descriptors that the streaming kernel cannot take (m % 256 != 0,
+ * batch = 1.  Jobs must be independent: no job's y may overlap any job's y,
+ * x, w, bias or prologue aux (plan_create checks this: EINVAL).  Descriptors that the streaming kernel cannot take (m % 256 != 0,
  * unaligned pointers, short buffers) are run by the generic kernel in the
  * same plan.  A plan stores the pointers: update the x buffers in place and
  * run it again (it is safe to capture plan_run in a HIP graph).
@@ -255,6 +279,17 @@ int hypno_hip_rms_norm_dev(float* out, const float* x, const float* weight, size
  * silu(gate[i]) * up[i] over n floats; out may equal gate.  Device pointers. */
 int hypno_hip_silu_mul_dev(float* out, const float* gate, const float* up, size_t n,
                            void* stream);
+
+/* How the Q4_0 prefill GEMM applies the block scales (no counterpart in
+ * hypno, whose CPU kernel has one arithmetic).  AUTO (the default) picks per
+ * call as described at the top of this file; EXACT always feeds the MFMAs
+ * the integer nibbles and applies each block's d to its partial in fp32 (the
+ * arithmetic the reference's block-at-a-time dequantisation implies), at
+ * some speed from 128-256 tokens up.  Process-wide; returns the previous
+ * mode, or -EINVAL for an unknown one. */
+#define HYPNO_HIP_GEMM_AUTO 0u
+#define HYPNO_HIP_GEMM_EXACT 1u
+int hypno_hip_set_gemm_numerics(uint32_t mode);
 
 /* Block until all work this library queued on `stream` is done. */
 int hypno_hip_stream_synchronize(void* stream);

@@ -88,3 +88,50 @@ def test_product_never_imports_oracle():
             if f.endswith((".py", ".hip", ".cpp", ".hpp", ".h")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert "oracle" not in text.lower(), f"{f} mentions the oracle"
+
+
+def test_overlap_rejected_without_device(lib):
+    """y may not share memory with an input (the reference's &mut y beside
+    shared borrows); the check runs before any device call, so fake device
+    addresses suffice here."""
+    base = 1 << 40
+    P = ctypes.c_void_p
+    # y = x (batch 1): EINVAL
+    assert lib.hypno_hip_matmul_q4_0_dev(P(base), P(base + 4096), 18 * 8, P(base), None, 4, 64, 1,
+                                         None) == 22
+    assert b"overlap" in lib.hypno_hip_last_error()
+    # y straddles the end of w
+    assert lib.hypno_hip_matmul_f16_dev(P(base + 1000), P(base), 1024, P(base + 8192), None, 4,
+                                        128, 1, None) == 22
+    # bias inside y
+    assert lib.hypno_hip_matmul_q8_0_dev(P(base), P(base + 4096), 34 * 8, P(base + 8192),
+                                         P(base + 4), 4, 64, 1, None) == 22
+    assert lib.hypno_hip_matmul_q4_0_col_dev(P(base), P(base + 4096), 18 * 8, P(base + 8),
+                                             None, 4, 64, 1, None) == 22
+
+
+def test_plan_overlap_rejected_without_device(lib):
+    from hypno_amd._lib import GemvDesc, GemvPrologue
+    base = 1 << 40
+    plan = ctypes.c_void_p()
+
+    def descs(*ds):
+        arr = (GemvDesc * len(ds))()
+        for i, (y, w, x, n, m) in enumerate(ds):
+            arr[i].y, arr[i].w_q, arr[i].w_len = base + y, base + w, n * m // 32 * 18
+            arr[i].x, arr[i].bias, arr[i].n, arr[i].m = base + x, None, n, m
+        return arr
+
+    # two jobs writing overlapping y
+    d = descs((0, 1 << 20, 2 << 20, 256, 256), (512, 3 << 20, 2 << 20, 256, 256))
+    assert lib.hypno_hip_q4_0_gemv_plan_create(d, 2, ctypes.byref(plan)) == 22
+    assert b"overlap" in lib.hypno_hip_last_error()
+    # job 1 reads job 0's output as its x
+    d = descs((0, 1 << 20, 2 << 20, 256, 256), (4096, 3 << 20, 0, 256, 256))
+    assert lib.hypno_hip_q4_0_gemv_plan_create(d, 2, ctypes.byref(plan)) == 22
+    # a prologue operand inside another job's y
+    d = descs((0, 1 << 20, 2 << 20, 256, 256), (4096, 3 << 20, 2 << 20, 256, 256))
+    pros = (GemvPrologue * 2)()
+    pros[1].kind, pros[1].aux, pros[1].eps = 1, base + 64, 1e-5
+    assert lib.hypno_hip_q4_0_gemv_plan_create_ex(d, pros, 2, ctypes.byref(plan)) == 22
+    assert not plan.value
