@@ -30,6 +30,7 @@ SIGNATURES = {
     "hypno_hip_weight_register": (_i, [_vp, _sz]),
     "hypno_hip_weight_unregister": (_i, [_vp]),
     "hypno_hip_matmul_q4_0_dev": (_i, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "hypno_hip_matmul_q4_0_dev_noalloc": (_i, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _vp]),
     "hypno_hip_matmul_f16_dev": (_i, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _vp]),
     "hypno_hip_matmul_q8_0_dev": (_i, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _vp]),
     "hypno_hip_quantize_q8_0_dev": (_i, [_vp, _vp, _sz, _vp]),

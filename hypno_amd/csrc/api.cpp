@@ -175,8 +175,18 @@ bool mul_overflows(size_t a, size_t b) { return a != 0 && b > SIZE_MAX / a; }
 
 // --- dispatch on device pointers (caller holds no lock) ---------------------
 
+// A fixed device buffer standing in for the per-stream workspace (the
+// no-allocation entry point): `ptr` holds `bytes`; `cus` is the device's CU
+// count.
+struct FixedScratch {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  int cus = 256;
+};
+
 int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const float* bias,
-             size_t n, size_t m, size_t batch, hipStream_t s) {
+             size_t n, size_t m, size_t batch, hipStream_t s,
+             const FixedScratch* fixed = nullptr) {
   if (n == 0 || batch == 0) return HYPNO_HIP_OK;
   if (!y || !x) return fail(HYPNO_HIP_EINVAL, "y and x must not be NULL");
   if (!w && w_len) return fail(HYPNO_HIP_EINVAL, "w_q is NULL but w_len > 0");
@@ -186,17 +196,30 @@ int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
   if (st) return st;
   int cus = 256;
   DeviceState* ds = nullptr;
-  {
+  if (fixed) {
+    cus = fixed->cus;
+  } else {
     std::lock_guard<std::mutex> g(g_mu);
     st = device_state(&ds);
     if (st) return st;
     cus = ds->cus;
   }
+  // The call's scratch memory: the stream's workspace (locked for the span
+  // of the launches), or the fixed buffer when it is large enough.
+  auto scratch_for = [&](size_t bytes, WsLock& ws, const char* what) -> int {
+    if (!fixed) return lock_workspace(ds, s, bytes, ws, what);
+    if (bytes > fixed->bytes)
+      return fail(HYPNO_HIP_EINVAL,
+                  "%s: this call needs %zu bytes of scratch; the fixed scratch array holds %zu",
+                  what, bytes, fixed->bytes);
+    ws.p = fixed->ptr;
+    return HYPNO_HIP_OK;
+  };
   hipError_t e;
   if (batch >= 2 && batch <= kSkinnyMaxBatch && q4_0_skinny_ok(w, w_len, n, m, batch, cus) &&
       aligned16(x)) {
     WsLock ws;
-    st = lock_workspace(ds, s, skinny_workspace_bytes(batch, n, m, cus), ws, "skinny workspace");
+    st = scratch_for(skinny_workspace_bytes(batch, n, m, cus), ws, "skinny workspace");
     if (st) return st;
     e = launch_q4_0_skinny(y, w, x, bias, n, m, batch, ws.p, cus, s);
     if (e != hipSuccess) return hip_fail(e, "q4_0 skinny launch");
@@ -205,9 +228,9 @@ int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
   const bool v3 = batch >= kGemmMinBatch && q4_0_gemm_v3_ok(w, w_len, n, m, batch);
   if (v3 || (batch >= kGemmMinBatch && q4_0_gemm_ok(w, w_len, n, m, batch))) {
     WsLock ws;
-    st = lock_workspace(
-        ds, s, v3 ? gemm_v3_workspace_bytes(batch, n, m, cus) : gemm_workspace_bytes(batch, m),
-        ws, "GEMM workspace");
+    st = scratch_for(
+        v3 ? gemm_v3_workspace_bytes(batch, n, m, cus) : gemm_workspace_bytes(batch, m), ws,
+        "GEMM workspace");
     if (st) return st;
     e = v3 ? launch_q4_0_gemm_v3(y, w, x, bias, n, m, batch, ws.p, cus, s)
            : launch_q4_0_gemm(y, w, x, bias, n, m, batch, ws.p, cus, s);
@@ -458,6 +481,48 @@ hipError_t set_lds_limit(const void* kernel, int bytes) {
 
 }  // namespace hypno
 
+namespace {
+
+// Scratch memory of the no-allocation entry point: one fixed array per GPU
+// (every device the library runs on holds its own copy until the process
+// ends).  Host code never uses the array's name as an address: the device
+// address comes from hipGetSymbolAddress, once per device with that device
+// current, and is kept in g_scratch.
+constexpr size_t kScratchBytes = HYPNO_HIP_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+FixedScratch g_scratch[kMaxDevices];
+
+int scratch_of_current_device(FixedScratch* out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(HYPNO_HIP_EINVAL, "device %d: the no-allocation path supports %d devices", dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  FixedScratch& sc = g_scratch[dev];
+  if (!sc.ptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(HYPNO_HIP_EDEVICE, "hipGetSymbolAddress(scratch) gave NULL");
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    sc.cus = cus;
+    sc.bytes = kScratchBytes;
+    sc.ptr = p;
+  }
+  *out = sc;
+  return HYPNO_HIP_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int hypno_hip_abi_version(void) { return HYPNO_HIP_ABI_VERSION; }
@@ -572,6 +637,16 @@ int hypno_hip_matmul_q4_0_dev(float* y, const uint8_t* w_q, size_t w_len, const 
                               const float* bias, size_t n, size_t m, size_t batch,
                               void* stream) {
   return q4_0_dev(y, w_q, w_len, x, bias, n, m, batch, (hipStream_t)stream);
+}
+
+int hypno_hip_matmul_q4_0_dev_noalloc(float* y, const uint8_t* w_q, size_t w_len,
+                                      const float* x, const float* bias, size_t n, size_t m,
+                                      size_t batch, void* stream) {
+  if (n == 0 || batch == 0) return HYPNO_HIP_OK;
+  FixedScratch sc;
+  int st = scratch_of_current_device(&sc);
+  if (st) return st;
+  return q4_0_dev(y, w_q, w_len, x, bias, n, m, batch, (hipStream_t)stream, &sc);
 }
 
 int hypno_hip_matmul_f16_dev(float* y, const uint8_t* w, size_t w_len, const float* x,

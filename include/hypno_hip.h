@@ -169,6 +169,22 @@ int hypno_hip_matmul_q4_0_dev(float* y, const uint8_t* w_q, size_t w_len, const 
                               const float* bias, size_t n, size_t m, size_t batch,
                               void* stream);
 
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments, semantics and kernels as
+ * hypno_hip_matmul_q4_0_dev, but the scratch memory those kernels use (fp16
+ * activations, per-token exponents, split-K partial planes) is one fixed
+ * array of HYPNO_HIP_NOALLOC_SCRATCH_BYTES per GPU, in the library's device
+ * image, instead of the per-stream workspace: the call allocates nothing.
+ * A call that would need more scratch (e.g. 2048 tokens at m = 16384) is
+ * EINVAL before anything is launched.  Every call on one GPU shares that
+ * array and nothing in it carries over between calls: calls that overlap on
+ * one GPU (other streams, other threads) race, so serialise them. */
+#define HYPNO_HIP_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int hypno_hip_matmul_q4_0_dev_noalloc(float* y, const uint8_t* w_q, size_t w_len,
+                                      const float* x, const float* bias, size_t n, size_t m,
+                                      size_t batch, void* stream);
+
 /* Column-major Q4_0 on device pointers (semantics of
  * hypno_hip_matmul_q4_0_col; batch > 1: token by token, turbo.rs:322-326). */
 int hypno_hip_matmul_q4_0_col_dev(float* y, const uint8_t* w_q, size_t w_len, const float* x,
