@@ -616,6 +616,71 @@ def lm_head(torch, lib):
                         "of 512/1024), M in {1,128}, Q4_0 and FP16 weights", "results": out}
 
 
+def next_token(torch, lib):
+    """The step after the lm_head on its N = 128256 logits (run.rs:203-251):
+    greedy argmax and sample_token at typical settings, GPU us per call (graph
+    replay), each result checked against an independent host evaluation of
+    the same logits (argmax; the temperature-0 sampling arithmetic in numpy
+    float32)."""
+    import numpy as np
+
+    import hypno_amd as hk
+    n = 128256
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    logits = torch.randn(n, generator=gen, device="cuda").mul_(3.0)
+    lh = logits.cpu().numpy()
+    tok = torch.empty(1, dtype=torch.int32, device="cuda")
+    state = torch.tensor([88172645463325252], dtype=torch.int64, device="cuda")
+    lp, tp, sp = (ctypes.c_void_p(t.data_ptr()) for t in (logits, tok, state))
+    out = {}
+    cases = {"argmax": None, "T0.7_topk40_topp0.9": (0.7, 0.9, 40),
+             "T1.0_topp0.9_no_topk": (1.0, 0.9, 0), "T1.0_no_filters": (1.0, 1.0, 0)}
+    for name, cfg in cases.items():
+        def issue(st, i, cfg=cfg):
+            rc = (lib.lib.hypno_hip_argmax_dev(tp, lp, n, st) if cfg is None else
+                  lib.lib.hypno_hip_sample_token_dev(tp, sp, lp, n, cfg[0], cfg[1], cfg[2], st))
+            if rc:
+                lib.check(rc, "next token")
+        us = time_calls_graph(torch, issue, reps=10)
+        out[name] = {"us": round(us, 2)}
+    # checks: the argmax, and a temperature-0 draw over positive logits,
+    # against numpy
+    issue_st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = lib.lib.hypno_hip_argmax_dev(tp, lp, n, issue_st)
+    torch.cuda.synchronize()
+    ok = rc == 0 and int(tok.item()) == int(n - 1 - np.argmax(lh[::-1]))
+    p = np.abs(lh)
+    pg = torch.from_numpy(p).cuda()
+    st0 = 987654321
+    state.fill_(st0)
+    hk.sample_token(pg, 0.0, 1.0, 0, state)
+    torch.cuda.synchronize()
+    f = np.float32
+    s = f(-0.0)
+    for v in p:
+        s = f(s + v)
+    x = st0
+    M = (1 << 64) - 1
+    x ^= (x << 13) & M
+    x ^= x >> 7
+    x ^= (x << 17) & M
+    r = f((x >> 40) / 2.0**24)
+    want, cum = None, f(0)
+    for i, v in enumerate(p):
+        cum = f(cum + f(v / s))
+        if r < cum:
+            want = i
+            break
+    got = hk.sample_token(pg, 0.0, 1.0, 0, torch.tensor([st0], dtype=torch.int64,
+                                                        device="cuda"))
+    torch.cuda.synchronize()
+    ok = ok and want is not None and int(got.item()) == want
+    return {"workload": "next token from K=4096 x N=128256 lm_head logits: greedy argmax and "
+                        "sample_token (one work-group; sequential fp32 walks as the "
+                        "reference); GPU us per call", "results": out,
+            "check": {"checked": bool(ok), "bar": "token equal to a host evaluation"}}
+
+
 def q8_0_decode(torch, lib):
     """Q8_0 weights (34-byte blocks, 1.0625 B per weight) at the Mistral-7B
     projection shapes, M = 1: GPU time per hypno_hip_matmul_q8_0_dev call over
@@ -1076,7 +1141,8 @@ def main():
         sec = {}
         for key, fn in (("c0_single_gemv", single_gemv), ("c1_tinyllama_stream", None),
                         ("c2_prefill_gemm", prefill_gemm), ("c3_m_sweep", mistral_m_sweep),
-                        ("c4_lm_head", lm_head), ("model_load", model_load),
+                        ("c4_lm_head", lm_head), ("c4_next_token", next_token),
+                        ("model_load", model_load),
                         ("q8_0_decode", q8_0_decode), ("col_major", col_major)):
             print(f"[bench] secondary: {key}", file=sys.stderr, flush=True)
             if fn is None:

@@ -10,10 +10,12 @@ from .kernels import (  # noqa: F401
     DType,
     GemvPlan,
     HypnoHipError,
+    argmax,
     batch_matmul,
     dequantize_q4_0,
     dequantize_q8_0,
     device_count,
+    embed_tokens,
     matmul_f16,
     matmul_q4_0,
     matmul_q4_0_col,
@@ -22,11 +24,14 @@ from .kernels import (  # noqa: F401
     matmul_vec_col,
     matmul_vec_f16,
     matmul_vec_q4_0,
+    q4_0_extract_row,
+    q8_0_extract_row,
     quantize_f32_to_q4_0,
     quantize_f32_to_q8_0,
     register_weight,
     rms_norm,
     rms_norm_in_place,
+    sample_token,
     set_gemm_numerics,
     silu_mul,
     unregister_weight,

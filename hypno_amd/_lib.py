@@ -46,6 +46,12 @@ SIGNATURES = {
     "hypno_hip_silu_mul_dev": (_i, [_vp, _vp, _vp, _sz, _vp]),
     "hypno_hip_stream_synchronize": (_i, [_vp]),
     "hypno_hip_set_gemm_numerics": (_i, [_u32]),
+    "hypno_hip_q4_0_extract_row_dev": (_i, [_vp, _vp, _sz, _sz, _sz, _vp]),
+    "hypno_hip_q8_0_extract_row_dev": (_i, [_vp, _vp, _sz, _sz, _sz, _vp]),
+    "hypno_hip_embed_tokens_dev": (_i, [_vp, _vp, _sz, _u32, _vp, _sz, _sz, _vp]),
+    "hypno_hip_argmax_dev": (_i, [_vp, _vp, _sz, _vp]),
+    "hypno_hip_sample_token_dev": (_i, [_vp, _vp, _vp, _sz, ctypes.c_float, ctypes.c_float,
+                                        _sz, _vp]),
     "hypno_hip_model_open": (_i, [ctypes.c_char_p, _u32, ctypes.POINTER(_vp)]),
     "hypno_hip_model_close": (_i, [_vp]),
     "hypno_hip_model_header": (_i, [_vp, ctypes.POINTER(_u32), ctypes.POINTER(_u32),

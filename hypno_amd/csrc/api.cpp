@@ -960,6 +960,81 @@ int hypno_hip_silu_mul_dev(float* out, const float* gate, const float* up, size_
   return HYPNO_HIP_OK;
 }
 
+int hypno_hip_q4_0_extract_row_dev(float* out, const uint8_t* q, size_t q_len, size_t row_idx,
+                                   size_t row_width, void* stream) {
+  if (row_width == 0) return HYPNO_HIP_OK;
+  if (!out) return fail(HYPNO_HIP_EINVAL, "extract_row: NULL output");
+  const size_t bpr = row_width / kBlockElems;
+  if (bpr && (mul_overflows(row_idx + 1, bpr * kBlockBytes) || !q ||
+              (row_idx + 1) * bpr * kBlockBytes > q_len))
+    return fail(HYPNO_HIP_EINVAL, "extract_row: row %zu is past the end of the %zu-byte matrix",
+                row_idx, q_len);
+  hipError_t e = launch_embed_rows(out, q, q_len, (int)HYPNO_DTYPE_Q4_0, nullptr, row_idx, 1,
+                                   row_width, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "extract_row launch");
+  return HYPNO_HIP_OK;
+}
+
+int hypno_hip_q8_0_extract_row_dev(float* out, const uint8_t* q, size_t q_len, size_t row_idx,
+                                   size_t row_width, void* stream) {
+  if (row_width == 0) return HYPNO_HIP_OK;
+  if (!out) return fail(HYPNO_HIP_EINVAL, "extract_row: NULL output");
+  const size_t bpr = row_width / kBlockElems;
+  if (bpr && (mul_overflows(row_idx + 1, bpr * kQ8BlockBytes) || !q ||
+              (row_idx + 1) * bpr * kQ8BlockBytes > q_len))
+    return fail(HYPNO_HIP_EINVAL, "extract_row: row %zu is past the end of the %zu-byte matrix",
+                row_idx, q_len);
+  hipError_t e = launch_embed_rows(out, q, q_len, (int)HYPNO_DTYPE_Q8_0, nullptr, row_idx, 1,
+                                   row_width, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "extract_row launch");
+  return HYPNO_HIP_OK;
+}
+
+int hypno_hip_embed_tokens_dev(float* out, const uint8_t* table, size_t table_len,
+                               uint32_t dtype, const uint32_t* ids, size_t count, size_t hd,
+                               void* stream) {
+  if (dtype > HYPNO_DTYPE_Q4_0) return fail(HYPNO_HIP_EINVAL, "embed: unknown dtype %u", dtype);
+  if (count == 0 || hd == 0) return HYPNO_HIP_OK;
+  if (!out || !ids || (!table && table_len)) return fail(HYPNO_HIP_EINVAL, "embed: NULL pointer");
+  if (count > 0x7FFFFFFF || mul_overflows(count, hd) || hd > ((size_t)1 << 40))
+    return fail(HYPNO_HIP_EINVAL, "embed: shape out of range");
+  hipError_t e = launch_embed_rows(out, table, table_len, (int)dtype, ids, 0, count, hd,
+                                   (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "embed launch");
+  return HYPNO_HIP_OK;
+}
+
+int hypno_hip_argmax_dev(uint32_t* index, const float* logits, size_t n, void* stream) {
+  if (!index || (!logits && n)) return fail(HYPNO_HIP_EINVAL, "argmax: NULL pointer");
+  if (n > 0x7FFFFFFF) return fail(HYPNO_HIP_EINVAL, "argmax: n out of range");
+  hipError_t e = launch_sample_token(index, nullptr, logits, n, 0.0f, 1.0f, 0, nullptr,
+                                     (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "argmax launch");
+  return HYPNO_HIP_OK;
+}
+
+int hypno_hip_sample_token_dev(uint32_t* token, uint64_t* rng_state, const float* logits,
+                               size_t n, float temperature, float top_p, size_t top_k,
+                               void* stream) {
+  if (!token || !rng_state || (!logits && n))
+    return fail(HYPNO_HIP_EINVAL, "sample_token: NULL pointer");
+  if (n > 0x7FFFFFFF) return fail(HYPNO_HIP_EINVAL, "sample_token: n out of range");
+  hipStream_t s = (hipStream_t)stream;
+  DeviceState* ds = nullptr;
+  {
+    std::lock_guard<std::mutex> g(g_mu);
+    int st = device_state(&ds);
+    if (st) return st;
+  }
+  WsLock ws;
+  int st = lock_workspace(ds, s, sample_workspace_bytes(n), ws, "sampling workspace");
+  if (st) return st;
+  hipError_t e = launch_sample_token(token, rng_state, logits, n, temperature, top_p, top_k,
+                                     ws.p, s);
+  if (e != hipSuccess) return hip_fail(e, "sample_token launch");
+  return HYPNO_HIP_OK;
+}
+
 int hypno_hip_set_gemm_numerics(uint32_t mode) {
   if (mode != HYPNO_HIP_GEMM_AUTO && mode != HYPNO_HIP_GEMM_EXACT) {
     fail(HYPNO_HIP_EINVAL, "set_gemm_numerics: unknown mode %u", mode);

@@ -356,6 +356,19 @@ hipError_t launch_rms_norm(float* out, const float* x, const float* weight, size
 hipError_t launch_silu_mul(float* out, const float* gate, const float* up, size_t n,
                            hipStream_t s);
 
+// Embedding rows (sample.hip): out[t][0..hd) = row ids[t] (or the single
+// row id0 when ids is NULL) of an FP32 / FP16 / Q8_0 / Q4_0 table (dtype =
+// HYPNO_DTYPE_*); rows outside the table are NaN.
+hipError_t launch_embed_rows(float* out, const uint8_t* table, size_t table_len, int dtype,
+                             const uint32_t* ids, size_t id0, size_t count, size_t hd,
+                             hipStream_t s);
+// Next token from n logits (sample.hip): ws == NULL gives the greedy argmax,
+// otherwise sample_token with a workspace of sample_workspace_bytes(n).
+size_t sample_workspace_bytes(size_t n);
+hipError_t launch_sample_token(uint32_t* token, uint64_t* state, const float* logits, size_t n,
+                               float temperature, float top_p, size_t top_k, void* ws,
+                               hipStream_t s);
+
 // Status reporting shared by the C ABI sources (api.cpp): record `msg` as the
 // calling thread's last error and return `status`; hip_status maps a HIP error
 // to ENOMEM / EDEVICE the same way.

@@ -33,7 +33,8 @@ __all__ = [
     "dequantize_q4_0", "register_weight", "unregister_weight", "device_count", "GemvPlan",
     "rms_norm", "rms_norm_in_place", "silu_mul", "matmul_q8_0", "quantize_f32_to_q8_0",
     "dequantize_q8_0", "matmul_q4_0_col", "matmul_vec_col", "set_gemm_numerics",
-    "GEMM_AUTO", "GEMM_EXACT",
+    "GEMM_AUTO", "GEMM_EXACT", "q4_0_extract_row", "q8_0_extract_row", "embed_tokens",
+    "argmax", "sample_token",
 ]
 
 GEMM_AUTO, GEMM_EXACT = 0, 1  # HYPNO_HIP_GEMM_AUTO / _EXACT
@@ -405,3 +406,68 @@ def register_weight(w: np.ndarray) -> None:
 
 def unregister_weight(w: np.ndarray) -> None:
     check(load().hypno_hip_weight_unregister(_host_ptr(w, np.uint8, "w")), "weight_unregister")
+
+
+# --- the embedding gather and the next-token choice (device tensors) ---------------
+
+def _extract_row(fn, q, row_idx: int, row_width: int):
+    torch = _torch()
+    out = torch.empty(row_width, dtype=torch.float32, device=q.device)
+    check(fn(_dev_ptr(out, "f32", "out"), _dev_ptr(q, "u8", "q"), _nbytes(q), int(row_idx),
+             int(row_width), _stream(q.device)), "extract_row")
+    return out
+
+
+def q4_0_extract_row(q4_data, row_idx: int, row_width: int):
+    """quant.rs:139-153: row row_idx of a Q4_0 matrix, dequantised (new tensor)."""
+    return _extract_row(load().hypno_hip_q4_0_extract_row_dev, q4_data, row_idx, row_width)
+
+
+def q8_0_extract_row(q8_data, row_idx: int, row_width: int):
+    """quant.rs:158-175: the same for Q8_0."""
+    return _extract_row(load().hypno_hip_q8_0_extract_row_dev, q8_data, row_idx, row_width)
+
+
+def embed_tokens(table, dtype, token_ids, hd: int, out=None):
+    """Token embedding (transformer.rs:476-497, turbo.rs:38-66): rows
+    token_ids (int32/uint32 GPU tensor) of the table -> [len(ids), hd] fp32."""
+    torch = _torch()
+    ids = token_ids.to(torch.int32) if token_ids.dtype != torch.int32 else token_ids
+    if not ids.is_contiguous():
+        ids = ids.contiguous()
+    count = ids.numel()
+    if out is None:
+        out = torch.empty(count, hd, dtype=torch.float32, device=table.device)
+    check(load().hypno_hip_embed_tokens_dev(_dev_ptr(out, "f32", "out"),
+                                            _dev_ptr(table, "u8", "table"), _nbytes(table),
+                                            int(DType(dtype)), ctypes.c_void_p(ids.data_ptr()),
+                                            count, int(hd), _stream(table.device)),
+          "embed_tokens")
+    return out
+
+
+def argmax(logits):
+    """Index of the largest logit as Iterator::max_by picks it (run.rs:232-234),
+    as a one-element int32 GPU tensor."""
+    torch = _torch()
+    out = torch.empty(1, dtype=torch.int32, device=logits.device)
+    check(load().hypno_hip_argmax_dev(ctypes.c_void_p(out.data_ptr()),
+                                      _dev_ptr(logits, "f32", "logits"), logits.numel(),
+                                      _stream(logits.device)), "argmax")
+    return out
+
+
+def sample_token(logits, temperature: float, top_p: float, top_k: int, rng_state):
+    """sample_token (run.rs:203-251) on the GPU.  rng_state is a one-element
+    int64 GPU tensor holding the XorShift64 state (advanced in place); returns
+    a one-element int32 GPU tensor with the token."""
+    torch = _torch()
+    if rng_state.dtype != torch.int64 or rng_state.numel() != 1 or not rng_state.is_cuda:
+        raise ValueError("rng_state must be a one-element int64 GPU tensor")
+    out = torch.empty(1, dtype=torch.int32, device=logits.device)
+    check(load().hypno_hip_sample_token_dev(ctypes.c_void_p(out.data_ptr()),
+                                            ctypes.c_void_p(rng_state.data_ptr()),
+                                            _dev_ptr(logits, "f32", "logits"), logits.numel(),
+                                            float(temperature), float(top_p), int(top_k),
+                                            _stream(logits.device)), "sample_token")
+    return out

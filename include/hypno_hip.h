@@ -307,6 +307,53 @@ int hypno_hip_silu_mul_dev(float* out, const float* gate, const float* up, size_
 #define HYPNO_HIP_GEMM_EXACT 1u
 int hypno_hip_set_gemm_numerics(uint32_t mode);
 
+/* ---------------------------------------------------------------------------
+ * Steps either side of the GEMVs that read whole rows: the token embedding
+ * before the first layer, the next-token choice after the lm_head.  Device
+ * pointers, asynchronous on `stream`.
+ * ------------------------------------------------------------------------- */
+
+/* q4_0_extract_row(q, row_idx, row_width) (quant.rs:139-153): out[0..row_width)
+ * = row row_idx of a Q4_0 matrix of floor(row_width / 32) blocks per row,
+ * dequantised bit-exactly; elements past those blocks are 0.  A row whose
+ * blocks are not all inside q_len bytes (a panic in the reference) is
+ * EINVAL. */
+int hypno_hip_q4_0_extract_row_dev(float* out, const uint8_t* q, size_t q_len, size_t row_idx,
+                                   size_t row_width, void* stream);
+
+/* q8_0_extract_row (quant.rs:158-175): the same with 34-byte Q8_0 blocks. */
+int hypno_hip_q8_0_extract_row_dev(float* out, const uint8_t* q, size_t q_len, size_t row_idx,
+                                   size_t row_width, void* stream);
+
+/* The token embedding of a decode step or a prefill batch (transformer.rs:
+ * 476-497, turbo.rs:38-66): out[t][0..hd) = row ids[t] of the embedding table
+ * (dtype FP32, FP16, Q8_0 or Q4_0; quantised rows as the extract functions
+ * above), for `count` token ids already in device memory.  A row outside the
+ * table (a panic in the reference) is written as NaN. */
+int hypno_hip_embed_tokens_dev(float* out, const uint8_t* table, size_t table_len,
+                               uint32_t dtype, const uint32_t* ids, size_t count, size_t hd,
+                               void* stream);
+
+/* Greedy next token: *index = the position of the largest of n logits, as
+ * Iterator::max_by with partial_cmp picks it (run.rs:232-234): the last of
+ * equal maxima, NaNs passed over by the comparisons; n = 0 gives 0.
+ * `index` is device memory. */
+int hypno_hip_argmax_dev(uint32_t* index, const float* logits, size_t n, void* stream);
+
+/* sample_token(logits, temperature, top_p, top_k, rng) (run.rs:203-251) on
+ * the device: temperature scaling, top-k, top-p and the draw, with the
+ * reference's fp32 sums in its order, so the chosen token is the
+ * reference's.  *rng_state (device) is its XorShift64 state (run.rs:267-278:
+ * seed with max(seed, 1)); it advances by one step when a draw is made, as
+ * the reference's does.  exp is evaluated in fp64 and rounded to fp32 (the
+ * reference's libm expf agrees but for results within ~2^-29 of a rounding
+ * boundary).  Logits must not hold NaN (the reference's sort is then not
+ * total).  One work-group; the top-p walk and the draw are sequential fp32
+ * loops over the tokens left after top-k, like the reference's. */
+int hypno_hip_sample_token_dev(uint32_t* token, uint64_t* rng_state, const float* logits,
+                               size_t n, float temperature, float top_p, size_t top_k,
+                               void* stream);
+
 /* Block until all work this library queued on `stream` is done. */
 int hypno_hip_stream_synchronize(void* stream);
 

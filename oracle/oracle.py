@@ -76,6 +76,14 @@ def lib():
     L.orc_matmul_q4_0_absdot_f64.argtypes = [vp, vp, sz, vp, sz, sz]
     L.orc_f32_to_f16_f16c.argtypes = [vp, vp, sz]
     L.orc_f16_to_f32_f16c.argtypes = [vp, vp, sz]
+    L.orc_xorshift64_next.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+    L.orc_xorshift64_next.restype = ctypes.c_uint64
+    L.orc_xorshift64_next_f32.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+    L.orc_xorshift64_next_f32.restype = fp
+    L.orc_argmax.argtypes = [vp, sz]
+    L.orc_argmax.restype = ctypes.c_uint32
+    L.orc_sample_token.argtypes = [vp, sz, fp, fp, sz, ctypes.POINTER(ctypes.c_uint64)]
+    L.orc_sample_token.restype = ctypes.c_uint32
     L.orc_set_threads.argtypes = [ctypes.c_int]
     L.orc_have_avx2_fma.restype = ctypes.c_int
     L.orc_have_f16c.restype = ctypes.c_int
@@ -348,3 +356,38 @@ def matmul_q4_0_col_f64(w_q, x, bias, n, m) -> np.ndarray:
     y = np.empty(n, np.float64)
     lib().orc_matmul_q4_0_col_f64(_p(y), _p(w), w.size, _p(xx), _p(b), n, m)
     return y
+
+
+# --- next-token choice (run.rs:203-278) -------------------------------------------
+
+def xorshift64_seed(seed: int) -> int:
+    """XorShift64::new (run.rs:270): max(seed, 1)."""
+    return max(int(seed) & ((1 << 64) - 1), 1)
+
+
+def xorshift64_next(state: int):
+    """(value, new state) of XorShift64::next (run.rs:271-276)."""
+    st = ctypes.c_uint64(state)
+    v = lib().orc_xorshift64_next(ctypes.byref(st))
+    return int(v), int(st.value)
+
+
+def xorshift64_next_f32(state: int):
+    st = ctypes.c_uint64(state)
+    v = lib().orc_xorshift64_next_f32(ctypes.byref(st))
+    return float(v), int(st.value)
+
+
+def argmax(v) -> int:
+    """Iterator::max_by(partial_cmp) index (run.rs:232-234)."""
+    v = _c(v, np.float32).ravel()
+    return int(lib().orc_argmax(_p(v), v.size))
+
+
+def sample_token(logits, temperature: float, top_p: float, top_k: int, state: int):
+    """(token, new state) of sample_token (run.rs:203-251)."""
+    lg = _c(logits, np.float32).ravel()
+    st = ctypes.c_uint64(state)
+    tok = lib().orc_sample_token(_p(lg), lg.size, ctypes.c_float(temperature),
+                                 ctypes.c_float(top_p), int(top_k), ctypes.byref(st))
+    return int(tok), int(st.value)

@@ -43,6 +43,15 @@
  *                       n % 8 tail's divide form) and an fp64 brute force
  *   orc_silu_mul        reference KAT turbo.rs:979-990; silu(v) - silu(-v) = v
  *                       and fp64 closed form
+ *   orc_xorshift64_*    Marsaglia's published xorshift64 (13, 7, 17) sequence
+ *                       from seed 88172645463325252; max(seed, 1) seeding
+ *   orc_argmax          Iterator::max_by fold semantics: hand-built ties,
+ *                       signed zeros and NaN positions
+ *   orc_sample_token    hand-computed draws whose r lies well inside one
+ *                       interval (exact decimal boundaries), top-k = 1 and
+ *                       a tiny top-p reduce to the argmax, uniform logits
+ *                       reduce to floor(r n), the sum <= 0 and never-crossed
+ *                       top-p paths, and a float32 restatement in numpy
  *
  * Build: oracle/Makefile (gcc, -ffp-contract=off, no fast-math; the AVX2
  * kernels use target attributes so the library runs on any x86-64 host and
@@ -703,4 +712,115 @@ void orc_matmul_q4_0_col_f64(double* y, const uint8_t* w, size_t w_len, const fl
             }
         }
     }
+}
+
+
+/* ------------------------------------------------------------------------ */
+/* Next-token choice after the lm_head (run.rs:203-278; serve.rs:279-312 is  */
+/* the same code).                                                           */
+/* ------------------------------------------------------------------------ */
+
+/* XorShift64::next (run.rs:271-276): x ^= x << 13; x ^= x >> 7; x ^= x << 17.
+ * The state is seeded with max(seed, 1) (run.rs:270). */
+uint64_t orc_xorshift64_next(uint64_t* state) {
+    uint64_t x = *state;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *state = x;
+    return x;
+}
+
+/* XorShift64::next_f32 (run.rs:277): the top 24 bits over 2^24 (exact). */
+float orc_xorshift64_next_f32(uint64_t* state) {
+    return (float)(orc_xorshift64_next(state) >> 40) / 16777216.0f;
+}
+
+/* Iterator::max_by(|a, b| a.partial_cmp(b).unwrap_or(Equal)) over v[0..n),
+ * returning the index (run.rs:232-234, :248-250): the fold keeps the current
+ * element only when it compares Greater, so equal maxima resolve to the last
+ * and a NaN (Equal to everything) takes over and hands over to the next.
+ * Empty input: 0 (unwrap_or(0)). */
+uint32_t orc_argmax(const float* v, size_t n) {
+    size_t cur = 0;
+    for (size_t i = 1; i < n; i++)
+        if (!(v[cur] > v[i])) cur = i;
+    return (uint32_t)cur;
+}
+
+typedef struct {
+    size_t i;
+    float v;
+} orc_iv;
+
+/* sort_unstable_by(|a, b| b.1.partial_cmp(&a.1).unwrap_or(Equal)): descending;
+ * the order among equal values is immaterial (equal values add equal terms),
+ * ties broken by index here only to make qsort's output reproducible. */
+static int orc_cmp_desc(const void* pa, const void* pb) {
+    const orc_iv* a = (const orc_iv*)pa;
+    const orc_iv* b = (const orc_iv*)pb;
+    if (b->v < a->v) return -1;
+    if (b->v > a->v) return 1;
+    return a->i < b->i ? -1 : (a->i > b->i ? 1 : 0);
+}
+
+/* The fp32 sum of probs in index order (probs.iter().sum(): a fold from
+ * -0.0 in current Rust, 0.0 in older; only the sign of a zero sum differs,
+ * which no later step can see). */
+static float orc_sum_f32(const float* p, size_t n) {
+    float s = -0.0f;
+    for (size_t i = 0; i < n; i++) s += p[i];
+    return s;
+}
+
+/* sample_token (run.rs:203-251), step by step.  exp is the platform's expf,
+ * as Rust's f32::exp calls it. */
+uint32_t orc_sample_token(const float* logits, size_t n, float temperature, float top_p,
+                          size_t top_k, uint64_t* state) {
+    float* probs = (float*)malloc((n ? n : 1) * sizeof(float));
+    orc_iv* idx = (orc_iv*)malloc((n ? n : 1) * sizeof(orc_iv));
+    uint32_t out;
+    memcpy(probs, logits, n * sizeof(float));
+    if (temperature > 0.0f) {
+        const float inv_temp = 1.0f / temperature;
+        for (size_t i = 0; i < n; i++) probs[i] = expf(probs[i] * inv_temp);
+    }
+    if (top_k > 0 && top_k < n) {
+        for (size_t i = 0; i < n; i++) { idx[i].i = i; idx[i].v = probs[i]; }
+        qsort(idx, n, sizeof(orc_iv), orc_cmp_desc);
+        const float threshold = idx[top_k - 1].v;
+        for (size_t i = 0; i < n; i++)
+            if (probs[i] < threshold) probs[i] = 0.0f;
+    }
+    if (top_p < 1.0f) {
+        for (size_t i = 0; i < n; i++) { idx[i].i = i; idx[i].v = probs[i]; }
+        qsort(idx, n, sizeof(orc_iv), orc_cmp_desc);
+        const float sum = orc_sum_f32(probs, n);
+        if (sum > 0.0f) {
+            float cumsum = 0.0f;
+            float threshold = 3.40282347e+38f; /* f32::MAX */
+            for (size_t j = 0; j < n; j++) {
+                cumsum += idx[j].v / sum;
+                if (cumsum > top_p) { threshold = idx[j].v; break; }
+            }
+            for (size_t i = 0; i < n; i++)
+                if (probs[i] < threshold) probs[i] = 0.0f;
+        }
+    }
+    const float sum = orc_sum_f32(probs, n);
+    if (sum <= 0.0f) {
+        out = orc_argmax(logits, n);
+    } else {
+        const float r = orc_xorshift64_next_f32(state);
+        float cumsum = 0.0f;
+        out = UINT32_MAX;
+        for (size_t i = 0; i < n; i++) {
+            cumsum += probs[i] / sum;
+            if (r < cumsum) { out = (uint32_t)i; break; }
+        }
+        if (out == UINT32_MAX) out = orc_argmax(probs, n);
+    }
+    free(probs);
+    free(idx);
+    return out;
 }
