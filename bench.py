@@ -1042,6 +1042,15 @@ def cpu_baseline(mats, x_host):
 
 # --- main -------------------------------------------------------------------------------
 
+# Secondary workloads in the order the full run times them (None: the TinyLlama
+# stream, which takes the run's --steps/--warmup).
+SECONDARY = (("c0_single_gemv", single_gemv), ("c1_tinyllama_stream", None),
+             ("c2_prefill_gemm", prefill_gemm), ("c3_m_sweep", mistral_m_sweep),
+             ("c4_lm_head", lm_head), ("c4_next_token", next_token),
+             ("model_load", model_load),
+             ("q8_0_decode", q8_0_decode), ("col_major", col_major))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -1053,6 +1062,11 @@ def main():
                     help="time only the value's launches (no secondary, no CPU baseline)")
     ap.add_argument("--tinyllama-only", action="store_true",
                     help="time only the TinyLlama stream plan (profiling its traffic)")
+    ap.add_argument("--only", metavar="WORKLOAD", default=None,
+                    help="run only this secondary workload and print its result "
+                         "(c0_single_gemv, c2_prefill_gemm, c3_m_sweep, c4_lm_head, "
+                         "c4_next_token, model_load, q8_0_decode, col_major); used to "
+                         "profile one workload's kernels")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run only a plain 1 GiB device copy, 20 times (HBM counter "
                          "calibration under rocprofv3 --pmc)")
@@ -1071,6 +1085,13 @@ def main():
         copy_probe(torch)
         return
     lib = Lib()
+    if args.only is not None:
+        fns = dict(SECONDARY)
+        if fns.get(args.only) is None:
+            print(f"--only: unknown workload {args.only!r}", file=sys.stderr)
+            sys.exit(2)
+        print(json.dumps({args.only: fns[args.only](torch, lib)}), flush=True)
+        return
     if args.tinyllama_only:
         import hypno_amd as hk
         arena, offs, xs, jobs = build_stream(torch, lib, TINYLLAMA, TINYLLAMA_LAYERS, seed=1234)
@@ -1139,11 +1160,7 @@ def main():
     torch.cuda.empty_cache()
     if not args.no_secondary:
         sec = {}
-        for key, fn in (("c0_single_gemv", single_gemv), ("c1_tinyllama_stream", None),
-                        ("c2_prefill_gemm", prefill_gemm), ("c3_m_sweep", mistral_m_sweep),
-                        ("c4_lm_head", lm_head), ("c4_next_token", next_token),
-                        ("model_load", model_load),
-                        ("q8_0_decode", q8_0_decode), ("col_major", col_major)):
+        for key, fn in SECONDARY:
             print(f"[bench] secondary: {key}", file=sys.stderr, flush=True)
             if fn is None:
                 sec[key] = tinyllama_stream(torch, lib, args.steps, args.warmup)
