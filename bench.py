@@ -676,8 +676,9 @@ def next_token(torch, lib):
     torch.cuda.synchronize()
     ok = ok and want is not None and int(got.item()) == want
     return {"workload": "next token from K=4096 x N=128256 lm_head logits: greedy argmax and "
-                        "sample_token (one work-group; sequential fp32 walks as the "
-                        "reference); GPU us per call", "results": out,
+                        "sample_token (a launch over 63 ranges of the logits, then one "
+                        "work-group; the fp32 sums and walks one lane's sequential "
+                        "additions, as the reference's); GPU us per call", "results": out,
             "check": {"checked": bool(ok), "bar": "token equal to a host evaluation"}}
 
 

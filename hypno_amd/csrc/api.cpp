@@ -1007,8 +1007,17 @@ int hypno_hip_embed_tokens_dev(float* out, const uint8_t* table, size_t table_le
 int hypno_hip_argmax_dev(uint32_t* index, const float* logits, size_t n, void* stream) {
   if (!index || (!logits && n)) return fail(HYPNO_HIP_EINVAL, "argmax: NULL pointer");
   if (n > 0x7FFFFFFF) return fail(HYPNO_HIP_EINVAL, "argmax: n out of range");
-  hipError_t e = launch_sample_token(index, nullptr, logits, n, 0.0f, 1.0f, 0, nullptr,
-                                     (hipStream_t)stream);
+  hipStream_t s = (hipStream_t)stream;
+  DeviceState* ds = nullptr;
+  {
+    std::lock_guard<std::mutex> g(g_mu);
+    int st = device_state(&ds);
+    if (st) return st;
+  }
+  WsLock ws;
+  int st = lock_workspace(ds, s, sample_workspace_bytes(n, true), ws, "argmax workspace");
+  if (st) return st;
+  hipError_t e = launch_sample_token(index, nullptr, logits, n, 0.0f, 1.0f, 0, true, ws.p, s);
   if (e != hipSuccess) return hip_fail(e, "argmax launch");
   return HYPNO_HIP_OK;
 }
@@ -1027,10 +1036,10 @@ int hypno_hip_sample_token_dev(uint32_t* token, uint64_t* rng_state, const float
     if (st) return st;
   }
   WsLock ws;
-  int st = lock_workspace(ds, s, sample_workspace_bytes(n), ws, "sampling workspace");
+  int st = lock_workspace(ds, s, sample_workspace_bytes(n, false), ws, "sampling workspace");
   if (st) return st;
   hipError_t e = launch_sample_token(token, rng_state, logits, n, temperature, top_p, top_k,
-                                     ws.p, s);
+                                     false, ws.p, s);
   if (e != hipSuccess) return hip_fail(e, "sample_token launch");
   return HYPNO_HIP_OK;
 }

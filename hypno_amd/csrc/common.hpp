@@ -362,12 +362,13 @@ hipError_t launch_silu_mul(float* out, const float* gate, const float* up, size_
 hipError_t launch_embed_rows(float* out, const uint8_t* table, size_t table_len, int dtype,
                              const uint32_t* ids, size_t id0, size_t count, size_t hd,
                              hipStream_t s);
-// Next token from n logits (sample.hip): ws == NULL gives the greedy argmax,
-// otherwise sample_token with a workspace of sample_workspace_bytes(n).
-size_t sample_workspace_bytes(size_t n);
+// Next token from n logits (sample.hip): the greedy argmax (greedy), or
+// sample_token; two launches, with a workspace of
+// sample_workspace_bytes(n, greedy).
+size_t sample_workspace_bytes(size_t n, bool greedy);
 hipError_t launch_sample_token(uint32_t* token, uint64_t* state, const float* logits, size_t n,
-                               float temperature, float top_p, size_t top_k, void* ws,
-                               hipStream_t s);
+                               float temperature, float top_p, size_t top_k, bool greedy,
+                               void* ws, hipStream_t s);
 
 // Status reporting shared by the C ABI sources (api.cpp): record `msg` as the
 // calling thread's last error and return `status`; hip_status maps a HIP error

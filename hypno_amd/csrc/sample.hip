@@ -7,7 +7,9 @@
 //    dequantised bit-exactly, one work-group per token;
 //  * next-token choice from the lm_head's logits: greedy argmax and
 //    sample_token (run.rs:203-251) with its XorShift64 generator
-//    (run.rs:267-278), in one single-work-group kernel.
+//    (run.rs:267-278), in two launches: up to 64 work-groups over
+//    consecutive ranges of the logits (per-range argmax, p_i, top-k level-1
+//    histograms), then one work-group for the rest.
 //
 // sample_token, as the reference defines it:
 //   p_i = exp(l_i * (1 / temperature)) if temperature > 0, else l_i;
@@ -24,12 +26,14 @@
 // follows the last NaN, or the NaN itself when it is the last element).
 //
 // Here: the k-th largest p comes from a three-level radix select (11 + 11 +
-// 10 bits of an order-preserving key, LDS histograms); the p left non-zero
-// are compacted in index order (wave ballots) -- zeros add nothing to the
-// running sums, so walking only the non-zero p gives the reference's fp32
-// sums bit for bit; the top-p walk sorts them with a stable LSD radix sort
-// (four 8-bit passes, wave-ballot ranks); the running sums are one lane's
-// sequential fp32 additions and IEEE divisions, exactly the reference's.
+// 10 bits of an order-preserving key; the first level's histograms come
+// from the first launch); the p left non-zero are compacted in index order
+// -- zeros add nothing to the running sums, so walking only the non-zero p
+// gives the reference's fp32 sums bit for bit; the top-p walk sorts them
+// with a stable LSD radix sort (four 8-bit passes, wave-ballot ranks); the
+// running sums are one lane's sequential fp32 additions, exactly the
+// reference's, of quotients p / S that the other lanes divide out (IEEE
+// division, as the reference's) ahead of it.
 // exp is computed in fp64 and rounded once to fp32 (the reference calls the
 // platform's expf; the two agree except where a result lies within about
 // 2^-29 of a rounding boundary).
@@ -101,8 +105,11 @@ __global__ void __launch_bounds__(256) embed_rows_kernel(const EmbedArgs a) {
 
 // --- argmax and sampling ------------------------------------------------------------
 
-constexpr int kST = 1024;  // threads of the sampling work-group
+constexpr int kST = 1024;  // threads of a sampling work-group
 constexpr int kSW = kST / 64;
+constexpr int kMaxParts = 64;     // work-groups of the first sampling kernel
+constexpr int kPartElems = 2048;  // at least this many logits per such work-group
+constexpr int kBins1 = 2048;      // level-1 bins of the top-k radix select
 
 // Order-preserving map of fp32 bit patterns to u32 (ascending key = ascending
 // value, -0 just below +0) and back.
@@ -114,16 +121,31 @@ __device__ __forceinline__ float funkey(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
+// Argmax of one range of the logits: the last NaN in it (-1: none) and the
+// best (value, index) over the elements after that NaN, the later index among
+// equal values (bi = -1: nothing follows the NaN).
+struct ArgPart {
+  int ln;
+  int bi;
+  float bv;
+  int pad;
+};
+
 struct SampleArgs {
   const float* logits;
   int n;
   int greedy_only;  // argmax of the logits, nothing else
   float temperature, inv_temp, top_p;
   int top_k;
+  int parts;        // work-groups of the first kernel
   uint32_t* token;
   uint64_t* state;
-  // workspace, n entries each
-  float* probs;
+  // workspace
+  ArgPart* part;    // [parts]
+  int* seg_cnt;     // [parts]: candidates of each range
+  float* probs;     // n entries each from here on
+  uint32_t* seg_idx;  // range g's candidates at [lo_g, lo_g + seg_cnt[g])
+  float* seg_val;
   uint32_t* a_idx;
   float* a_val;
   uint32_t* k0;
@@ -134,7 +156,8 @@ constexpr int kChunk = 8192;  // floats of a sequential pass staged in LDS at a 
 
 struct SampleShared {
   float chunk[kChunk];
-  uint32_t hist[2048];
+  double mass[kBins1];
+  uint32_t hist[kBins1];
   uint32_t cnt[kSW][256];
   uint32_t base[256];
   uint32_t tot[256];
@@ -182,13 +205,18 @@ __device__ void select_from_top(SampleShared& sh, int nbins, uint32_t kk, uint32
   __syncthreads();
 }
 
-// Iterator::max_by(partial_cmp) over v(0..n): the last of equal maxima after
-// the last NaN (or that NaN if it is the last element); n == 0 gives 0.
+// (value, index) pairs: a replaces b when it is larger, or equal with the
+// larger index (Iterator::max_by keeps the last of equal maxima).
+__device__ __forceinline__ bool arg_better(float av, int ai, float bv, int bi) {
+  return ai >= 0 && (bi < 0 || av > bv || (av == bv && ai > bi));
+}
+
+// ArgPart of v(lo..hi), work-group wide; every thread gets the result.
 template <typename V>
-__device__ uint32_t argmax_fold(int n, V v, SampleShared& sh) {
+__device__ ArgPart argmax_part(int lo, int hi, V v, SampleShared& sh) {
   const int t = threadIdx.x;
-  int ln = -1;  // last NaN
-  for (int i = t; i < n; i += kST)
+  int ln = -1;
+  for (int i = lo + t; i < hi; i += kST)
     if (__builtin_isnan(v(i))) ln = i;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) ln = max(ln, __shfl_xor(ln, off, 64));
@@ -197,23 +225,20 @@ __device__ uint32_t argmax_fold(int n, V v, SampleShared& sh) {
   __syncthreads();
   ln = -1;
   for (int w = 0; w < kSW; w++) ln = max(ln, sh.ired[w]);
-  if (n == 0) return 0u;
-  if (ln == n - 1) return (uint32_t)ln;
   float bv = 0.0f;
   int bi = -1;
-  for (int i = ln + 1 + t; i < n; i += kST) {
+  for (int i = (ln >= 0 ? ln + 1 : lo) + t; i < hi; i += kST) {
     const float x = v(i);
     if (bi < 0 || x >= bv) {  // ties: the later index (i grows per thread)
       bv = x;
       bi = i;
     }
   }
-  // combine (value, index): larger value, then larger index
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     const float ov = __shfl_xor(bv, off, 64);
     const int oi = __shfl_xor(bi, off, 64);
-    if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi))) {
+    if (arg_better(ov, oi, bv, bi)) {
       bv = ov;
       bi = oi;
     }
@@ -226,30 +251,57 @@ __device__ uint32_t argmax_fold(int n, V v, SampleShared& sh) {
   __syncthreads();
   bv = 0.0f;
   bi = -1;
-  for (int w = 0; w < kSW; w++) {
-    const float ov = sh.fred[w];
-    const int oi = sh.ired[w];
-    if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi))) {
-      bv = ov;
-      bi = oi;
+  for (int w = 0; w < kSW; w++)
+    if (arg_better(sh.fred[w], sh.ired[w], bv, bi)) {
+      bv = sh.fred[w];
+      bi = sh.ired[w];
     }
-  }
   __syncthreads();
+  return ArgPart{ln, bi, bv, 0};
+}
+
+// Iterator::max_by(partial_cmp) over n values from the ArgParts of
+// consecutive ranges covering them: the last of equal maxima after the last
+// NaN, or that NaN if it is the last element; n == 0 gives 0.  Each range's
+// best already excludes what precedes its own last NaN, and ranges before
+// the range of the overall last NaN hold only indices below it.
+__device__ uint32_t argmax_combine(const ArgPart* p, int parts, int n) {
+  if (n == 0) return 0u;
+  int ln = -1;
+  for (int g = 0; g < parts; g++) ln = max(ln, p[g].ln);
+  if (ln == n - 1) return (uint32_t)ln;
+  float bv = 0.0f;
+  int bi = -1;
+  for (int g = 0; g < parts; g++)
+    if (p[g].bi > ln && arg_better(p[g].bv, p[g].bi, bv, bi)) {
+      bv = p[g].bv;
+      bi = p[g].bi;
+    }
   return (uint32_t)bi;
 }
 
-// Compact the elements i in [0, n) with val(i) != 0 (NaN counts) into
-// (idx[], v[]) in index order; returns their count.
+// Iterator::max_by over v(0..n) in one work-group.
 template <typename V>
-__device__ int compact_nonzero(int n, V val, uint32_t* idx, float* v, SampleShared& sh) {
+__device__ uint32_t argmax_fold(int n, V v, SampleShared& sh) {
+  const ArgPart p = argmax_part(0, n, v, sh);
+  return argmax_combine(&p, 1, n);
+}
+
+// Compact the elements i in [lo, hi) for which keep(i, x) holds, x = val(i),
+// into (idx[], v[]) in index order (idx holds i); returns their count.  A
+// work-group pass per kST elements: wave ballots give ranks, LDS the wave
+// offsets.
+template <typename V, typename K>
+__device__ int compact_range(int lo, int hi, V val, K keep, uint32_t* idx, float* v,
+                             SampleShared& sh) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const uint64_t lt = (1ull << lane) - 1ull;
   int L = 0;
-  for (int b0 = 0; b0 < n; b0 += kST) {
+  for (int b0 = lo; b0 < hi; b0 += kST) {
     const int i = b0 + t;
-    const float x = i < n ? val(i) : 0.0f;
-    const bool nz = i < n && x != 0.0f;
-    const uint64_t m = __ballot(nz);
+    const float x = i < hi ? val(i) : 0.0f;
+    const bool kp = i < hi && keep(i, x);
+    const uint64_t m = __ballot(kp);
     if (lane == 0) sh.wsum[wave] = (uint32_t)__popcll(m);
     __syncthreads();
     int off = L, tot = 0;
@@ -258,7 +310,7 @@ __device__ int compact_nonzero(int n, V val, uint32_t* idx, float* v, SampleShar
       if (w < wave) off += c;
       tot += c;
     }
-    if (nz) {
+    if (kp) {
       const int d = off + __popcll(m & lt);
       idx[d] = (uint32_t)i;
       v[d] = x;
@@ -326,29 +378,163 @@ __device__ void radix_sort_keys(uint32_t* k0, uint32_t* k1, int L, SampleShared&
   }
 }
 
-// One thread's in-order pass over x(0..cnt) (the reference's sequential fp32
-// loops), the work-group staging kChunk values at a time in LDS: f(j, x_j)
-// for j = 0, 1, ... until it returns true.  Returns that j, or -1.
-template <typename X, typename F>
-__device__ int seq_walk(int cnt, X x, F f, SampleShared& sh) {
+// The k-th largest (1-based, 1 <= kk <= cnt) of the keys key(j), j in
+// [0, cnt), by radix select: 11, 11 and 10 bits of the key, one histogram
+// pass per level.
+template <typename Key>
+__device__ uint32_t kth_largest_key(int cnt, Key key, uint32_t kk, SampleShared& sh) {
   const int t = threadIdx.x;
+  uint32_t b1, b2, b3;
+  for (int i = t; i < 2048; i += kST) sh.hist[i] = 0;
+  __syncthreads();
+  for (int j = t; j < cnt; j += kST) atomicAdd(&sh.hist[key(j) >> 21], 1u);
+  __syncthreads();
+  select_from_top(sh, 2048, kk, &b1, &kk);
+  for (int i = t; i < 2048; i += kST) sh.hist[i] = 0;
+  __syncthreads();
+  for (int j = t; j < cnt; j += kST) {
+    const uint32_t k = key(j);
+    if ((k >> 21) == b1) atomicAdd(&sh.hist[(k >> 10) & 2047u], 1u);
+  }
+  __syncthreads();
+  select_from_top(sh, 2048, kk, &b2, &kk);
+  for (int i = t; i < 1024; i += kST) sh.hist[i] = 0;
+  __syncthreads();
+  const uint32_t pre = (b1 << 11) | b2;
+  for (int j = t; j < cnt; j += kST) {
+    const uint32_t k = key(j);
+    if ((k >> 10) == pre) atomicAdd(&sh.hist[k & 1023u], 1u);
+  }
+  __syncthreads();
+  select_from_top(sh, 1024, kk, &b3, &kk);
+  return (pre << 10) | b3;
+}
+
+// The reference's sequential fp32 loops run on thread 0 over values the whole
+// work-group stages in LDS, kChunk at a time.  The values themselves (the
+// quotients p / S of the walks) are computed by the staging threads: only the
+// dependent additions stay serial.  Thread 0 reads the next run of kRun
+// staged values while it adds the current one (two register buffers in
+// turn), so the LDS latency hides behind the additions.
+constexpr int kRun = 32;
+constexpr int kRunV = kRun / 4;  // float4 per run
+
+__device__ __forceinline__ void load_run(float4 (&v)[kRunV], const float4* c4, int r) {
+#pragma unroll
+  for (int u = 0; u < kRunV; u++) v[u] = c4[r * kRunV + u];
+}
+
+// -0.0 + x(0) + x(1) + ... in index order, fp32 (Iterator::sum); every thread
+// gets the result.
+template <typename X>
+__device__ float seq_sum(int cnt, X x, SampleShared& sh) {
+  const int t = threadIdx.x;
+  float s = -0.0f;
   for (int b0 = 0; b0 < cnt; b0 += kChunk) {
     const int len = min(kChunk, cnt - b0);
     for (int j = t; j < len; j += kST) sh.chunk[j] = x(b0 + j);
     __syncthreads();
     if (t == 0) {
-      int hit = -1;
-      int j = 0;
-      for (; j + 4 <= len; j += 4) {  // 16-byte LDS reads, in order
-        const float4 q = *reinterpret_cast<const float4*>(&sh.chunk[j]);
-        if (f(b0 + j, q.x)) { hit = b0 + j; break; }
-        if (f(b0 + j + 1, q.y)) { hit = b0 + j + 1; break; }
-        if (f(b0 + j + 2, q.z)) { hit = b0 + j + 2; break; }
-        if (f(b0 + j + 3, q.w)) { hit = b0 + j + 3; break; }
+      const float4* c4 = reinterpret_cast<const float4*>(sh.chunk);
+      const int runs = len / kRun;
+      float4 v[kRunV], w[kRunV];
+      auto add = [&](const float4(&q)[kRunV]) {
+#pragma unroll
+        for (int u = 0; u < kRunV; u++) {
+          s += q[u].x;
+          s += q[u].y;
+          s += q[u].z;
+          s += q[u].w;
+        }
+      };
+      if (runs > 0) load_run(v, c4, 0);
+      for (int r = 0; r < runs; r += 2) {
+        if (r + 1 < runs) load_run(w, c4, r + 1);
+        add(v);
+        if (r + 1 >= runs) break;
+        if (r + 2 < runs) load_run(v, c4, r + 2);
+        add(w);
       }
-      if (hit < 0)
-        for (; j < len; j++)
-          if (f(b0 + j, sh.chunk[j])) { hit = b0 + j; break; }
+      for (int j = runs * kRun; j < len; j++) s += sh.chunk[j];
+    }
+    __syncthreads();
+  }
+  if (t == 0) sh.f[0] = s;
+  __syncthreads();
+  const float r = sh.f[0];
+  __syncthreads();
+  return r;
+}
+
+// The first j in [0, cnt) at which cum (0.0 + q(0) + ... + q(j), fp32, in
+// order) exceeds thr (thread 0's value); -1 if none.  Thread 0 forms a run of
+// kRun running sums at a time and compares once per run:
+//  * when every staged value of the chunk is >= 0 (no NaN), the sums never
+//    decrease (fp32 addition of a non-negative value is monotone), so the
+//    run's last sum exceeds thr exactly when one of its sums does (a NaN sum
+//    carried in from before compares false throughout, as it should);
+//  * otherwise it compares the maximum of the run's sums (fmaxf passes over
+//    NaN and returns one of its operands).
+// The run that crosses is walked again one value at a time.
+template <typename Q>
+__device__ int seq_cross(int cnt, Q q, float thr, SampleShared& sh) {
+  const int t = threadIdx.x;
+  float cum = 0.0f;
+  for (int b0 = 0; b0 < cnt; b0 += kChunk) {
+    const int len = min(kChunk, cnt - b0);
+    int odd = 0;
+    for (int j = t; j < len; j += kST) {
+      const float v = q(b0 + j);
+      sh.chunk[j] = v;
+      odd |= !(v >= 0.0f);
+    }
+    const bool mono = __syncthreads_or(odd) == 0;
+    if (t == 0) {
+      const float4* c4 = reinterpret_cast<const float4*>(sh.chunk);
+      const int runs = len / kRun;
+      int hit = -1, r = 0;
+      float4 v[kRunV], w[kRunV];
+      // cum over one run; true (cum unchanged) when the run crosses thr
+      auto run = [&](const float4(&x)[kRunV]) {
+        float c = cum;
+        if (mono) {
+#pragma unroll
+          for (int u = 0; u < kRunV; u++) {
+            c += x[u].x;
+            c += x[u].y;
+            c += x[u].z;
+            c += x[u].w;
+          }
+          if (c > thr) return true;
+        } else {
+          float m = -__builtin_inff();
+#pragma unroll
+          for (int u = 0; u < kRunV; u++) {
+            const float c0 = c + x[u].x, c1 = c0 + x[u].y, c2 = c1 + x[u].z, c3 = c2 + x[u].w;
+            m = fmaxf(m, fmaxf(fmaxf(c0, c1), fmaxf(c2, c3)));
+            c = c3;
+          }
+          if (m > thr) return true;
+        }
+        cum = c;
+        return false;
+      };
+      if (runs > 0) load_run(v, c4, 0);
+      for (; r < runs;) {
+        if (r + 1 < runs) load_run(w, c4, r + 1);
+        if (run(v)) break;
+        if (++r >= runs) break;
+        if (r + 1 < runs) load_run(v, c4, r + 1);
+        if (run(w)) break;
+        ++r;
+      }
+      for (int j = r * kRun; j < len; j++) {  // the crossing run, or the tail
+        cum += sh.chunk[j];
+        if (cum > thr) {
+          hit = b0 + j;
+          break;
+        }
+      }
       sh.ired[0] = hit;
     }
     __syncthreads();
@@ -359,89 +545,164 @@ __device__ int seq_walk(int cnt, X x, F f, SampleShared& sh) {
   return -1;
 }
 
+// First kernel, `parts` work-groups over consecutive ranges [lo, hi) of the
+// logits: each range's ArgPart; unless greedy, p_i for its elements and the
+// range's candidates, in index order, at [lo, lo + seg_cnt[g]) of
+// seg_idx / seg_val:
+//  * with top-k, the elements whose key is at least the range's own k-th
+//    largest key (every element of a range of at most k), and every NaN: an
+//    element that top-k keeps is at least the overall k-th largest p, and
+//    fewer than k elements in all (so in its range) exceed it;
+//  * without, the non-zero p (zeros add nothing to the running sums).
+__global__ void __launch_bounds__(kST) sample_parts_kernel(const SampleArgs a) {
+  __shared__ SampleShared sh;
+  const int t = threadIdx.x, g = blockIdx.x;
+  const int lo = (int)((long long)a.n * g / a.parts);
+  const int hi = (int)((long long)a.n * (g + 1) / a.parts);
+  const ArgPart ap = argmax_part(lo, hi, [&](int i) { return a.logits[i]; }, sh);
+  if (t == 0) a.part[g] = ap;
+  if (a.greedy_only) return;
+  const bool scale = a.temperature > 0.0f;
+  for (int i = lo + t; i < hi; i += kST) {
+    const float l = a.logits[i];
+    a.probs[i] = scale ? (float)exp((double)(l * a.inv_temp)) : l;
+  }
+  __syncthreads();
+  const bool use_k = a.top_k > 0 && a.top_k < a.n;
+  int cnt;
+  if (use_k) {
+    const uint32_t kth = hi - lo > a.top_k
+                             ? kth_largest_key(hi - lo, [&](int j) { return fkey(a.probs[lo + j]); },
+                                               (uint32_t)a.top_k, sh)
+                             : 0u;
+    cnt = compact_range(
+        lo, hi, [&](int i) { return a.probs[i]; },
+        [&](int, float x) { return fkey(x) >= kth || __builtin_isnan(x); }, a.seg_idx + lo,
+        a.seg_val + lo, sh);
+  } else {
+    cnt = compact_range(
+        lo, hi, [&](int i) { return a.probs[i]; }, [&](int, float x) { return x != 0.0f; },
+        a.seg_idx + lo, a.seg_val + lo, sh);
+  }
+  if (t == 0) a.seg_cnt[g] = cnt;
+}
+
+// Second kernel, one work-group: the rest of sample_token.
 __global__ void __launch_bounds__(kST) sample_token_kernel(const SampleArgs a) {
   __shared__ SampleShared sh;
   const int t = threadIdx.x;
   const int n = a.n;
   if (a.greedy_only) {
-    const uint32_t am = argmax_fold(n, [&](int i) { return a.logits[i]; }, sh);
-    if (t == 0) *a.token = am;
+    if (t == 0) *a.token = argmax_combine(a.part, a.parts, n);
     return;
   }
   const bool use_k = a.top_k > 0 && a.top_k < n;
-  const bool scale = a.temperature > 0.0f;
-
-  // p_i, and the level-1 histogram of their keys for top-k
-  if (use_k)
-    for (int i = t; i < 2048; i += kST) sh.hist[i] = 0;
-  __syncthreads();
-  for (int i = t; i < n; i += kST) {
-    const float l = a.logits[i];
-    const float p = scale ? (float)exp((double)(l * a.inv_temp)) : l;
-    a.probs[i] = p;
-    if (use_k) atomicAdd(&sh.hist[fkey(p) >> 21], 1u);
+  // the ranges' candidate lists, concatenated in order (index order): into
+  // k0 (indices) / k1 (values) for the top-k pass, else straight into the
+  // non-zero list a_idx / a_val
+  if (t == 0) {
+    int run = 0;
+    for (int g = 0; g < a.parts; g++) {
+      sh.cnt[0][g] = (uint32_t)run;
+      run += a.seg_cnt[g];
+    }
+    sh.u[2] = (uint32_t)run;
   }
   __syncthreads();
-  // top_k: the k-th largest p by radix select (11, 11, 10 bits of its key)
+  const int C = (int)sh.u[2];
+  uint32_t* cidx = use_k ? a.k0 : a.a_idx;
+  float* cval = use_k ? reinterpret_cast<float*>(a.k1) : a.a_val;
+  for (int g = 0; g < a.parts; g++) {
+    const int lo = (int)((long long)n * g / a.parts);
+    const int off = (int)sh.cnt[0][g], c = a.seg_cnt[g];
+    for (int j = t; j < c; j += kST) {
+      cidx[off + j] = a.seg_idx[lo + j];
+      cval[off + j] = a.seg_val[lo + j];
+    }
+  }
+  __syncthreads();
+  // top_k: the k-th largest p; the non-zero p not below it, in index order
   float thr_k = -__builtin_inff();  // p < thr_k -> 0 (nothing when -inf)
+  int L;
   if (use_k) {
-    uint32_t b1, b2, b3, kk;
-    select_from_top(sh, 2048, (uint32_t)a.top_k, &b1, &kk);
-    for (int i = t; i < 2048; i += kST) sh.hist[i] = 0;
+    thr_k = funkey(kth_largest_key(C, [&](int j) { return fkey(cval[j]); }, (uint32_t)a.top_k, sh));
+    L = compact_range(
+        0, C, [&](int j) { return cval[j]; },
+        [&](int, float x) { return !(x < thr_k) && x != 0.0f; }, a.a_idx, a.a_val, sh);
+    for (int j = t; j < L; j += kST) a.a_idx[j] = a.k0[a.a_idx[j]];  // positions -> tokens
     __syncthreads();
-    for (int i = t; i < n; i += kST) {
-      const uint32_t k = fkey(a.probs[i]);
-      if ((k >> 21) == b1) atomicAdd(&sh.hist[(k >> 10) & 2047u], 1u);
-    }
-    __syncthreads();
-    select_from_top(sh, 2048, kk, &b2, &kk);
-    for (int i = t; i < 1024; i += kST) sh.hist[i] = 0;
-    __syncthreads();
-    const uint32_t pre = (b1 << 11) | b2;
-    for (int i = t; i < n; i += kST) {
-      const uint32_t k = fkey(a.probs[i]);
-      if ((k >> 10) == pre) atomicAdd(&sh.hist[k & 1023u], 1u);
-    }
-    __syncthreads();
-    select_from_top(sh, 1024, kk, &b3, &kk);
-    thr_k = funkey((pre << 10) | b3);
+  } else {
+    L = C;
   }
-  auto eff1 = [&](int i) {
-    const float p = a.probs[i];
-    return p < thr_k ? 0.0f : p;
-  };
-  // the non-zero p in index order (zeros add nothing to the running sums)
-  const int L = compact_nonzero(n, eff1, a.a_idx, a.a_val, sh);
-  // fp32 sum in index order (thread 0 keeps it; the others only need the
-  // branch outcomes, which are shared through LDS)
-  auto seq_sum = [&](const float* v, int cnt) {
-    float s = -0.0f;
-    seq_walk(cnt, [&](int j) { return v[j]; }, [&](int, float x) { s += x; return false; }, sh);
-    if (threadIdx.x == 0) sh.f[0] = s;
-    __syncthreads();
-    const float r = sh.f[0];
-    __syncthreads();
-    return r;
-  };
-  // top_p: walk the p in descending order (sorted keys, zeros skipped)
+  // top_p: walk the p in descending order (sorted keys)
   float thr_p = -__builtin_inff();
   int Lb = L;
   const float* bval = a.a_val;
   const uint32_t* bidx = a.a_idx;
   if (a.top_p < 1.0f) {
-    const float sum1 = seq_sum(a.a_val, L);
+    const float sum1 = seq_sum(L, [&](int j) { return a.a_val[j]; }, sh);
     if (sum1 > 0.0f) {
-      for (int j = t; j < L; j += kST) a.k0[j] = ~fkey(a.a_val[j]);  // descending
-      __syncthreads();
-      radix_sort_keys(a.k0, a.k1, L, sh);
-      float cum = 0.0f;
-      const int at = seq_walk(
-          L, [&](int j) { return funkey(~a.k0[j]); },
-          [&](int, float p) {
-            cum += p / sum1;
-            return cum > a.top_p;
-          },
-          sh);
+      // The walk only reaches the largest p: for long lists, sort just the
+      // bins (11 key bits) from the top down to where their exact mass
+      // reaches top_p + margin of the total, the margin covering how far the
+      // fp32 sums can stray from exact ones (2 (L + 2) 2^-24 relative);
+      // failing that (top_p near 1, negative or non-finite p), or should the
+      // walk not cross in them, all of the p.
+      const double margin = 2.0 * ((double)L + 2.0) * 0x1p-24;
+      int at = -1;
+      if (L > kChunk && (double)a.top_p + margin < 1.0) {
+        for (int i = t; i < kBins1; i += kST) {
+          sh.hist[i] = 0;
+          sh.mass[i] = 0.0;
+        }
+        __syncthreads();
+        int bad = 0;
+        for (int j = t; j < L; j += kST) {
+          const float x = a.a_val[j];
+          bad |= !(x > 0.0f && x < __builtin_inff());
+          const uint32_t b = fkey(x) >> 21;
+          atomicAdd(&sh.hist[b], 1u);
+          atomicAdd(&sh.mass[b], (double)x);
+        }
+        bad = __syncthreads_or(bad);
+        if (t == 0) {
+          int top = -1;
+          if (!bad) {
+            double tot = 0.0;
+            for (int b = 0; b < kBins1; b++) tot += sh.mass[b];
+            const double need = ((double)a.top_p + margin) * tot;
+            double acc = 0.0;
+            for (int b = kBins1 - 1; b >= 0; b--) {
+              acc += sh.mass[b];
+              if (acc >= need) {
+                top = b;
+                break;
+              }
+            }
+          }
+          sh.ired[0] = top;
+        }
+        __syncthreads();
+        const int top = sh.ired[0];
+        __syncthreads();
+        if (top >= 0) {
+          const uint32_t tkey = (uint32_t)top << 21;
+          float* cv = reinterpret_cast<float*>(a.k0);
+          const int Lc = compact_range(
+              0, L, [&](int j) { return a.a_val[j]; },
+              [&](int, float x) { return fkey(x) >= tkey; }, a.k1, cv, sh);
+          for (int j = t; j < Lc; j += kST) a.k0[j] = ~fkey(cv[j]);  // descending
+          __syncthreads();
+          radix_sort_keys(a.k0, a.k1, Lc, sh);
+          at = seq_cross(Lc, [&](int j) { return funkey(~a.k0[j]) / sum1; }, a.top_p, sh);
+        }
+      }
+      if (at < 0) {
+        for (int j = t; j < L; j += kST) a.k0[j] = ~fkey(a.a_val[j]);  // descending
+        __syncthreads();
+        radix_sort_keys(a.k0, a.k1, L, sh);
+        at = seq_cross(L, [&](int j) { return funkey(~a.k0[j]) / sum1; }, a.top_p, sh);
+      }
       thr_p = at >= 0 ? funkey(~a.k0[at]) : 3.40282347e+38f;
       // p < thr_p -> 0: keep the survivors of the index-ordered list, in
       // order (k0 / k1 reused as the second list's storage)
@@ -450,19 +711,19 @@ __global__ void __launch_bounds__(kST) sample_token_kernel(const SampleArgs a) {
       const uint32_t* ai = a.a_idx;
       const float* av = a.a_val;
       __syncthreads();
-      Lb = compact_nonzero(L, [&](int j) { return av[j] < thr_p ? 0.0f : av[j]; }, b_idx, b_val,
-                           sh);
-      // compact_nonzero stored list positions; map them to token indices
+      Lb = compact_range(
+          0, L, [&](int j) { return av[j]; }, [&](int, float x) { return !(x < thr_p); }, b_idx,
+          b_val, sh);
+      // compact_range stored list positions; map them to token indices
       for (int j = t; j < Lb; j += kST) b_idx[j] = ai[b_idx[j]];
       __syncthreads();
       bval = b_val;
       bidx = b_idx;
     }
   }
-  const float sum2 = seq_sum(bval, Lb);
+  const float sum2 = seq_sum(Lb, [&](int j) { return bval[j]; }, sh);
   if (sum2 <= 0.0f) {
-    const uint32_t am = argmax_fold(n, [&](int i) { return a.logits[i]; }, sh);
-    if (t == 0) *a.token = am;
+    if (t == 0) *a.token = argmax_combine(a.part, a.parts, n);
     return;
   }
   // r = next_f32(): xorshift 13, 7, 17, then the top 24 bits / 2^24
@@ -475,14 +736,8 @@ __global__ void __launch_bounds__(kST) sample_token_kernel(const SampleArgs a) {
     *a.state = x;
     r = (float)(x >> 40) / 16777216.0f;
   }
-  float cum = 0.0f;
-  const int at = seq_walk(
-      Lb, [&](int j) { return bval[j]; },
-      [&](int, float p) {
-        cum += p / sum2;
-        return r < cum;
-      },
-      sh);
+  // the first token whose running sum of p / S exceeds r (r < cum)
+  const int at = seq_cross(Lb, [&](int j) { return bval[j] / sum2; }, r, sh);
   if (at >= 0) {
     if (t == 0) *a.token = bidx[at];
     return;
@@ -508,28 +763,50 @@ hipError_t launch_embed_rows(float* out, const uint8_t* table, size_t table_len,
   return hipGetLastError();
 }
 
-size_t sample_workspace_bytes(size_t n) { return 5 * ((n * 4 + 255) / 256 * 256) + 256; }
+static size_t round_up256(size_t v) { return (v + 255) / 256 * 256; }
+
+static int sample_parts(size_t n) {
+  const size_t p = (n + kPartElems - 1) / kPartElems;
+  return (int)(p < 1 ? 1 : p > (size_t)kMaxParts ? (size_t)kMaxParts : p);
+}
+
+size_t sample_workspace_bytes(size_t n, bool greedy) {
+  const size_t head = round_up256(kMaxParts * sizeof(ArgPart)) + round_up256(kMaxParts * 4);
+  if (greedy) return head;
+  return head + 7 * round_up256(n * 4);
+}
 
 hipError_t launch_sample_token(uint32_t* token, uint64_t* state, const float* logits, size_t n,
-                               float temperature, float top_p, size_t top_k, void* ws,
-                               hipStream_t s) {
+                               float temperature, float top_p, size_t top_k, bool greedy,
+                               void* ws, hipStream_t s) {
   SampleArgs a;
   a.logits = logits;
   a.n = (int)n;
-  a.greedy_only = ws == nullptr;
+  a.greedy_only = greedy ? 1 : 0;
   a.temperature = temperature;
   a.inv_temp = 1.0f / temperature;  // as the reference: 1.0 / temperature in f32
   a.top_p = top_p;
   a.top_k = top_k > 0x7FFFFFFFull ? 0x7FFFFFFF : (int)top_k;
+  a.parts = sample_parts(n);
   a.token = token;
   a.state = state;
-  const size_t plane = (n * 4 + 255) / 256 * 256;
   uint8_t* w = static_cast<uint8_t*>(ws);
-  a.probs = reinterpret_cast<float*>(w);
-  a.a_idx = reinterpret_cast<uint32_t*>(w ? w + plane : nullptr);
-  a.a_val = reinterpret_cast<float*>(w ? w + 2 * plane : nullptr);
-  a.k0 = reinterpret_cast<uint32_t*>(w ? w + 3 * plane : nullptr);
-  a.k1 = reinterpret_cast<uint32_t*>(w ? w + 4 * plane : nullptr);
+  const size_t parts_b = round_up256(kMaxParts * sizeof(ArgPart));
+  const size_t plane = round_up256(n * 4);
+  a.part = reinterpret_cast<ArgPart*>(w);
+  a.seg_cnt = reinterpret_cast<int*>(w + parts_b);
+  uint8_t* q = greedy ? nullptr : w + parts_b + round_up256(kMaxParts * 4);
+  auto pl = [&](int i) { return q ? q + (size_t)i * plane : nullptr; };
+  a.probs = reinterpret_cast<float*>(pl(0));
+  a.seg_idx = reinterpret_cast<uint32_t*>(pl(1));
+  a.seg_val = reinterpret_cast<float*>(pl(2));
+  a.a_idx = reinterpret_cast<uint32_t*>(pl(3));
+  a.a_val = reinterpret_cast<float*>(pl(4));
+  a.k0 = reinterpret_cast<uint32_t*>(pl(5));
+  a.k1 = reinterpret_cast<uint32_t*>(pl(6));
+  hipLaunchKernelGGL(sample_parts_kernel, dim3(a.parts), dim3(kST), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(sample_token_kernel, dim3(1), dim3(kST), 0, s, a);
   return hipGetLastError();
 }

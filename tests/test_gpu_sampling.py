@@ -106,6 +106,24 @@ def test_argmax(env, orc):
     cases.append(w)
     cases.append(np.array([0.0, -0.0], np.float32))
     cases.append(np.array([-1.0], np.float32))
+    # the device splits the logits into consecutive ranges: NaNs and maxima
+    # on either side of range boundaries, a maximum before the last NaN,
+    # every element NaN, and sizes with one, two and three ranges
+    u = x.copy()
+    u[3] = 100.0                       # larger than anything after the NaN
+    u[[10, 64000]] = np.nan
+    cases.append(u)
+    for b in (2035, 2036, 4071, 4072, 126220):  # near 128256 * g / 63
+        v = x.copy()
+        v[b] = np.nan
+        v[b - 1] = 60.0
+        v[b + 1] = 40.0
+        cases.append(v)
+    cases.append(np.full(5000, np.nan, np.float32))
+    for n in (2047, 2049, 5000):
+        s = rng.standard_normal(n).astype(np.float32)
+        s[[0, n - 1]] = s.max()
+        cases.append(s)
     for c in cases:
         got = hk.argmax(torch.from_numpy(c).cuda())
         torch.cuda.synchronize()
@@ -119,6 +137,9 @@ def test_argmax(env, orc):
 
 EXACT_CASES = [  # (top_p, top_k)
     (1.0, 0), (1.0, 40), (0.9, 0), (0.9, 40), (0.5, 1000), (0.95, 1), (0.999, 50000),
+    # k around the length of the device's per-range candidate lists (128256
+    # logits in 63 ranges of 2035-2036) and k = n - 1
+    (0.9, 2035), (1.0, 2036), (0.8, 3000), (1.0, VOCAB - 1),
 ]
 
 
