@@ -5,10 +5,13 @@
 // Q4_0 block of W exactly once, in coalesced 16-byte pieces of contiguous
 // row segments, and does the arithmetic on the matrix cores:
 //
-//  * A work-group owns 64 rows of W (16 per wave, one MFMA column tile each)
-//    and a range of K; K streams through LDS in stages of 256 (8 blocks):
-//    DMA (global_load_lds) of the stage's activation rows and W row segments
-//    into a ring of LDS slots, one barrier per stage.
+//  * A work-group owns 64 rows of W and a range of K; K streams through LDS
+//    in stages of 256 (8 blocks): DMA (global_load_lds) of the stage's
+//    activation rows and W row segments into a ring of LDS slots, one
+//    barrier per stage.  Its 8 waves form 4 row groups (16 rows, one MFMA
+//    column tile each) x 2 K-groups (blocks 0-3 / 4-7 of every stage): two
+//    waves per SIMD, so one's unpacking overlaps the other's waits; at the
+//    end K-group 1 hands its sums to K-group 0 through LDS (fixed order).
 //  * Lane (n, g) of a wave takes nibble quarter g of row n's block from LDS
 //    (4 bytes), turns it into exact fp16 (nib - 8) in registers and feeds
 //    v_mfma_f32_16x16x32_f16; the block's partial is scaled in fp32.
@@ -106,7 +109,9 @@ x_skinny_kernel(uint8_t* __restrict__ xa, float* __restrict__ inv_s, const float
 // a row's 144 bytes of a stage start 16-byte aligned (rows are K/32*18 =
 // multiples of 144 bytes when K % 256 == 0), so they move as nine 16-byte
 // pieces.
-constexpr int kSkWaves = 4;                    // waves per work-group, 16 W rows each
+constexpr int kSkWaves = 4;                    // row groups per work-group, 16 W rows each
+constexpr int kSkKGroups = 2;                  // waves per row group, half a stage's blocks each
+constexpr int kSkThreads = 64 * kSkWaves * kSkKGroups;
 constexpr int kSkRowBytes = 144;               // W bytes of one row and stage
 constexpr int kSkRowPieces = kSkRowBytes / 16;  // 9
 constexpr int kSkWDma = (16 * kSkRowPieces + 63) / 64;  // 3 DMAs per wave and stage
@@ -118,13 +123,18 @@ template <int MF>
 struct SkGeom {
   static constexpr int kRows = 16 * MF;                      // A rows
   static constexpr int kXBytes = kRows * kSkXRowBytes;       // X chunk per stage
-  static constexpr int kXDma = kXBytes / 1024 / kSkWaves;    // X DMAs per wave and stage
+  static constexpr int kXDma = kXBytes / 1024 / (kSkWaves * kSkKGroups);  // X DMAs per wave
   static constexpr int kSlot = kXBytes + kSkWaves * kSkWBytes;
   static constexpr int kRing = MF == 4 ? 3 : 4;              // stages in LDS
   static constexpr int kLds = kRing * kSlot;                 // 80 / 112 / 132 KB
-  static constexpr int kReads = kXDma + kSkWDma;             // DMAs per wave and stage
+  // DMAs per wave and stage: the row group's first two W DMAs go with K-group
+  // 0, the third (16 rows' last pieces and, when split, the 1/s table) with
+  // K-group 1.
+  static constexpr int kReads0 = kXDma + 2;
+  static constexpr int kReads1 = kXDma + 1;
+  static_assert(kSkWDma == 3, "W DMA split between the K-groups");
   static_assert(kLds <= 160 * 1024, "LDS budget");
-  static_assert((kRing - 2) * kReads <= 63, "vmcnt range");
+  static_assert((kRing - 2) * kReads0 <= 63, "vmcnt range");
 };
 
 // Wait until at most N of this wave's global reads are outstanding and its
@@ -170,13 +180,15 @@ struct SkinnyArgs {
 // row n; it becomes exact fp16 (nib - 8) in registers, and the block's
 // partial is scaled in fp32.
 template <int MF, bool SPLIT>
-__global__ void __launch_bounds__(64 * kSkWaves) q4_0_skinny_kernel(const SkinnyArgs a) {
+__global__ void __launch_bounds__(kSkThreads) q4_0_skinny_kernel(const SkinnyArgs a) {
   using G = SkGeom<MF>;
   extern __shared__ __align__(16) uint8_t smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rw = wave & 3;   // row group: W rows 16 rw .. 16 rw + 15 of the tile
+  const int kg = wave >> 2;  // K-group: blocks 4 kg .. 4 kg + 3 of every stage
   const int n16 = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * 16 * kSkWaves + 16 * wave;  // this wave's first W row
+  const int n0 = blockIdx.x * 16 * kSkWaves + 16 * rw;  // this wave's first W row
   const int gsteps = a.K / kSkStageK;
   const int z = blockIdx.y;
   const int s0 = (int)((long long)gsteps * z / a.splits);
@@ -184,9 +196,10 @@ __global__ void __launch_bounds__(64 * kSkWaves) q4_0_skinny_kernel(const Skinny
   const size_t w_row = (size_t)(a.K / 32) * 18;
   const size_t x_row = (size_t)a.K * 2;
 
-  // W DMA i, lane -> piece p = 64 i + lane of the wave's 16 x 9 pieces: row
-  // p / 9, piece p % 9 (lanes past 144 are idle).  Rows past N re-read row
-  // N - 1 (their outputs are not stored).
+  // W DMA i, lane -> piece p = 64 i + lane of the row group's 16 x 9 pieces:
+  // row p / 9, piece p % 9 (lanes past 144 are idle).  Rows past N re-read
+  // row N - 1 (their outputs are not stored).  K-group 0 issues DMAs 0 and
+  // 1, K-group 1 DMA 2.
   uint32_t woff[kSkWDma];
 #pragma unroll
   for (int i = 0; i < kSkWDma; i++) {
@@ -202,8 +215,9 @@ __global__ void __launch_bounds__(64 * kSkWaves) q4_0_skinny_kernel(const Skinny
   constexpr int kInvOff = 16 * kSkRowPieces * 16;  // 2304
   const int w_active = kWLast + (SPLIT ? kMh / 4 : 0);
   const bool inv_lane = SPLIT && lane >= kWLast;
-  // X DMA i of this wave covers pieces p = 64 (wave * kXDma + i) + lane of the
-  // chunk: row p / 32, slot p % 32 holding logical piece (p % 32) ^ (row & 15).
+  // X DMA i of this wave (0..7) covers pieces p = 64 (wave * kXDma + i) + lane
+  // of the chunk: row p / 32, slot p % 32 holding logical piece
+  // (p % 32) ^ (row & 15).
   uint32_t xoff[G::kXDma];
 #pragma unroll
   for (int i = 0; i < G::kXDma; i++) {
@@ -220,13 +234,16 @@ __global__ void __launch_bounds__(64 * kSkWaves) q4_0_skinny_kernel(const Skinny
 #pragma unroll
     for (int i = 0; i < G::kXDma; i++) dma16(xsrc + xoff[i], slot + (wave * G::kXDma + i) * 1024);
     const uint8_t* wsrc = a.w + (size_t)gs * kSkRowBytes;
-    uint8_t* wdst = slot + G::kXBytes + wave * kSkWBytes;
-#pragma unroll
-    for (int i = 0; i < kSkWDma - 1; i++) dma16(wsrc + woff[i], wdst + i * 1024);
-    const uint8_t* last = wsrc + woff[kSkWDma - 1];
-    if (inv_lane)
-      last = reinterpret_cast<const uint8_t*>(a.inv_s + (size_t)gs * kMh + 4 * (lane - kWLast));
-    if (lane < w_active) dma16(last, wdst + (kSkWDma - 1) * 1024);
+    uint8_t* wdst = slot + G::kXBytes + rw * kSkWBytes;
+    if (kg == 0) {
+      dma16(wsrc + woff[0], wdst);
+      dma16(wsrc + woff[1], wdst + 1024);
+    } else {
+      const uint8_t* last = wsrc + woff[kSkWDma - 1];
+      if (inv_lane)
+        last = reinterpret_cast<const uint8_t*>(a.inv_s + (size_t)gs * kMh + 4 * (lane - kWLast));
+      if (lane < w_active) dma16(last, wdst + (kSkWDma - 1) * 1024);
+    }
   };
 
   floatx4 acc[MF];
@@ -240,31 +257,35 @@ __global__ void __launch_bounds__(64 * kSkWaves) q4_0_skinny_kernel(const Skinny
     for (int f = 0; f < MF; f++) st_[f] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     floatx4(&st)[MF] = SPLIT ? st_ : acc;  // stage sums (SPLIT) or the totals
     const uint8_t* xs = smem + slot_i * G::kSlot;
-    const uint32_t* wr = reinterpret_cast<const uint32_t*>(xs + G::kXBytes + wave * kSkWBytes +
+    const uint32_t* wr = reinterpret_cast<const uint32_t*>(xs + G::kXBytes + rw * kSkWBytes +
                                                            n16 * kSkRowBytes);
-    // blocks 2 jp (byte 36 jp of the row) and 2 jp + 1 (byte 36 jp + 18)
-    uint32_t qe0[4], qe1[4], qo[4], se_bits[4], so_bits[4];
+    // this K-group's block pairs jp = 2 kg, 2 kg + 1 of the stage: blocks 2 jp
+    // (byte 36 jp of the row) and 2 jp + 1 (byte 36 jp + 18)
+    constexpr int kJp = 2;
+    uint32_t qe0[kJp], qe1[kJp], qo[kJp], se_bits[kJp], so_bits[kJp];
 #pragma unroll
-    for (int jp = 0; jp < 4; jp++) {
+    for (int jj = 0; jj < kJp; jj++) {
+      const int jp = 2 * kg + jj;
       const uint32_t* q = wr + 9 * jp;
-      qe0[jp] = q[g];
-      qe1[jp] = q[g + 1];
-      qo[jp] = q[5 + g];
-      se_bits[jp] = q[0];
-      so_bits[jp] = q[4];
+      qe0[jj] = q[g];
+      qe1[jj] = q[g + 1];
+      qo[jj] = q[5 + g];
+      se_bits[jj] = q[0];
+      so_bits[jj] = q[4];
     }
-    half8 xe[MF][4], xo[MF][4];
+    half8 xe[MF][kJp], xo[MF][kJp];
 #pragma unroll
     for (int f = 0; f < MF; f++) {
       const uint8_t* xr = xs + (16 * f + n16) * kSkXRowBytes;  // A row of this lane
 #pragma unroll
-      for (int jp = 0; jp < 4; jp++) {
-        xe[f][jp] = *reinterpret_cast<const half8*>(xr + (((8 * jp + g) ^ n16) << 4));
-        xo[f][jp] = *reinterpret_cast<const half8*>(xr + (((8 * jp + 4 + g) ^ n16) << 4));
+      for (int jj = 0; jj < kJp; jj++) {
+        const int jp = 2 * kg + jj;
+        xe[f][jj] = *reinterpret_cast<const half8*>(xr + (((8 * jp + g) ^ n16) << 4));
+        xo[f][jj] = *reinterpret_cast<const half8*>(xr + (((8 * jp + 4 + g) ^ n16) << 4));
       }
     }
 #pragma unroll
-    for (int jp = 0; jp < 4; jp++) {
+    for (int jp = 0; jp < kJp; jp++) {
       const half8 be = __builtin_bit_cast(
           half8, unpack8(__builtin_amdgcn_perm(qe1[jp], qe0[jp], 0x05040302u)));
       const half8 bo = __builtin_bit_cast(half8, unpack8(qo[jp]));
@@ -284,7 +305,7 @@ __global__ void __launch_bounds__(64 * kSkWaves) q4_0_skinny_kernel(const Skinny
     // and lo rows share one frag) were scaled by s of this stage.
     if (SPLIT) {
       const floatx4 inv = *reinterpret_cast<const floatx4*>(
-          xs + G::kXBytes + wave * kSkWBytes + kInvOff + 16 * (MF == 1 ? (g & 1) : g));
+          xs + G::kXBytes + rw * kSkWBytes + kInvOff + 16 * (MF == 1 ? (g & 1) : g));
 #pragma unroll
       for (int f = 0; f < MF; f++)
 #pragma unroll
@@ -294,11 +315,30 @@ __global__ void __launch_bounds__(64 * kSkWaves) q4_0_skinny_kernel(const Skinny
 
   for (int s = 0; s < G::kRing - 1; s++) issue(s);
   for (int s = 0; s < steps; s++) {
-    wait_reads_barrier<(G::kRing - 2) * G::kReads>();  // stage s landed, slot of s-1 free
+    // stage s landed (each wave waits for its own DMAs), slot of s-1 free
+    if (kg == 0)
+      wait_reads_barrier<(G::kRing - 2) * G::kReads0>();
+    else
+      wait_reads_barrier<(G::kRing - 2) * G::kReads1>();
     issue(s + G::kRing - 1);
     compute(s % G::kRing);
   }
-  asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // trailing DMAs landed
+  // Trailing DMAs landed and every wave is done with the ring; then K-group 1
+  // hands its sums to K-group 0 through LDS (a fixed order: deterministic).
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" : : : "memory");
+  float* red = reinterpret_cast<float*>(smem) + (size_t)rw * MF * 4 * 64 + lane;
+  if (kg == 1) {
+#pragma unroll
+    for (int f = 0; f < MF; f++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) red[(f * 4 + i) * 64] = acc[f][i];
+  }
+  __syncthreads();
+  if (kg == 1) return;
+#pragma unroll
+  for (int f = 0; f < MF; f++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[f][i] += red[(f * 4 + i) * 64];
 
   // lane holds A rows 16 f + 4 g + i of W row n
   const int n = n0 + n16;
@@ -393,7 +433,7 @@ hipError_t launch_mf(const SkinnyArgs& a, dim3 grid, hipStream_t s) {
   hipError_t e = set_lds_limit(reinterpret_cast<const void*>(q4_0_skinny_kernel<MF, SPLIT>),
                                SkGeom<MF>::kLds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((q4_0_skinny_kernel<MF, SPLIT>), grid, dim3(64 * kSkWaves), SkGeom<MF>::kLds,
+  hipLaunchKernelGGL((q4_0_skinny_kernel<MF, SPLIT>), grid, dim3(kSkThreads), SkGeom<MF>::kLds,
                      s, a);
   return hipGetLastError();
 }
