@@ -491,6 +491,189 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   }
 }
 
+// ---------------------------------------------------------------------------
+// Folded-scale GEMM on 256 x 128 tiles (q4_0_gemm_v4_kernel), for grids
+// of such tiles that fill the GPU.  The same operands, layouts and
+// arithmetic as q4_0_gemm_v3_kernel<true>, with every wave on a 64 x 64
+// sub-tile over both blocks of a stage (32 MFMAs per stage instead of 16)
+// and 256 rows of X sharing each expanded weight tile: per MFMA, half the
+// barriers, half the weight expansion (VALU and LDS writes) and half the
+// weight reads.
+//
+//  * 8 waves: wave w covers rows 64 (w >> 1) .. +63, columns 64 (w & 1) .. +63.
+//  * X: LDS DMA into a 3-slot ring of 32 KB (256 rows x 64 K), two stages
+//    ahead, four VMEM instructions per wave and stage; chunk c of row r at
+//    c ^ ((r >> 1) & 7), as in the 128-row kernel.
+//  * W: the 128-row tile's stage bytes read into registers three stages
+//    ahead (one 12-byte read per thread), unpacked and scaled one stage ahead
+//    into a 2-slot fp16 B ring.
+//  * Stage s: block 0's operands are read from LDS right after the barrier
+//    that opens the stage, block 1's during block 0's MFMAs; then stage
+//    s + 1's B tile is written, the wave waits for all but its newest five
+//    global reads (stage s + 2's X DMAs and stage s + 3's W words) and meets
+//    the work-group at the barrier.
+// ---------------------------------------------------------------------------
+constexpr int kV4BM = 256;
+constexpr int kV4XRing = 3;
+constexpr int kV4BRing = 2;
+constexpr int kV4XTile = kV4BM * kRowBytes;                   // 32 KB
+constexpr int kV4OffB = kV4XRing * kV4XTile;                  // 96 KB
+constexpr int kV4Lds = kV4OffB + kV4BRing * kTileBytes;       // 128 KB
+static_assert(kV4Lds <= 160 * 1024, "LDS budget");
+
+__global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v4_kernel(const Args a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+  const int lr = lane & 15;
+  const int lq = lane >> 4;
+
+  int tile = blockIdx.x;
+  const int ntiles = a.tiles_m * a.tiles_n;
+  if (a.xcd_map) tile = (tile & 7) * (ntiles >> 3) + (tile >> 3);
+  const int m0 = (tile % a.tiles_m) * kV4BM;
+  const int n0 = (tile / a.tiles_m) * BN;
+  const int steps = a.K / BK;
+  const size_t x_row = (size_t)a.K * 2;
+  const size_t w_row = (size_t)(a.K / 32) * 18;
+
+  // X DMA: instruction i of wave w fills rows 64 i + 8 w .. +7 (1 KB);
+  // lane -> row 64 i + 8 w + (lane >> 3), slot lane & 7 = logical chunk
+  // (lane & 7) ^ ((row >> 1) & 7) ((row >> 1) & 7 does not depend on i).
+  const int xr = 8 * wave + (lane >> 3);
+  const int xc = (lane & 7) ^ ((xr >> 1) & 7);
+  const uint8_t* xsrc = a.xh + (size_t)(m0 + xr) * x_row + xc * 16;
+  auto issue = [&](int s) {  // X DMA of stage min(s, steps-1) into the ring slot of s
+    const int sc = s < steps ? s : steps - 1;
+    uint8_t* adst = smem + (s % kV4XRing) * kV4XTile + wave * 1024;
+    const uint8_t* asrc = xsrc + (size_t)sc * kRowBytes;
+#pragma unroll
+    for (int i = 0; i < 4; i++) dma16(asrc + (size_t)(64 * i) * x_row, adst + i * 8 * 1024);
+  };
+
+  // Expansion role, as in q4_0_gemm_v3_kernel: thread -> row er, block eb of
+  // the stage, half eh of the block's nibbles.
+  const int erk = (t >> 2) & 15;
+  const int er = (t >> 6) * 16 + ((erk & 12) | ((erk & 1) << 1) | ((erk >> 1) & 1));
+  const int eb = (t >> 1) & 1, eh = t & 1;
+  const bool evalid = n0 + er < a.N;
+  const uint32_t esel = eb ? 0x07060504u : 0x05040302u;
+  const uint8_t* erow = a.w + (size_t)min(n0 + er, a.N - 1) * w_row + 16 * eb + 8 * eh;
+  const uint32_t boff0 = tile_off(er, 4 * eb + 2 * eh);
+  const uint32_t boff1 = tile_off(er, 4 * eb + 2 * eh + 1);
+  const int eexp = evalid ? a.rowexp[n0 + er] : 0;
+  using RawW = u32x3;
+  auto raw_load = [&](int s) -> RawW {
+    return global_load_w(erow + (size_t)(s < steps ? s : steps - 1) * 36);
+  };
+  auto expand = [&](int s, const RawW& r) {  // stage s's B tile into its ring slot
+    const uint32_t own = (r.x >> (eb ? 16 : 0)) & 0xFFFFu;
+    const uint32_t dbits = (uint32_t)__builtin_amdgcn_mov_dpp((int)own, 0xA0, 0xF, 0xF, false);
+    const _Float16 h = evalid ? (_Float16)ldexpf(f16_bits_to_f32(dbits), -eexp) : (_Float16)0.0f;
+    const half2v hh = {h, h};
+    const u32x4 lo = unpack8(__builtin_amdgcn_perm(r.y, r.x, esel));
+    const u32x4 hi = unpack8(__builtin_amdgcn_perm(r.z, r.y, esel));
+    u32x4 elo, ehi;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t wl = lo[i], wh = hi[i];
+      elo[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, wl) * hh);
+      ehi[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, wh) * hh);
+    }
+    uint8_t* bt = smem + kV4OffB + (s % kV4BRing) * kTileBytes;
+    *reinterpret_cast<u32x4*>(bt + boff0) = elo;
+    *reinterpret_cast<u32x4*>(bt + boff1) = ehi;
+  };
+
+  // MFMA operands of block kb of stage s.
+  auto load_ops = [&](int s, int kb, half8 (&fa)[4], half8 (&fb)[4]) {
+    const uint32_t chunk = ((4 * kb + lq) ^ ((lr >> 1) & 7)) << 4;
+    const uint8_t* xt = smem + (s % kV4XRing) * kV4XTile + (wm * 64 + lr) * kRowBytes + chunk;
+    const uint8_t* wt = smem + kV4OffB + (s % kV4BRing) * kTileBytes + (wn * 64 + lr) * kRowBytes +
+                        chunk;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      fa[i] = *reinterpret_cast<const half8*>(xt + i * 16 * kRowBytes);
+      fb[i] = *reinterpret_cast<const half8*>(wt + i * 16 * kRowBytes);
+    }
+  };
+
+  floatx4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto mma = [&](const half8 (&fa)[4], const half8 (&fb)[4]) {
+#pragma unroll
+    for (int q = 0; q < 16; q++)
+      acc[q >> 2][q & 3] =
+          __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[q >> 2], fb[q & 3], acc[q >> 2][q & 3], 0, 0, 0);
+  };
+
+  // Prologue: X of stages 0 and 1 and the W words of stages 0 and 1 landed,
+  // stage 0's B tile written, stage 2's W words in flight.
+  issue(0);
+  issue(1);
+  RawW r0 = raw_load(0), ra = raw_load(1);
+  asm volatile("s_waitcnt vmcnt(0)" : "+v"(r0), "+v"(ra) : : "memory");
+  expand(0, r0);
+  RawW rb = raw_load(2);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  // Stage s.  At its top (just past the barrier): X of s and s+1 landed, B
+  // tile of s visible, the W words of s+1 in registers (landed) and those of
+  // s+2 issued one stage earlier.
+  //  - X DMA of stage s+2 into the slot of stage s-1: every wave finished
+  //    reading stage s-1's operands before the barrier;
+  //  - operands of both blocks of s, block 0's MFMAs, stage s+1's B tile
+  //    (into the slot of s-1), block 1's MFMAs;
+  //  - the W words of s+3 into the registers just expanded;
+  //  - wait for all but this stage's five reads (so X of s+1 and the W words
+  //    of s+2 have landed; those registers pass through the statement, so
+  //    nothing reads them before it) and for the LDS writes; barrier.
+  // Unrolled by two so the W registers keep static names: a register that a
+  // read issued from asm is still filling is never copied (steps is even).
+  auto stage = [&](int s, RawW& rx) {
+    issue(s + 2);
+    half8 fa0[4], fb0[4], fa1[4], fb1[4];
+    load_ops(s, 0, fa0, fb0);
+    load_ops(s, 1, fa1, fb1);
+    mma(fa0, fb0);
+    expand(s + 1, rx);
+    mma(fa1, fb1);
+    rx = raw_load(s + 3);
+  };
+  for (int s = 0; s < steps; s += 2) {
+    stage(s, ra);
+    asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" : "+v"(rb) : : "memory");
+    stage(s + 1, rb);
+    asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" : "+v"(ra) : : "memory");
+  }
+  // The trailing reads (re-reads of the last stage) land before the
+  // work-group's LDS is released.
+  asm volatile("s_waitcnt vmcnt(0)" : "+v"(ra), "+v"(rb) : : "memory");
+
+  // Output column n scaled by D_n = 2^rowexp[n], row m by 2^xexp[m] (exact).
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int n = n0 + wn * 64 + 16 * j + lr;
+    const bool nok = n < a.N;
+    const float bv = (a.bias && nok) ? a.bias[n] : 0.0f;
+    const int en = nok ? a.rowexp[n] : 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int m = m0 + wm * 64 + 16 * i + 4 * lq + r;
+        if (nok && m < a.M)
+          a.y[(size_t)m * a.N + n] = ldexpf(acc[i][j][r], en + a.xexp[m]) + bv;
+      }
+  }
+}
+
 // Y = sum of the K-split partial planes in split order (+ bias): a fixed
 // order, so results do not depend on which work-group finished first.
 __global__ void __launch_bounds__(256)
@@ -766,6 +949,21 @@ hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const
                        dim3(256), 0, s, static_cast<u32x4*>(ws), gemm_x_exponents(ws, batch, m), x,
                        (int)batch, (int)mp, (int)m, rowexp, w, (int)n);
     if ((e = hipGetLastError()) != hipSuccess) return e;
+    // 256-row tiles when their grid alone fills three quarters of the CUs
+    // and the fp16 X rows (Mp, a multiple of 128) cover whole 256-row tiles.
+    const size_t tiles4 = (mp / kV4BM + (mp % kV4BM ? 1 : 0)) * (size_t)a.tiles_n;
+    if (mp % kV4BM == 0 && tiles4 * 4 >= (size_t)num_cus * 3) {
+      if ((e = set_lds_limit(reinterpret_cast<const void*>(q4_0_gemm_v4_kernel), kV4Lds)) !=
+          hipSuccess)
+        return e;
+      Args b = a;
+      b.tiles_m = (int)(mp / kV4BM);
+      const int t4 = b.tiles_m * b.tiles_n;
+      b.xcd_map = (t4 % 8) == 0 ? 1 : 0;
+      b.splits = 1;
+      hipLaunchKernelGGL(q4_0_gemm_v4_kernel, dim3(t4), dim3(kThreads), kV4Lds, s, b);
+      return hipGetLastError();
+    }
     hipLaunchKernelGGL(q4_0_gemm_v3_kernel<true>, dim3(tiles, a.splits), dim3(kThreads), kLdsBytes,
                        s, a);
   } else {

@@ -416,6 +416,47 @@ def test_gemm_q4_0_scale_range(torch, hk, orc, batch):
         assert err <= GEMM_TOL, (j, err)
 
 
+@pytest.mark.parametrize("batch,n,m", [(500, 12289, 1024), (512, 12300, 512)])
+def test_gemm_q4_0_256_row_tiles(torch, hk, orc, batch, n, m):
+    """Grids of 256-row tiles that fill the GPU take the 256 x 128 tile
+    kernel: an M tail inside the last tile (500 of 512 rows), an N tail (one
+    column past 96 tiles, or 12 past), a bias, and rows of extreme block
+    scales (as test_gemm_q4_0_scale_range); checked on a seeded sample of
+    columns plus the special ones against fp64."""
+    q = _q4(orc, n, m, seed=batch + 3 * n)
+    blk = q.reshape(n, m // 32, 18)
+
+    def set_d(rows, vals):
+        bits = np.asarray(vals, np.float16).view(np.uint8).reshape(-1, 2)
+        blk[rows, :, 0] = bits[:, 0]
+        blk[rows, :, 1] = bits[:, 1]
+    set_d(0, np.full(m // 32, 60000.0))
+    set_d(1, np.full(m // 32, 1e-6))
+    set_d(2, np.where(np.arange(m // 32) % 2 == 0, 1e3, 1e-3))
+    set_d(n - 1, np.full(m // 32, 65504.0))
+    x = orc.normal_f32(batch + 17, (batch, m))
+    bias = orc.normal_f32(batch + 18, n)
+    import ctypes
+    from hypno_amd import _lib
+    lib = _lib.load()
+    y = torch.empty(batch * n, dtype=torch.float32, device="cuda")
+    qg, xg, bg = _gpu(torch, q), _gpu(torch, x), _gpu(torch, bias)
+    st = lib.hypno_hip_matmul_q4_0_dev(ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(qg.data_ptr()),
+                                       q.size, ctypes.c_void_p(xg.data_ptr()),
+                                       ctypes.c_void_p(bg.data_ptr()), n, m, batch, None)
+    assert st == 0
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().reshape(batch, n)
+    rng = np.random.default_rng(n)
+    cols = np.unique(np.concatenate([[0, 1, 2, n - 1, n - 2], rng.choice(n, 300, replace=False)]))
+    w = orc.dequantize_q4_0(q).reshape(n, m)[cols].astype(np.float64)
+    ref = x.astype(np.float64) @ w.T + bias[cols].astype(np.float64)
+    assert orc.rel_l2(got[:, cols], ref) <= GEMM_TOL
+    for k, c in enumerate(cols):
+        if c < 3 or c >= n - 2:
+            assert orc.rel_l2(got[:, c], ref[:, k]) <= GEMM_TOL, c
+
+
 @pytest.mark.parametrize("m", [320, 384])
 def test_gemm_bias_and_tails(torch, hk, orc, m):
     # M and N tails with a bias; m = 320 takes the 64-column kernel, m = 384
