@@ -569,20 +569,23 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v4_kernel(const Args a)
   auto raw_load = [&](int s) -> RawW {
     return global_load_w(erow + (size_t)(s < steps ? s : steps - 1) * 36);
   };
-  auto expand = [&](int s, const RawW& r) {  // stage s's B tile into its ring slot
+  // This thread's 16 weights of a stage as fp16 (nib - 8)·(d / D_n), and
+  // their store into the stage's B ring slot.
+  auto expand_regs = [&](const RawW& r, u32x4& elo, u32x4& ehi) {
     const uint32_t own = (r.x >> (eb ? 16 : 0)) & 0xFFFFu;
     const uint32_t dbits = (uint32_t)__builtin_amdgcn_mov_dpp((int)own, 0xA0, 0xF, 0xF, false);
     const _Float16 h = evalid ? (_Float16)ldexpf(f16_bits_to_f32(dbits), -eexp) : (_Float16)0.0f;
     const half2v hh = {h, h};
     const u32x4 lo = unpack8(__builtin_amdgcn_perm(r.y, r.x, esel));
     const u32x4 hi = unpack8(__builtin_amdgcn_perm(r.z, r.y, esel));
-    u32x4 elo, ehi;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const uint32_t wl = lo[i], wh = hi[i];
       elo[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, wl) * hh);
       ehi[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, wh) * hh);
     }
+  };
+  auto expand_store = [&](int s, const u32x4& elo, const u32x4& ehi) {
     uint8_t* bt = smem + kV4OffB + (s % kV4BRing) * kTileBytes;
     *reinterpret_cast<u32x4*>(bt + boff0) = elo;
     *reinterpret_cast<u32x4*>(bt + boff1) = ehi;
@@ -619,17 +622,24 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v4_kernel(const Args a)
   issue(1);
   RawW r0 = raw_load(0), ra = raw_load(1);
   asm volatile("s_waitcnt vmcnt(0)" : "+v"(r0), "+v"(ra) : : "memory");
-  expand(0, r0);
+  {
+    u32x4 elo, ehi;
+    expand_regs(r0, elo, ehi);
+    expand_store(0, elo, ehi);
+  }
   RawW rb = raw_load(2);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
   // Stage s.  At its top (just past the barrier): X of s and s+1 landed, B
   // tile of s visible, the W words of s+1 in registers (landed) and those of
   // s+2 issued one stage earlier.
-  //  - X DMA of stage s+2 into the slot of stage s-1: every wave finished
-  //    reading stage s-1's operands before the barrier;
-  //  - operands of both blocks of s, block 0's MFMAs, stage s+1's B tile
-  //    (into the slot of s-1), block 1's MFMAs;
+  //  - operand reads of both blocks of s, with stage s+1's weights unpacked
+  //    between them (VALU work that hides the reads' latency; a scheduling
+  //    barrier keeps the MFMAs after it);
+  //  - block 0's MFMAs, then the B tile of s+1 stored (into the slot of
+  //    s-1) and the X DMA of stage s+2 issued (into the slot of s-1: every
+  //    wave finished reading stage s-1's operands before the barrier), then
+  //    block 1's MFMAs;
   //  - the W words of s+3 into the registers just expanded;
   //  - wait for all but this stage's five reads (so X of s+1 and the W words
   //    of s+2 have landed; those registers pass through the statement, so
@@ -637,12 +647,15 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v4_kernel(const Args a)
   // Unrolled by two so the W registers keep static names: a register that a
   // read issued from asm is still filling is never copied (steps is even).
   auto stage = [&](int s, RawW& rx) {
-    issue(s + 2);
     half8 fa0[4], fb0[4], fa1[4], fb1[4];
+    u32x4 elo, ehi;
     load_ops(s, 0, fa0, fb0);
+    expand_regs(rx, elo, ehi);
     load_ops(s, 1, fa1, fb1);
+    __builtin_amdgcn_sched_barrier(0);
     mma(fa0, fb0);
-    expand(s + 1, rx);
+    expand_store(s + 1, elo, ehi);
+    issue(s + 2);
     mma(fa1, fb1);
     rx = raw_load(s + 3);
   };
