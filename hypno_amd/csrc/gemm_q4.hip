@@ -53,6 +53,8 @@
 // Requirements (q4_0_gemm_v3_ok): K % 256 == 0 (rows of W start on 16-byte
 // boundaries), w 16-byte aligned, w holds N whole rows.  Rows past N read
 // row N-1 with a zero scale; rows/columns past M/N are not stored.
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace hypno {
@@ -536,7 +538,13 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v4_kernel(const Args a)
   if (a.xcd_map) tile = (tile & 7) * (ntiles >> 3) + (tile >> 3);
   const int m0 = (tile % a.tiles_m) * kV4BM;
   const int n0 = (tile / a.tiles_m) * BN;
-  const int steps = a.K / BK;
+  // This work-group's K range: stages [s0, s0 + steps) of gsteps (even
+  // bounds; the ring code runs on local stage numbers, addresses use s0 + s).
+  const int gsteps = a.K / BK;
+  const int z = blockIdx.y;
+  const int s0 = (int)((long long)gsteps * z / a.splits) & ~1;
+  const int s1 = z == a.splits - 1 ? gsteps : (int)((long long)gsteps * (z + 1) / a.splits) & ~1;
+  const int steps = s1 - s0;
   const size_t x_row = (size_t)a.K * 2;
   const size_t w_row = (size_t)(a.K / 32) * 18;
 
@@ -549,7 +557,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v4_kernel(const Args a)
   auto issue = [&](int s) {  // X DMA of stage min(s, steps-1) into the ring slot of s
     const int sc = s < steps ? s : steps - 1;
     uint8_t* adst = smem + (s % kV4XRing) * kV4XTile + wave * 1024;
-    const uint8_t* asrc = xsrc + (size_t)sc * kRowBytes;
+    const uint8_t* asrc = xsrc + (size_t)(s0 + sc) * kRowBytes;
 #pragma unroll
     for (int i = 0; i < 4; i++) dma16(asrc + (size_t)(64 * i) * x_row, adst + i * 8 * 1024);
   };
@@ -567,7 +575,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v4_kernel(const Args a)
   const int eexp = evalid ? a.rowexp[n0 + er] : 0;
   using RawW = u32x3;
   auto raw_load = [&](int s) -> RawW {
-    return global_load_w(erow + (size_t)(s < steps ? s : steps - 1) * 36);
+    return global_load_w(erow + (size_t)(s0 + (s < steps ? s : steps - 1)) * 36);
   };
   // This thread's 16 weights of a stage as fp16 (nib - 8)·(d / D_n), and
   // their store into the stage's B ring slot.
@@ -670,19 +678,22 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v4_kernel(const Args a)
   asm volatile("s_waitcnt vmcnt(0)" : "+v"(ra), "+v"(rb) : : "memory");
 
   // Output column n scaled by D_n = 2^rowexp[n], row m by 2^xexp[m] (exact).
+  // Split K: this range's sum goes to its partial plane, the bias is added
+  // by the reduction.
+  float* dst = a.splits > 1 ? a.part + (size_t)z * a.M * a.N : a.y;
+  const float* bias = a.splits > 1 ? nullptr : a.bias;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const int n = n0 + wn * 64 + 16 * j + lr;
     const bool nok = n < a.N;
-    const float bv = (a.bias && nok) ? a.bias[n] : 0.0f;
+    const float bv = (bias && nok) ? bias[n] : 0.0f;
     const int en = nok ? a.rowexp[n] : 0;
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int m = m0 + wm * 64 + 16 * i + 4 * lq + r;
-        if (nok && m < a.M)
-          a.y[(size_t)m * a.N + n] = ldexpf(acc[i][j][r], en + a.xexp[m]) + bv;
+        if (nok && m < a.M) dst[(size_t)m * a.N + n] = ldexpf(acc[i][j][r], en + a.xexp[m]) + bv;
       }
   }
 }
@@ -844,6 +855,7 @@ __global__ void __launch_bounds__(F16Geom<NW>::kThreads, 1) f16_gemm_v2_kernel(c
 constexpr int kMinSplitStages = 8;
 int pick_splits(size_t tiles, size_t m, int num_cus) {
   const size_t stages = m / BK;
+  if (tiles == 0) return 1;
   if (tiles * 4 >= (size_t)num_cus * 3) return 1;
   size_t s = (size_t)num_cus / tiles;
   if (s > stages / kMinSplitStages) s = stages / kMinSplitStages;
@@ -858,7 +870,9 @@ size_t round256(size_t v) { return (v + 255) / 256 * 256; }
 // any), then the row exponents.
 size_t gemm_v3_workspace_bytes(size_t batch, size_t n, size_t m, int num_cus) {
   const size_t tiles = ((n + BN - 1) / BN) * ((batch + BM - 1) / BM);
-  const int splits = pick_splits(tiles, m, num_cus);
+  const size_t mp = (batch + BM - 1) / BM * BM;
+  const size_t tiles4 = ((n + BN - 1) / BN) * ((mp + kV4BM - 1) / kV4BM);
+  const int splits = std::max(pick_splits(tiles, m, num_cus), pick_splits(tiles4, m, num_cus));
   const size_t xb = round256(gemm_workspace_bytes(batch, m));
   const size_t pb = splits > 1 ? round256((size_t)splits * batch * n * 4) : 0;
   return xb + pb + round256(n * 4);
@@ -962,23 +976,27 @@ hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const
                        dim3(256), 0, s, static_cast<u32x4*>(ws), gemm_x_exponents(ws, batch, m), x,
                        (int)batch, (int)mp, (int)m, rowexp, w, (int)n);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    // 256-row tiles when their grid alone fills three quarters of the CUs
-    // and the fp16 X rows (Mp, a multiple of 128) cover whole 256-row tiles.
-    const size_t tiles4 = (mp / kV4BM + (mp % kV4BM ? 1 : 0)) * (size_t)a.tiles_n;
-    if (mp % kV4BM == 0 && tiles4 * 4 >= (size_t)num_cus * 3) {
+    // 256-row tiles when the fp16 X rows (Mp, a multiple of 128) cover whole
+    // 256-row tiles, the grid (K split by the same rule) fills three
+    // quarters of the CUs, and it needs no K-split reduction that the
+    // 128-row grid would not (the reduction launch costs more than the
+    // larger tiles save on a small grid).
+    const size_t tiles4 = (mp / kV4BM) * (size_t)a.tiles_n;  // 0 when mp < 256
+    const int splits4 = tiles4 ? pick_splits(tiles4, m, num_cus) : 1;
+    if (tiles4 && mp % kV4BM == 0 && tiles4 * (size_t)splits4 * 4 >= (size_t)num_cus * 3 &&
+        (splits4 == 1 || a.splits > 1)) {
       if ((e = set_lds_limit(reinterpret_cast<const void*>(q4_0_gemm_v4_kernel), kV4Lds)) !=
           hipSuccess)
         return e;
-      Args b = a;
-      b.tiles_m = (int)(mp / kV4BM);
-      const int t4 = b.tiles_m * b.tiles_n;
-      b.xcd_map = (t4 % 8) == 0 ? 1 : 0;
-      b.splits = 1;
-      hipLaunchKernelGGL(q4_0_gemm_v4_kernel, dim3(t4), dim3(kThreads), kV4Lds, s, b);
-      return hipGetLastError();
+      a.tiles_m = (int)(mp / kV4BM);
+      a.xcd_map = (tiles4 % 8) == 0 ? 1 : 0;
+      a.splits = splits4;
+      hipLaunchKernelGGL(q4_0_gemm_v4_kernel, dim3((unsigned)tiles4, a.splits), dim3(kThreads),
+                         kV4Lds, s, a);
+    } else {
+      hipLaunchKernelGGL(q4_0_gemm_v3_kernel<true>, dim3(tiles, a.splits), dim3(kThreads),
+                         kLdsBytes, s, a);
     }
-    hipLaunchKernelGGL(q4_0_gemm_v3_kernel<true>, dim3(tiles, a.splits), dim3(kThreads), kLdsBytes,
-                       s, a);
   } else {
     if ((e = launch_x_f16_permuted(x, batch, m, ws, s)) != hipSuccess) return e;
     hipLaunchKernelGGL(q4_0_gemm_v3_kernel<false>, dim3(tiles, a.splits), dim3(kThreads),
