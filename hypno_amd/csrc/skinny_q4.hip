@@ -8,10 +8,11 @@
 //  * A work-group owns 64 rows of W and a range of K; K streams through LDS
 //    in stages of 256 (8 blocks): DMA (global_load_lds) of the stage's
 //    activation rows and W row segments into a ring of LDS slots, one
-//    barrier per stage.  Its 8 waves form 4 row groups (16 rows, one MFMA
-//    column tile each) x 2 K-groups (blocks 0-3 / 4-7 of every stage): two
-//    waves per SIMD, so one's unpacking overlaps the other's waits; at the
-//    end K-group 1 hands its sums to K-group 0 through LDS (fixed order).
+//    barrier per stage.  Its 16 waves form 4 row groups (16 rows, one MFMA
+//    column tile each) x 4 K-groups (block pair kg of every stage): four
+//    waves per SIMD, so their unpacking overlaps the others' waits; at the
+//    end K-groups 1-3 hand their sums to K-group 0 through LDS (added in
+//    K-group order: deterministic).
 //  * Lane (n, g) of a wave takes nibble quarter g of row n's block from LDS
 //    (4 bytes), turns it into exact fp16 (nib - 8) in registers and feeds
 //    v_mfma_f32_16x16x32_f16; the block's partial is scaled in fp32.
@@ -110,7 +111,7 @@ x_skinny_kernel(uint8_t* __restrict__ xa, float* __restrict__ inv_s, const float
 // multiples of 144 bytes when K % 256 == 0), so they move as nine 16-byte
 // pieces.
 constexpr int kSkWaves = 4;                    // row groups per work-group, 16 W rows each
-constexpr int kSkKGroups = 2;                  // waves per row group, half a stage's blocks each
+constexpr int kSkKGroups = 4;                  // waves per row group, a quarter of a stage's blocks each
 constexpr int kSkThreads = 64 * kSkWaves * kSkKGroups;
 constexpr int kSkRowBytes = 144;               // W bytes of one row and stage
 constexpr int kSkRowPieces = kSkRowBytes / 16;  // 9
@@ -123,18 +124,17 @@ template <int MF>
 struct SkGeom {
   static constexpr int kRows = 16 * MF;                      // A rows
   static constexpr int kXBytes = kRows * kSkXRowBytes;       // X chunk per stage
-  static constexpr int kXDma = kXBytes / 1024 / (kSkWaves * kSkKGroups);  // X DMAs per wave
+  static constexpr int kXTot = kXBytes / 1024;               // X DMAs per stage (8/16/32)
+  static constexpr int kXDma = kXTot >= 16 ? kXTot / 16 : 1;  // per issuing wave
   static constexpr int kSlot = kXBytes + kSkWaves * kSkWBytes;
   static constexpr int kRing = MF == 4 ? 3 : 4;              // stages in LDS
   static constexpr int kLds = kRing * kSlot;                 // 80 / 112 / 132 KB
-  // DMAs per wave and stage: the row group's first two W DMAs go with K-group
-  // 0, the third (16 rows' last pieces and, when split, the 1/s table) with
-  // K-group 1.
-  static constexpr int kReads0 = kXDma + 2;
-  static constexpr int kReads1 = kXDma + 1;
+  // Per wave and stage: kXDma X DMAs (waves below kXTot / kXDma) and W DMA
+  // i from K-group i of the row group (i < 3; the third carries the 16 rows'
+  // last pieces and, when split, the 1/s table).
   static_assert(kSkWDma == 3, "W DMA split between the K-groups");
   static_assert(kLds <= 160 * 1024, "LDS budget");
-  static_assert((kRing - 2) * kReads0 <= 63, "vmcnt range");
+  static_assert((kRing - 2) * (kXDma + 1) <= 63, "vmcnt range");
 };
 
 // Wait until at most N of this wave's global reads are outstanding and its
@@ -186,7 +186,8 @@ __global__ void __launch_bounds__(kSkThreads) q4_0_skinny_kernel(const SkinnyArg
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rw = wave & 3;   // row group: W rows 16 rw .. 16 rw + 15 of the tile
-  const int kg = wave >> 2;  // K-group: blocks 4 kg .. 4 kg + 3 of every stage
+  const int kg = wave >> 2;  // K-group: blocks 2 kg, 2 kg + 1 of every stage
+  const bool xact = wave * G::kXDma < G::kXTot;  // this wave DMAs X pieces
   const int n16 = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 16 * kSkWaves + 16 * rw;  // this wave's first W row
   const int gsteps = a.K / kSkStageK;
@@ -198,8 +199,8 @@ __global__ void __launch_bounds__(kSkThreads) q4_0_skinny_kernel(const SkinnyArg
 
   // W DMA i, lane -> piece p = 64 i + lane of the row group's 16 x 9 pieces:
   // row p / 9, piece p % 9 (lanes past 144 are idle).  Rows past N re-read
-  // row N - 1 (their outputs are not stored).  K-group 0 issues DMAs 0 and
-  // 1, K-group 1 DMA 2.
+  // row N - 1 (their outputs are not stored).  K-group i issues DMA i
+  // (i < 3); K-group 3 none.
   uint32_t woff[kSkWDma];
 #pragma unroll
   for (int i = 0; i < kSkWDma; i++) {
@@ -215,9 +216,9 @@ __global__ void __launch_bounds__(kSkThreads) q4_0_skinny_kernel(const SkinnyArg
   constexpr int kInvOff = 16 * kSkRowPieces * 16;  // 2304
   const int w_active = kWLast + (SPLIT ? kMh / 4 : 0);
   const bool inv_lane = SPLIT && lane >= kWLast;
-  // X DMA i of this wave (0..7) covers pieces p = 64 (wave * kXDma + i) + lane
-  // of the chunk: row p / 32, slot p % 32 holding logical piece
-  // (p % 32) ^ (row & 15).
+  // X DMA i of this wave (0..15; only waves below kXTot / kXDma issue any)
+  // covers pieces p = 64 (wave * kXDma + i) + lane of the chunk: row p / 32,
+  // slot p % 32 holding logical piece (p % 32) ^ (row & 15).
   uint32_t xoff[G::kXDma];
 #pragma unroll
   for (int i = 0; i < G::kXDma; i++) {
@@ -231,14 +232,17 @@ __global__ void __launch_bounds__(kSkThreads) q4_0_skinny_kernel(const SkinnyArg
     const int gs = s0 + (s < steps ? s : steps - 1);
     uint8_t* slot = smem + (s % G::kRing) * G::kSlot;
     const uint8_t* xsrc = a.xa + (size_t)gs * kSkXRowBytes;
+    if (xact) {
 #pragma unroll
-    for (int i = 0; i < G::kXDma; i++) dma16(xsrc + xoff[i], slot + (wave * G::kXDma + i) * 1024);
+      for (int i = 0; i < G::kXDma; i++) dma16(xsrc + xoff[i], slot + (wave * G::kXDma + i) * 1024);
+    }
     const uint8_t* wsrc = a.w + (size_t)gs * kSkRowBytes;
     uint8_t* wdst = slot + G::kXBytes + rw * kSkWBytes;
     if (kg == 0) {
       dma16(wsrc + woff[0], wdst);
+    } else if (kg == 1) {
       dma16(wsrc + woff[1], wdst + 1024);
-    } else {
+    } else if (kg == 2) {
       const uint8_t* last = wsrc + woff[kSkWDma - 1];
       if (inv_lane)
         last = reinterpret_cast<const uint8_t*>(a.inv_s + (size_t)gs * kMh + 4 * (lane - kWLast));
@@ -261,11 +265,11 @@ __global__ void __launch_bounds__(kSkThreads) q4_0_skinny_kernel(const SkinnyArg
                                                            n16 * kSkRowBytes);
     // this K-group's block pairs jp = 2 kg, 2 kg + 1 of the stage: blocks 2 jp
     // (byte 36 jp of the row) and 2 jp + 1 (byte 36 jp + 18)
-    constexpr int kJp = 2;
+    constexpr int kJp = 1;
     uint32_t qe0[kJp], qe1[kJp], qo[kJp], se_bits[kJp], so_bits[kJp];
 #pragma unroll
     for (int jj = 0; jj < kJp; jj++) {
-      const int jp = 2 * kg + jj;
+      const int jp = kg + jj;
       const uint32_t* q = wr + 9 * jp;
       qe0[jj] = q[g];
       qe1[jj] = q[g + 1];
@@ -279,7 +283,7 @@ __global__ void __launch_bounds__(kSkThreads) q4_0_skinny_kernel(const SkinnyArg
       const uint8_t* xr = xs + (16 * f + n16) * kSkXRowBytes;  // A row of this lane
 #pragma unroll
       for (int jj = 0; jj < kJp; jj++) {
-        const int jp = 2 * kg + jj;
+        const int jp = kg + jj;
         xe[f][jj] = *reinterpret_cast<const half8*>(xr + (((8 * jp + g) ^ n16) << 4));
         xo[f][jj] = *reinterpret_cast<const half8*>(xr + (((8 * jp + 4 + g) ^ n16) << 4));
       }
@@ -316,29 +320,39 @@ __global__ void __launch_bounds__(kSkThreads) q4_0_skinny_kernel(const SkinnyArg
   for (int s = 0; s < G::kRing - 1; s++) issue(s);
   for (int s = 0; s < steps; s++) {
     // stage s landed (each wave waits for its own DMAs), slot of s-1 free
-    if (kg == 0)
-      wait_reads_barrier<(G::kRing - 2) * G::kReads0>();
-    else
-      wait_reads_barrier<(G::kRing - 2) * G::kReads1>();
+    // this wave's reads per stage: X pieces (xact) + one W DMA (K-groups 0-2)
+    if (xact) {
+      if (kg < 3)
+        wait_reads_barrier<(G::kRing - 2) * (G::kXDma + 1)>();
+      else
+        wait_reads_barrier<(G::kRing - 2) * G::kXDma>();
+    } else {
+      if (kg < 3)
+        wait_reads_barrier<(G::kRing - 2) * 1>();
+      else
+        wait_reads_barrier<0>();
+    }
     issue(s + G::kRing - 1);
     compute(s % G::kRing);
   }
   // Trailing DMAs landed and every wave is done with the ring; then K-group 1
   // hands its sums to K-group 0 through LDS (a fixed order: deterministic).
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" : : : "memory");
-  float* red = reinterpret_cast<float*>(smem) + (size_t)rw * MF * 4 * 64 + lane;
-  if (kg == 1) {
+  float* red = reinterpret_cast<float*>(smem) + ((size_t)(kg * 4 + rw) * MF * 4) * 64 + lane;
+  if (kg > 0) {
 #pragma unroll
     for (int f = 0; f < MF; f++)
 #pragma unroll
       for (int i = 0; i < 4; i++) red[(f * 4 + i) * 64] = acc[f][i];
   }
   __syncthreads();
-  if (kg == 1) return;
+  if (kg > 0) return;
 #pragma unroll
-  for (int f = 0; f < MF; f++)
+  for (int g2 = 1; g2 < kSkKGroups; g2++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) acc[f][i] += red[(f * 4 + i) * 64];
+    for (int f = 0; f < MF; f++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) acc[f][i] += red[((size_t)g2 * 4 * MF * 4 + (f * 4 + i)) * 64];
 
   // lane holds A rows 16 f + 4 g + i of W row n
   const int n = n0 + n16;
