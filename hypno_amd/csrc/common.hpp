@@ -267,6 +267,8 @@ struct GemvGroupGeom {
   int S = 0;     // steps per partial-sum chunk
   int maxB = 0;  // largest B (activation staging size)
   int pro = 0;   // some job stages a prologue operand too
+  int ring = 0;  // weight steps in flight per wave (LDS ring depth)
+  size_t ring_off = 0;  // LDS offset of the weight rings
   size_t lds = 0;
 };
 
@@ -276,6 +278,7 @@ struct GemvLaunch {
   int njobs;
   int total_steps;
   int S;
+  int ring_off;  // LDS offset of the per-wave weight rings
 };
 
 // Adds a job with m columns to group g if the shared shape still fits.

@@ -108,13 +108,16 @@ hipError_t launch_q8_0_generic(float* y, const uint8_t* w, const float* x, const
 // has a block.
 //
 // The steps of all jobs form one global sequence; each work-group takes a
-// contiguous range of it (possibly spanning jobs).  A lane loads its own
-// block straight from HBM as the 20-byte window [18t & ~3, +20) (a 16-byte
-// and a 4-byte load; the 64 lanes of a wave cover one contiguous 1152-byte
-// span, so the loads coalesce), and keeps the next three steps in flight in
-// a register ring that runs across job boundaries.  A lane-dependent byte
-// permute realigns the nibble dwords (a block starts at byte 0 or 2 of its
-// window); nib ^ 8 read as a signed i4 is nib - 8, and v_dot8_i32_i4
+// contiguous range of it (possibly spanning jobs).  The 64 blocks a wave owns
+// in a step are one contiguous 1152-byte span; LDS DMA copies it into the
+// wave's own ring of two or three step slots in LDS (one 1 KB and one
+// 128-byte non-temporal piece, so every cache line is read by exactly one
+// instruction), running ahead across job boundaries, and each lane reads its
+// block back as the 20-byte window [18 lane & ~3, +20) of the span.  The
+// ring is private to the wave, so no barrier orders it: a wave waits only
+// for its own oldest DMAs.  A lane-dependent byte permute realigns the
+// nibble dwords (a block starts at byte 0 or 2 of its window); nib ^ 8 read
+// as a signed i4 is nib - 8, and v_dot8_i32_i4
 // multiplies eight of them with eight i4 digits of the block's activations
 // (the limbs below) into an exact int32 sum; the limb sums combine into one
 // fp32 value that the block scale d and the block's exponent scale.  Each
@@ -125,9 +128,9 @@ hipError_t launch_q8_0_generic(float* y, const uint8_t* w, const float* x, const
 // restaged (coalesced, through LDS with an XOR swizzle) only when the job
 // changes.
 //
-// Bounds: a matrix of whole rows is a multiple of 144 bytes, so its last
-// block starts 2 bytes past a dword boundary and its window ends exactly at
-// the end of the matrix; every other window ends inside the next block.
+// Bounds: the DMAs read through a buffer resource sized to the step's valid
+// bytes, so nothing past a job's last row is read (out-of-range dwords
+// arrive as zeros, in rows that are never written).
 // ---------------------------------------------------------------------------
 
 // Activations as exact integer limbs.  For each block of 32 activations let
@@ -157,10 +160,6 @@ struct Fmt<kFmtQ4_0> {
   static constexpr int kLimbDwords = 4;   // dwords per block per digit plane
   static constexpr int kMantBits = 18;
   static constexpr int kDigitBias = 0x88888;
-  struct Slot {  // this lane's 20-byte window of one step
-    u32x4 a;
-    uint32_t b;
-  };
 };
 template <>
 struct Fmt<kFmtQ8_0> {
@@ -169,11 +168,6 @@ struct Fmt<kFmtQ8_0> {
   static constexpr int kLimbDwords = 8;
   static constexpr int kMantBits = 22;
   static constexpr int kDigitBias = 0x808080;
-  struct Slot {  // this lane's 36-byte window of one step
-    u32x4 a;
-    u32x4 b;
-    uint32_t c;
-  };
 };
 constexpr int kBadExp = -100000;  // block with inf or NaN activations
 
@@ -204,7 +198,12 @@ static void finish_geometry(GemvGroupGeom& g) {
   const size_t digits = g.fmt == kFmtQ8_0 ? 4 * Fmt<kFmtQ8_0>::kLimbs * 8
                                           : 4 * Fmt<kFmtQ4_0>::kLimbs * 4;
   const size_t xs = (size_t)g.maxB * (digits + 4) + 4 * (size_t)g.W;
-  g.lds = xs > loop ? xs : loop;
+  g.ring_off = ((xs > loop ? xs : loop) + 15) & ~(size_t)15;
+  // Each wave's ring of weight spans (64 blocks per step) follows: three
+  // steps deep when two work-groups still share a CU, else two.
+  const size_t span = 64 * (size_t)(g.fmt == kFmtQ8_0 ? Fmt<kFmtQ8_0>::kBytes : kBlockBytes);
+  g.ring = 2 * (g.ring_off + (size_t)g.W * 3 * span) <= 160 * 1024 ? 3 : 2;
+  g.lds = g.ring_off + (size_t)g.W * g.ring * span;
 }
 
 static const size_t kMaxLds = 160 * 1024;  // gfx950 LDS per work-group
@@ -253,12 +252,34 @@ struct RingCursor {
 
 __device__ __forceinline__ int job_steps(const GemvJob& J) { return (J.n + J.rps - 1) / J.rps; }
 
+// Raw buffer resource over [base, base + bytes) for dword accesses (word 3:
+// 32-bit data format); loads at offsets past `bytes` return zeros, checked
+// per dword.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+// LDS DMA, non-temporal: 16 bytes per lane from rs at byte offset voff to
+// LDS dst + 16 * lane (dst wave-uniform).
+__device__ __forceinline__ void lds_dma16_nt(__amdgpu_buffer_rsrc_t rs, uint8_t* dst,
+                                             uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)dst, 16,
+                                           voff, 0, 0, 2);
+}
+
+// First product of a v_dot8_i32_i4 chain, in the form with an inline zero
+// accumulator (no register to clear first).
+__device__ __forceinline__ int sdot8_first(uint32_t a, uint32_t b) {
+  int r;
+  asm("v_dot8_i32_i4 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 // PRO: some job of the launch has a prologue (a separate instantiation, so
 // launches without one keep the smaller staging code and register budget).
-template <int F, bool PRO>
+template <int F, bool PRO, int R>
 __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
   using FT = Fmt<F>;
-  using Slot = typename FT::Slot;
   constexpr int kLimbs = FT::kLimbs;
   constexpr int kLD = FT::kLimbDwords;
   constexpr int kMantBits = FT::kMantBits;
@@ -299,40 +320,50 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
     j0 = lo;
   }
 
-  // Ring loads are unconditional (a lane with nothing to fetch re-reads the
-  // first bytes of a job's weights, always in bounds): a load under a
-  // branch is waited for at once, which would serialise the ring.  The job
-  // table is read only when the ring crosses into the next job.
+  // The weights stream through a ring of R step spans per wave in LDS, filled
+  // by LDS DMA: each wave owns blocks [64w, 64w + 64) of every step, i.e. the
+  // span of 64 * kBytes contiguous bytes at 64w * kBytes, fetched as whole
+  // 1 KB pieces plus one 128-byte piece (every cache line read by one
+  // instruction, non-temporal).  The DMAs go through a buffer resource whose
+  // size is the step's valid bytes (0 past the work-group's range), so a
+  // partial last step or the ring's run-out past s_end reads zeros instead
+  // of memory beyond the job; the range check is per dword and valid bytes
+  // are a multiple of 4.  The job table is read only when the ring crosses
+  // into the next job.
+  constexpr int kSpan = 64 * FT::kBytes;
+  constexpr int kFull = kSpan / 1024;        // whole 1 KB pieces per span
+  static_assert(kSpan - kFull * 1024 == 128, "span = whole KBs + 128 bytes");
+  constexpr int kDmaPerStep = kFull + 1;
+  const int lane = t & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform
+  uint8_t* ring = smem + L.ring_off + (size_t)wv * (R * kSpan);
   RingCursor pc = cursor_at(j0, s_begin);
   int pg = s_begin;  // next step the ring fetches
   const uint8_t* wsafe = pc.next;
-  // Window start inside a step: the block at byte kBytes * t, rounded down to
-  // a dword (a block starts at byte 0 or 2 of its window; the last block of
-  // a step or matrix has an odd index, so its window ends with it).
-  const uint32_t win = (uint32_t)(FT::kBytes * t) & ~3u;
-  auto issue = [&]() -> Slot {
-    const uint8_t* p = wsafe;
+  const uint32_t dma_off = (uint32_t)(wv * kSpan + 16 * lane);
+  auto issue = [&](int slot) {
+    const uint8_t* base = wsafe;
+    int nrec = 0;
     if (pg < s_end) {
       if (pg == pc.end) pc = cursor_at(pc.j + 1, pg);
-      const int vu = pg == pc.end - 1 ? pc.last_units : T;
-      if (t < vu) p = pc.next + win;
+      base = pc.next;
+      nrec = pg == pc.end - 1 ? pc.last_units * FT::kBytes : pc.bps;
       pc.next += pc.bps;
     }
     pg++;
-    Slot r;
-    if constexpr (F == kFmtQ4_0) {
-      r.a = load_global<u32x4>(p);
-      r.b = load_global<uint32_t>(p + 16);
-    } else {
-      r.a = load_global<u32x4>(p);
-      r.b = load_global<u32x4>(p + 16);
-      r.c = load_global<uint32_t>(p + 32);
-    }
-    return r;
+    const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(base, nrec);
+    uint8_t* dst = ring + slot * kSpan;
+#pragma unroll
+    for (int k = 0; k < kFull; k++) lds_dma16_nt(rs, dst + 1024 * k, dma_off + 1024 * k);
+    if (lane < 8) lds_dma16_nt(rs, dst + 1024 * kFull, dma_off + 1024 * kFull);
   };
-  Slot ring0 = issue();  // ring0 holds steps s_begin, s_begin+3, ...
-  Slot ring1 = issue();
-  Slot ring2 = issue();
+  // Window start inside a wave's span: the lane's block at byte kBytes *
+  // lane, rounded down to a dword (a block starts at byte 0 or 2 of its
+  // window; the span's last block has an odd lane, so its window ends with
+  // the span).
+  const uint32_t win = (uint32_t)(FT::kBytes * lane) & ~3u;
+#pragma unroll
+  for (int k = 0; k < R; k++) issue(k);
 
   // Byte selectors for v_perm_b32: a block starts at byte 0 (t even) or 2
   // (t odd) of its window; weight dword j is bytes [2+4j, 6+4j) of the block.
@@ -343,14 +374,12 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
   // [S][T/8] sums of 8-lane groups (a row of B blocks is B/8 whole groups
   // because B % 8 == 0); aliases the activation staging area.
   float* part = reinterpret_cast<float*>(smem);
-  const int T8 = T >> 3;
+  const int T8 = __builtin_amdgcn_readfirstlane(T >> 3);
 
   // State of the job being computed (work-group uniform except the limbs).
   GemvJob J = get(j0);
   int cj = j0;
   int seg_end = s_begin;  // end of this work-group's steps of job cj
-  int job_last = 0;       // the job's last global step
-  int last_units = 0;     // blocks in that step
   int c0 = s_begin;       // first step of the open partial-sum chunk
   u32x4 xl[kLimbs * kLD / 4];  // this lane's block column of x as digit planes
   int xe = 0;           // its exponent: x = 2^xe * sum_k base^k * digit_k
@@ -361,7 +390,7 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
   // and 8-byte aligned when B8 is even (T8 is a multiple of 8), so the reads
   // are vectorised with independent partial sums.  The bias branch is
   // uniform and kept apart: a bias load waited for in the common path would
-  // also wait for every ring load in flight.
+  // also wait for every ring DMA in flight.
   auto row_sum = [&](const float* pr, int B8) -> float {
     if ((B8 & 3) == 0) {
       float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
@@ -419,8 +448,6 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
     J = get(j);
     cj = j;
     const int steps = job_steps(J);
-    job_last = J.step0 + steps - 1;
-    last_units = (J.n - (steps - 1) * J.rps) * J.B;
     seg_end = min(s_end, J.step0 + steps);
     c0 = g;
     const int B = J.B;
@@ -530,10 +557,10 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
     __syncthreads();  // the activation region becomes partial space
   };
 
-  // One step: close the chunk / switch job when due (uniform branches),
-  // refill the ring slot with the step three ahead (returned), decode this
-  // lane's block and park its 8-lane group sum.
-  auto step = [&](int ss, const Slot sl) -> Slot {
+  // One step: close the chunk / switch job when due (uniform branches), read
+  // this lane's window from the step's slot, refill the slot with the step R
+  // ahead, decode the block and park its 8-lane group sum.
+  auto step = [&](int ss, int slot) {
     if (ss == seg_end) {
       flush(ss);
       enter(cj + 1, ss);
@@ -541,37 +568,38 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
       flush(ss);
       c0 = ss;
     }
-    const Slot next = issue();
-    const int vu = ss == job_last ? last_units : T;
-    float partial = 0.0f;
-    if (t < vu) {
+    // This slot's DMAs are the oldest of the R steps in flight (vector memory
+    // operations complete in order; any younger load only makes the wait
+    // longer).  Its window goes to registers, then the slot is refilled.
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"((R - 1) * kDmaPerStep) : "memory");
+    const uint32_t* wp = reinterpret_cast<const uint32_t*>(ring + slot * kSpan + win);
+    uint32_t d[FT::kBytes / 4 + 1];
+#pragma unroll
+    for (int k = 0; k < FT::kBytes / 4 + 1; k++) d[k] = wp[k];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot is read out
+    issue(slot);
+    float partial;
+    {
       if constexpr (F == kFmtQ4_0) {
-        const uint32_t d[5] = {sl.a.x, sl.a.y, sl.a.z, sl.a.w, sl.b};
         const float scale = f16_bits_to_f32(d[0] >> sh_d);
-        // D_l = sum_i (nib_i - 8) * digit_l(x_i): nib ^ 8 read as signed i4
-        // is nib - 8; eight products per v_dot8_i32_i4, exact in int32.
-        int acc[kLimbs] = {};
+        int acc[kLimbs];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
           const uint32_t q = __builtin_amdgcn_perm(d[j + 1], d[j], sel_q) ^ 0x88888888u;
 #pragma unroll
           for (int l = 0; l < kLimbs; l++)
-            acc[l] = __builtin_amdgcn_sdot8((int)q, (int)xl[l][j], acc[l], false);
+            acc[l] = j == 0 ? sdot8_first(q, xl[l][0])
+                            : __builtin_amdgcn_sdot8((int)q, (int)xl[l][j], acc[l], false);
         }
-        // sum_l 16^l * D_l: the top four limbs in int32 (|h| < 2^24, so the
-        // conversion to fp32 is exact), the last step in fp32.
+        // sum_l 16^l * D_l, exact in int32 (|sum| < 2^28), as a chain of
+        // shift-adds (one instruction per limb), then one rounding to fp32.
         int h = acc[kLimbs - 1];
 #pragma unroll
-        for (int l = kLimbs - 2; l >= 1; l--) h = (h << 4) + acc[l];
-        const float r = fmaf((float)h, 16.0f, (float)acc[0]);
-        partial = ldexpf(scale * r, xe) + xnan;
+        for (int l = kLimbs - 2; l >= 0; l--)
+          asm("v_lshl_add_u32 %0, %1, 4, %2" : "=v"(h) : "v"(h), "v"(acc[l]));
+        partial = ldexpf(scale * (float)h, xe) + xnan;
       } else {
-        const uint32_t d[9] = {sl.a.x, sl.a.y, sl.a.z, sl.a.w, sl.b.x,
-                               sl.b.y, sl.b.z, sl.b.w, sl.c};
         const float scale = f16_bits_to_f32(d[0] >> sh_d);
-        // D_l = sum_i (u_i - 128) * digit_l(x_i): u ^ 0x80 read as i8 is
-        // u - 128; four products per v_dot4_i32_i8, exact in int32
-        // (|D_l| <= 32 * 128 * 128).
         int acc[kLimbs] = {};
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -581,8 +609,6 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
             acc[l] = __builtin_amdgcn_sdot4((int)q, (int)xl[2 * l + (j >> 2)][j & 3], acc[l],
                                             false);
         }
-        // 65536 D_2 + 256 D_1 + D_0: the top two in int32 (|h| < 2^28), the
-        // rest in fp32 (a relative rounding of 2^-24 on the block sum).
         const int h = acc[2] * 256 + acc[1];
         const float r = fmaf((float)h, 256.0f, (float)acc[0]);
         partial = ldexpf(scale * r, xe) + xnan;
@@ -590,32 +616,31 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
     }
     partial = group8_sum(partial);
     if ((t & 7) == 7) part[(ss - c0) * T8 + (t >> 3)] = partial;
-    return next;
   };
 
   enter(j0, s_begin);
-  int ss = s_begin;
-  for (;;) {  // unrolled by the ring depth so every slot index is static
-    ring0 = step(ss, ring0);
-    if (++ss == s_end) break;
-    ring1 = step(ss, ring1);
-    if (++ss == s_end) break;
-    ring2 = step(ss, ring2);
-    if (++ss == s_end) break;
+  int slot = 0;
+  for (int ss = s_begin; ss < s_end; ss++) {
+    step(ss, slot);
+    slot = slot + 1 == R ? 0 : slot + 1;
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the ring's run-out DMAs
   flush(s_end);
 }
 
+template <int R>
 __global__ void __launch_bounds__(1024) q4_0_gemv_jobs_kernel(GemvLaunch L) {
-  gemv_jobs_body<kFmtQ4_0, false>(L);
+  gemv_jobs_body<kFmtQ4_0, false, R>(L);
 }
 
+template <int R>
 __global__ void __launch_bounds__(1024) q4_0_gemv_jobs_pro_kernel(GemvLaunch L) {
-  gemv_jobs_body<kFmtQ4_0, true>(L);
+  gemv_jobs_body<kFmtQ4_0, true, R>(L);
 }
 
+template <int R>
 __global__ void __launch_bounds__(1024) q8_0_gemv_jobs_kernel(GemvLaunch L) {
-  gemv_jobs_body<kFmtQ8_0, false>(L);
+  gemv_jobs_body<kFmtQ8_0, false, R>(L);
 }
 
 hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
@@ -623,9 +648,14 @@ hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
                                   hipStream_t s) {
   const bool q8 = g.fmt == kFmtQ8_0;
   const int which = q8 ? 2 : (g.pro ? 1 : 0);
-  const void* kern = which == 2   ? reinterpret_cast<const void*>(q8_0_gemv_jobs_kernel)
-                     : which == 1 ? reinterpret_cast<const void*>(q4_0_gemv_jobs_pro_kernel)
-                                  : reinterpret_cast<const void*>(q4_0_gemv_jobs_kernel);
+  const bool r3 = g.ring == 3;
+  const void* kern =
+      which == 2 ? (r3 ? reinterpret_cast<const void*>(q8_0_gemv_jobs_kernel<3>)
+                       : reinterpret_cast<const void*>(q8_0_gemv_jobs_kernel<2>))
+      : which == 1 ? (r3 ? reinterpret_cast<const void*>(q4_0_gemv_jobs_pro_kernel<3>)
+                         : reinterpret_cast<const void*>(q4_0_gemv_jobs_pro_kernel<2>))
+                   : (r3 ? reinterpret_cast<const void*>(q4_0_gemv_jobs_kernel<3>)
+                         : reinterpret_cast<const void*>(q4_0_gemv_jobs_kernel<2>));
   {
     hipError_t e = set_lds_limit(kern, (int)kMaxLds);
     if (e != hipSuccess) return e;
@@ -658,12 +688,9 @@ hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
   L.njobs = njobs;
   L.total_steps = total_steps;
   L.S = g.S;
-  if (which == 2)
-    hipLaunchKernelGGL(q8_0_gemv_jobs_kernel, dim3(grid), dim3(g.T), g.lds, s, L);
-  else if (which == 1)
-    hipLaunchKernelGGL(q4_0_gemv_jobs_pro_kernel, dim3(grid), dim3(g.T), g.lds, s, L);
-  else
-    hipLaunchKernelGGL(q4_0_gemv_jobs_kernel, dim3(grid), dim3(g.T), g.lds, s, L);
+  L.ring_off = (int)g.ring_off;
+  hipLaunchKernelGGL(reinterpret_cast<void (*)(GemvLaunch)>(const_cast<void*>(kern)), dim3(grid),
+                     dim3(g.T), g.lds, s, L);
   return hipGetLastError();
 }
 
