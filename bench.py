@@ -220,29 +220,46 @@ def time_graph(torch, fn, steps, warmup):
     return e0.elapsed_time(e1) / steps, g
 
 
-def time_launches(torch, fn, steps, warmup):
+def time_launches(torch, fn, steps, warmup, per_launch=False):
     """Back-to-back calls of `fn` (one kernel launch each) on the current
-    stream: an event before every launch and after the last, all on that
-    stream.  Returns (average ms over the timed region, per-launch ms)."""
+    stream, timed by one event before the first launch and one after the
+    last.  With per_launch, a second pass of `steps` launches follows the
+    timed region with an event after every launch, for the launch-to-launch
+    profile; an event between two launches leaves the GPU idle for ~6 us
+    (the next kernel starts only after the marker), so that pass is not used
+    for the average.  Returns (average ms over the timed region, per-launch
+    ms of the second pass or None)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    if not per_launch:
+        return ms, None
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     ev[0].record()
     for i in range(steps):
         fn()
         ev[i + 1].record()
     torch.cuda.synchronize()
-    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
-    return ev[0].elapsed_time(ev[steps]) / steps, per
+    return ms, [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
 
 
 def launch_stats(per_ms, bytes_per_launch):
+    """Launch-to-launch profile of the pass after the timed region."""
     k = max(1, min(5, len(per_ms) // 4))
     first, last = per_ms[:k], per_ms[-k:]
     us = lambda v: round(v * 1e3, 2)  # noqa: E731
     gbs = lambda ms: round(bytes_per_launch / (ms * 1e-3) / 1e9, 1)  # noqa: E731
-    return {"launches": len(per_ms), "median_us": us(statistics.median(per_ms)),
+    return {"pass": "after the timed region, an event after every launch (each adds ~6 us of "
+                    "GPU idle between launches)",
+            "launches": len(per_ms), "median_us": us(statistics.median(per_ms)),
             "min_us": us(min(per_ms)), "max_us": us(max(per_ms)),
             f"burst_first{k}_us": us(sum(first) / k), f"sustained_last{k}_us": us(sum(last) / k),
             f"burst_first{k}_gbs": gbs(sum(first) / k),
@@ -288,7 +305,7 @@ def mistral_stream(torch, lib, steps, warmup):
     arena, offs, xs, jobs = build_stream(torch, lib, MISTRAL, MISTRAL_LAYERS, seed=11)
     plan = plan_of(hk, arena, jobs)
     wb = sum(nb for _, nb in offs)
-    ms, per = time_launches(torch, plan.run, steps, warmup)
+    ms, per = time_launches(torch, plan.run, steps, warmup, per_launch=True)
     for _, _, y, *_ in jobs:
         y.fill_(float("nan"))
     plan.run()
@@ -320,7 +337,7 @@ def tinyllama_stream(torch, lib, steps, warmup):
             y.fill_(float("nan"))
 
     plan = plan_of(hk, arena, jobs)
-    ms, per = time_launches(torch, plan.run, steps, warmup)
+    ms, per = time_launches(torch, plan.run, steps, warmup, per_launch=True)
     reset()
     plan.run()
     torch.cuda.synchronize()
@@ -1109,8 +1126,7 @@ def main():
     print(f"[bench] decode stream {d['ms']:.4f} ms/step, {value:.1f} GB/s, checked "
           f"{d['check']['checked']}", file=sys.stderr, flush=True)
     # One kernel launch per step: the launch's average duration over the timed
-    # region is the step time (it includes the gap between back-to-back
-    # launches, a few microseconds).
+    # region is the step time (back-to-back launches, no event between them).
     launch_ms = d["ms"] / d["launches"]
     achieved = wb / d["launches"] / (launch_ms * 1e-3) / 1e9
     n_mats = len(d["jobs"])
