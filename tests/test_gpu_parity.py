@@ -323,6 +323,47 @@ def test_gemv_plan_mixed_jobs(torch, hk, orc):
     plan.close()
 
 
+def test_gemv_plan_many_small_jobs(torch, hk, orc):
+    """The streaming kernel's per-wave LDS rings run two or three steps ahead
+    across job boundaries: 40 jobs of 1-100 rows (one or two steps each,
+    most with a partial last step) so that a ring slot often belongs to a
+    later job than the step being computed, and work-groups whose range is
+    shorter than the ring (the run-out reads nothing)."""
+    rng = np.random.default_rng(71)
+    jobs, refs = [], []
+    for i in range(40):
+        m = int(rng.choice([256, 512]))
+        n = int(rng.choice([1, 3, 17, 64, 100]))
+        q = _q4(orc, n, m, seed=1000 + i)
+        x = orc.normal_f32(1100 + i, m)
+        bias = orc.normal_f32(1200 + i, n) if i % 5 == 0 else None
+        y = torch.full((n,), float("nan"), device="cuda")
+        jobs.append((y, _gpu(torch, q), _gpu(torch, x),
+                     None if bias is None else _gpu(torch, bias), n, m))
+        refs.append(orc.matmul_q4_0(q, x, bias, n, m))
+    plan = hk.GemvPlan(jobs)
+    assert plan.launches == 1
+    for rep in range(2):
+        for j in jobs:
+            j[0].fill_(float("nan"))
+        plan.run()
+        torch.cuda.synchronize()
+        for i, ((y, *_), ref) in enumerate(zip(jobs, refs)):
+            assert orc.normwise_err(y.cpu().numpy(), ref) <= GEMV_TOL, (rep, i)
+    plan.close()
+
+
+@pytest.mark.parametrize("n,m", [(40, 32768), (300, 16384)])
+def test_gemv_longest_rows(torch, hk, orc, n, m):
+    """K = 32768 (1024-thread work-groups, 16 per-wave rings beside 86 KB of
+    activation staging) and K = 16384, with partial last steps."""
+    q = _q4(orc, n, m, seed=n + m)
+    x = orc.normal_f32(m + 3, m)
+    got = _run_q4(torch, hk, _gpu(torch, q), _gpu(torch, x), None, n, m)
+    assert orc.normwise_err(got, orc.matmul_q4_0(q, x, None, n, m)) <= GEMV_TOL
+    assert orc.normwise_err(got, orc.matmul_q4_0_f64(q, x, None, n, m)) <= GEMV_TOL
+
+
 def test_gemv_plan_mistral_layer_in_graph(torch, hk, orc):
     # Mistral-7B layer shapes (m = 4096 and 14336 share T = 448), captured in a
     # HIP graph and replayed with fresh activations written in place
