@@ -426,13 +426,39 @@ __device__ __forceinline__ void load_run(float4 (&v)[kRunV], const float4* c4, i
 
 // -0.0 + x(0) + x(1) + ... in index order, fp32 (Iterator::sum); every thread
 // gets the result.
+// Stages x(b0 + j), j < len (1 <= len <= kChunk), into sh.chunk: each
+// thread's kChunk / kST values are all read before any is stored, so the
+// reads are in flight together (a loop that stores each value as it arrives
+// waits for the reads one at a time).  Positions past len evaluate x at the
+// last position (in bounds, unconditionally, so no read sits in a branch)
+// and are not stored.  Returns whether any staged value was not >= 0
+// (negative or NaN).
+template <typename X>
+__device__ __forceinline__ int stage_chunk(X x, int b0, int len, SampleShared& sh) {
+  const int t = threadIdx.x;
+  constexpr int kPer = kChunk / kST;
+  float v[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; u++) v[u] = x(b0 + min(t + u * kST, len - 1));
+  int odd = 0;
+#pragma unroll
+  for (int u = 0; u < kPer; u++) {
+    const int j = t + u * kST;
+    if (j < len) {
+      sh.chunk[j] = v[u];
+      odd |= !(v[u] >= 0.0f);
+    }
+  }
+  return odd;
+}
+
 template <typename X>
 __device__ float seq_sum(int cnt, X x, SampleShared& sh) {
   const int t = threadIdx.x;
   float s = -0.0f;
   for (int b0 = 0; b0 < cnt; b0 += kChunk) {
     const int len = min(kChunk, cnt - b0);
-    for (int j = t; j < len; j += kST) sh.chunk[j] = x(b0 + j);
+    stage_chunk(x, b0, len, sh);
     __syncthreads();
     if (t == 0) {
       const float4* c4 = reinterpret_cast<const float4*>(sh.chunk);
@@ -482,12 +508,7 @@ __device__ int seq_cross(int cnt, Q q, float thr, SampleShared& sh) {
   float cum = 0.0f;
   for (int b0 = 0; b0 < cnt; b0 += kChunk) {
     const int len = min(kChunk, cnt - b0);
-    int odd = 0;
-    for (int j = t; j < len; j += kST) {
-      const float v = q(b0 + j);
-      sh.chunk[j] = v;
-      odd |= !(v >= 0.0f);
-    }
+    const int odd = stage_chunk(q, b0, len, sh);
     const bool mono = __syncthreads_or(odd) == 0;
     if (t == 0) {
       const float4* c4 = reinterpret_cast<const float4*>(sh.chunk);
@@ -612,12 +633,43 @@ __global__ void __launch_bounds__(kST) sample_token_kernel(const SampleArgs a) {
   const int C = (int)sh.u[2];
   uint32_t* cidx = use_k ? a.k0 : a.a_idx;
   float* cval = use_k ? reinterpret_cast<float*>(a.k1) : a.a_val;
-  for (int g = 0; g < a.parts; g++) {
-    const int lo = (int)((long long)n * g / a.parts);
-    const int off = (int)sh.cnt[0][g], c = a.seg_cnt[g];
-    for (int j = t; j < c; j += kST) {
-      cidx[off + j] = a.seg_idx[lo + j];
-      cval[off + j] = a.seg_val[lo + j];
+  // Element i of the concatenation is element i - off[g] of range g, g the
+  // last range with off[g] <= i (a binary search over the range offsets);
+  // each thread reads kPer elements before storing any, so the reads are in
+  // flight together.
+  {
+    constexpr int kPer = 8;
+    auto range_of = [&](int i) {
+      int lo = 0, hi = a.parts - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if ((int)sh.cnt[0][mid] <= i)
+          lo = mid;
+        else
+          hi = mid - 1;
+      }
+      return lo;
+    };
+    for (int base = 0; base < C; base += kPer * kST) {
+      uint32_t vi[kPer];
+      float vv[kPer];
+      int dst[kPer];
+#pragma unroll
+      for (int u = 0; u < kPer; u++) {
+        const int i = min(base + u * kST + t, C - 1);
+        const int g = range_of(i);
+        const int src = (int)((long long)n * g / a.parts) + (i - (int)sh.cnt[0][g]);
+        vi[u] = a.seg_idx[src];
+        vv[u] = a.seg_val[src];
+        dst[u] = base + u * kST + t;
+      }
+#pragma unroll
+      for (int u = 0; u < kPer; u++) {
+        if (dst[u] < C) {
+          cidx[dst[u]] = vi[u];
+          cval[dst[u]] = vv[u];
+        }
+      }
     }
   }
   __syncthreads();
