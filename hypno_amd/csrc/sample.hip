@@ -166,6 +166,11 @@ struct SampleShared {
   int ired[kSW];
   uint32_t u[4];
   float f[4];
+  alignas(16) uint32_t acc_w[kSW];  // exact accumulation: per-wave increment totals
+  alignas(16) int acc_ev[kSW];      // ... per-wave first event
+  alignas(16) int acc_hit[kSW];     // ... per-wave first running sum above thr
+  int acc_i[4];    // sequential batch: -, first sum above thr, next position; hit flag
+  uint32_t acc_s;  // the running sum's bit pattern
 };
 
 // In the histogram hist[0..nbins), bins counted from the top: the bin holding
@@ -410,158 +415,311 @@ __device__ uint32_t kth_largest_key(int cnt, Key key, uint32_t kk, SampleShared&
   return (pre << 10) | b3;
 }
 
-// The reference's sequential fp32 loops run on thread 0 over values the whole
-// work-group stages in LDS, kChunk at a time.  The values themselves (the
-// quotients p / S of the walks) are computed by the staging threads: only the
-// dependent additions stay serial.  Thread 0 reads the next run of kRun
-// staged values while it adds the current one (two register buffers in
-// turn), so the LDS latency hides behind the additions.
-constexpr int kRun = 32;
-constexpr int kRunV = kRun / 4;  // float4 per run
+// The reference's sequential fp32 loops (s = s + v in index order) are
+// reproduced exactly, but mostly in parallel.  While s is finite and not
+// negative, every float32 at or above s in its binade is m u for an integer
+// m < 2^24 with u = 2^(E - 150), E = max(exponent field of s, 1); for v >= 0
+// finite, s + v = (m + v/u) u, so fl(s + v) = (m + d) u with d = v/u rounded
+// to the nearest integer -- as long as v/u is not exactly halfway between
+// two integers (then the tie goes to the even m + d, which depends on m) and
+// m + d < 2^24 (else the sum leaves the binade).  d comes from the bit
+// patterns by integer shifts, exactly (no division, no subnormal flushing).
+// So over a run of such values the running sums are m + prefix sums of the
+// d: the work-group computes them with a scan, finds the first value that is
+// an event (a tie, a crossing of 2^24, a negative, infinite or NaN value)
+// and, for a walk, the first running sum above thr, takes the sums up to
+// the event, and adds the event value with one float32 addition on thread
+// 0, as the reference does.  Events are rare (a binade crossing each time
+// the sum doubles, exact ties); when they come densely, or s itself is
+// negative, infinite or NaN (or -0), thread 0 adds the next values one at a
+// time.  The values are staged in LDS by the whole work-group, kChunk at a
+// time; the quotients p / S of the walks are computed by the staging
+// threads.
 
-__device__ __forceinline__ void load_run(float4 (&v)[kRunV], const float4* c4, int r) {
-#pragma unroll
-  for (int u = 0; u < kRunV; u++) v[u] = c4[r * kRunV + u];
-}
-
-// -0.0 + x(0) + x(1) + ... in index order, fp32 (Iterator::sum); every thread
-// gets the result.
 // Stages x(b0 + j), j < len (1 <= len <= kChunk), into sh.chunk: each
 // thread's kChunk / kST values are all read before any is stored, so the
 // reads are in flight together (a loop that stores each value as it arrives
 // waits for the reads one at a time).  Positions past len evaluate x at the
 // last position (in bounds, unconditionally, so no read sits in a branch)
-// and are not stored.  Returns whether any staged value was not >= 0
-// (negative or NaN).
+// and are not stored.
 template <typename X>
-__device__ __forceinline__ int stage_chunk(X x, int b0, int len, SampleShared& sh) {
+__device__ __forceinline__ void stage_chunk(X x, int b0, int len, SampleShared& sh) {
   const int t = threadIdx.x;
   constexpr int kPer = kChunk / kST;
   float v[kPer];
 #pragma unroll
   for (int u = 0; u < kPer; u++) v[u] = x(b0 + min(t + u * kST, len - 1));
-  int odd = 0;
 #pragma unroll
   for (int u = 0; u < kPer; u++) {
     const int j = t + u * kST;
-    if (j < len) {
-      sh.chunk[j] = v[u];
-      odd |= !(v[u] >= 0.0f);
-    }
+    if (j < len) sh.chunk[j] = v[u];
   }
-  return odd;
 }
 
+constexpr int kAccMinAdv = 32;  // a parallel pass advancing less: go one by one
+constexpr int kAccSeq = 256;    // values thread 0 adds one by one then
+constexpr int kRun = 32;        // ... read kRun at a time
+constexpr int kAccPer = 8;      // consecutive values per thread in a parallel pass
+static_assert(kAccPer * kST == kChunk, "a parallel pass covers a chunk");
+constexpr uint32_t kTwo24 = 1u << 24;
+
+__device__ __forceinline__ uint32_t usat_add(uint32_t a, uint32_t b) {
+  return __builtin_elementwise_add_sat(a, b);
+}
+
+// d = v / u rounded to the nearest integer for v >= +0 finite, on the grid
+// u = 2^(E - 150) of exponent field E >= 1, with sc = 150 - E: v 2^sc is
+// exact (a power-of-two scaling; an overflow to inf only where v / u >=
+// 2^24, a result below 2^-126 only where v / u < 1/2: d = 0 either way); d
+// >= 2^24 is returned as 2^24 (the sum leaves the binade whatever m is).
+// tie: v / u is exactly halfway between two integers.
+__device__ __forceinline__ uint32_t acc_increment(float v, int sc, bool& tie) {
+  const float q = ldexpf(v, sc);
+  tie = __builtin_amdgcn_fractf(q) == 0.5f;
+  return q >= 16777216.0f ? kTwo24 : (uint32_t)__builtin_rintf(q);
+}
+
+// Inclusive scan of x over the wave (lane order), saturating at 2^32 - 1:
+// sums over 1, 2, 4, 8 lanes within each row of 16, then each row takes the
+// previous rows' total (row_bcast:15, row_bcast:31).
+__device__ __forceinline__ uint32_t wave_scan_sat(uint32_t x) {
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false));
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false));
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false));
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false));
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false));
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false));
+  return x;
+}
+
+// Bit pattern of m u on the grid of exponent field E (m < 2^24; m < 2^23
+// only with E = 1, the subnormal range).
+__device__ __forceinline__ uint32_t acc_bits(int E, uint32_t m) {
+  return ((uint32_t)(E - 1) << 23) + m;
+}
+
+// s = s + sh.chunk[j] for j = 0 .. len-1 in order, float32, exactly as the
+// sequential loop; with WALK, stops after the first j at which s > thr and
+// returns that j (else -1).  s, thr and adv are the same in every thread;
+// adv, carried from chunk to chunk, is how far the last parallel pass got
+// (below kAccMinAdv, as at the start, thread 0 adds the next values one at
+// a time).
+template <bool WALK>
+__device__ int acc_chunk(int len, float& s, float thr, int& adv, SampleShared& sh) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  int pos = 0;
+  while (pos < len) {
+    const uint32_t sb = __float_as_uint(s);
+    const bool regular = (sb >> 31) == 0 && (sb >> 23) != 255u;  // +0 <= s < inf
+    if (!regular || adv < kAccMinAdv) {
+      // thread 0 adds the next values one at a time
+      if (t == 0) {
+        const int stop = min(len, pos + (regular ? kAccSeq : 64));
+        int hit = -1, j = pos;
+        float c = s;
+        // runs of kRun values: the run's reads are all issued before its
+        // additions; the first sum above thr is noted, the run finished
+        for (; j + kRun <= stop && hit < 0; j += kRun) {
+          float v[kRun];
+#pragma unroll
+          for (int u = 0; u < kRun; u++) v[u] = sh.chunk[j + u];
+#pragma unroll
+          for (int u = 0; u < kRun; u++) {
+            c += v[u];
+            if (WALK && hit < 0 && c > thr) hit = j + u;
+          }
+        }
+        for (; j < stop && hit < 0; j++) {
+          c += sh.chunk[j];
+          if (WALK && c > thr) hit = j;
+        }
+        sh.acc_s = __float_as_uint(c);
+        sh.acc_i[1] = hit;
+        sh.acc_i[2] = j;
+      }
+      __syncthreads();
+      s = __uint_as_float(sh.acc_s);
+      const int hit = sh.acc_i[1];
+      pos = sh.acc_i[2];
+      __syncthreads();
+      if (WALK && hit >= 0) return hit;
+      adv = kAccMinAdv;
+      if (s != s) return WALK ? -2 : -1;  // NaN: every later sum is NaN
+      continue;
+    }
+    // Parallel pass over [pos, len): thread t takes the kAccPer values from
+    // a0 + kAccPer t (a0 = pos rounded down to a multiple of kAccPer; values
+    // outside [pos, len) count as 0).
+    const int E = max((int)(sb >> 23), 1);
+    const int sc = 150 - E;
+    const uint32_t m0 = ((sb >> 23) ? 0x800000u : 0u) | (sb & 0x7FFFFFu);
+    const int a0 = pos & ~(kAccPer - 1);
+    const int lo = a0 + kAccPer * t;
+    float v[kAccPer];
+    if (lo < len) {  // in bounds: lo + kAccPer <= kChunk
+      const float4* c4 = reinterpret_cast<const float4*>(sh.chunk + lo);
+#pragma unroll
+      for (int q = 0; q < kAccPer / 4; q++) {
+        const float4 f = c4[q];
+        v[4 * q] = f.x;
+        v[4 * q + 1] = f.y;
+        v[4 * q + 2] = f.z;
+        v[4 * q + 3] = f.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < kAccPer; e++) v[e] = 0.0f;
+    }
+    uint32_t d[kAccPer];
+    bool ev[kAccPer];
+    bool any_ev = false;
+    uint32_t tot = 0;
+#pragma unroll
+    for (int e = 0; e < kAccPer; e++) {
+      const int j = lo + e;
+      const bool in = j >= pos && j < len;
+      bool tie;
+      const uint32_t de = acc_increment(v[e], sc, tie);
+      // negative (or -0), infinite or NaN values, and ties, are events
+      const bool odd = __builtin_isinf(v[e]) || __builtin_isnan(v[e]) || __builtin_signbit(v[e]);
+      ev[e] = in && (odd || tie);
+      d[e] = in && !ev[e] ? de : 0u;
+      tot += d[e];  // <= 8 2^24
+      any_ev = any_ev || ev[e];
+    }
+    const uint32_t inc = wave_scan_sat(tot);
+    if (lane == 63) sh.acc_w[w] = inc;
+    __syncthreads();
+    // the waves before this one: their totals, read four at a time
+    uint32_t woff = 0;
+    const uint4* w4 = reinterpret_cast<const uint4*>(sh.acc_w);
+#pragma unroll
+    for (int q = 0; q < kSW / 4; q++) {
+      const uint4 x = w4[q];
+      woff = usat_add(woff, 4 * q < w ? x.x : 0u);
+      woff = usat_add(woff, 4 * q + 1 < w ? x.y : 0u);
+      woff = usat_add(woff, 4 * q + 2 < w ? x.z : 0u);
+      woff = usat_add(woff, 4 * q + 3 < w ? x.w : 0u);
+    }
+    // this thread's running sums (exact while below 2^24): its first event
+    // (an event value, or a sum reaching 2^24) and, for a walk, its first sum
+    // above thr before that; run stops before the first of them.  The sums
+    // only grow, so a thread with no event value whose last sum stays below
+    // 2^24 (and, walking, at most thr) has neither; one starting at 2^24 or
+    // more has its first value in range as its event.
+    uint32_t run = usat_add(m0, usat_add(woff, inc - tot));
+    const uint32_t last = usat_add(run, tot);
+    int my_ev = len, my_hit = 0x7FFFFFFF;
+    if (run >= kTwo24) {
+      my_ev = max(lo, pos);
+    } else if (any_ev || last >= kTwo24 ||
+               (WALK && __uint_as_float(acc_bits(E, last)) > thr)) {
+      bool stop = false;
+#pragma unroll
+      for (int e = 0; e < kAccPer; e++) {
+        const uint32_t nr = usat_add(run, d[e]);
+        const bool is_ev = !stop && (ev[e] || nr >= kTwo24);
+        my_ev = is_ev ? lo + e : my_ev;
+        stop = stop || is_ev;
+        const bool is_hit = WALK && !stop && lo + e >= pos && lo + e < len &&
+                            __uint_as_float(acc_bits(E, nr)) > thr;
+        my_hit = is_hit ? lo + e : my_hit;
+        run = stop ? run : nr;
+        stop = stop || is_hit;
+      }
+    } else {
+      run = last;
+    }
+    // the wave's first event and first hit: those of its lowest lane that
+    // has one (the lanes' values are in index order)
+    const uint64_t em = __ballot(my_ev < len);
+    const uint64_t hm = WALK ? __ballot(my_hit != 0x7FFFFFFF) : 0ull;
+    const int wev = em ? __builtin_amdgcn_readlane(my_ev, __builtin_ctzll(em)) : len;
+    const int whit = hm ? __builtin_amdgcn_readlane(my_hit, __builtin_ctzll(hm)) : 0x7FFFFFFF;
+    if (lane == 0) {
+      sh.acc_ev[w] = wev;
+      sh.acc_hit[w] = whit;
+    }
+    __syncthreads();
+    int fe = len, fh = 0x7FFFFFFF;
+    {
+      const int4* e4 = reinterpret_cast<const int4*>(sh.acc_ev);
+      const int4* h4 = reinterpret_cast<const int4*>(sh.acc_hit);
+#pragma unroll
+      for (int q = 0; q < kSW / 4; q++) {
+        const int4 a = e4[q];
+        fe = min(fe, min(min(a.x, a.y), min(a.z, a.w)));
+        if (WALK) {
+          const int4 b = h4[q];
+          fh = min(fh, min(min(b.x, b.y), min(b.z, b.w)));
+        }
+      }
+    }
+    if (WALK && fh < fe) {
+      __syncthreads();  // every thread read acc_i before it is reused
+      return fh;
+    }
+    // The sum after the pass: the thread holding the first event adds the
+    // event value to the running sum before it (one float32 addition); with
+    // no event, the thread holding the last value has the sum.
+    const int owner = fe < len ? fe : len - 1;
+    if (owner >= lo && owner < lo + kAccPer) {
+      if (fe < len) {
+        const float c = __uint_as_float(acc_bits(E, run)) + sh.chunk[fe];
+        sh.acc_s = __float_as_uint(c);
+        sh.acc_i[2] = WALK && c > thr ? 1 : 0;
+      } else {
+        sh.acc_s = acc_bits(E, run);
+        sh.acc_i[2] = 0;
+      }
+    }
+    __syncthreads();
+    s = __uint_as_float(sh.acc_s);
+    if (WALK && sh.acc_i[2] != 0) {
+      __syncthreads();  // every thread read acc_i before it is reused
+      return fe;
+    }
+    adv = fe - pos;
+    pos = fe < len ? fe + 1 : len;
+    if (s != s) return WALK ? -2 : -1;
+  }
+  return -1;
+}
+
+// -0.0 + x(0) + x(1) + ... in index order, fp32 (Iterator::sum); every thread
+// gets the result.
 template <typename X>
 __device__ float seq_sum(int cnt, X x, SampleShared& sh) {
-  const int t = threadIdx.x;
   float s = -0.0f;
+  int adv = 0;  // the first values one at a time
   for (int b0 = 0; b0 < cnt; b0 += kChunk) {
     const int len = min(kChunk, cnt - b0);
     stage_chunk(x, b0, len, sh);
     __syncthreads();
-    if (t == 0) {
-      const float4* c4 = reinterpret_cast<const float4*>(sh.chunk);
-      const int runs = len / kRun;
-      float4 v[kRunV], w[kRunV];
-      auto add = [&](const float4(&q)[kRunV]) {
-#pragma unroll
-        for (int u = 0; u < kRunV; u++) {
-          s += q[u].x;
-          s += q[u].y;
-          s += q[u].z;
-          s += q[u].w;
-        }
-      };
-      if (runs > 0) load_run(v, c4, 0);
-      for (int r = 0; r < runs; r += 2) {
-        if (r + 1 < runs) load_run(w, c4, r + 1);
-        add(v);
-        if (r + 1 >= runs) break;
-        if (r + 2 < runs) load_run(v, c4, r + 2);
-        add(w);
-      }
-      for (int j = runs * kRun; j < len; j++) s += sh.chunk[j];
-    }
-    __syncthreads();
+    acc_chunk<false>(len, s, 0.0f, adv, sh);
+    if (s != s) return s;  // NaN stays NaN
   }
-  if (t == 0) sh.f[0] = s;
-  __syncthreads();
-  const float r = sh.f[0];
-  __syncthreads();
-  return r;
+  return s;
 }
 
 // The first j in [0, cnt) at which cum (0.0 + q(0) + ... + q(j), fp32, in
-// order) exceeds thr (thread 0's value); -1 if none.  Thread 0 forms a run of
-// kRun running sums at a time and compares once per run:
-//  * when every staged value of the chunk is >= 0 (no NaN), the sums never
-//    decrease (fp32 addition of a non-negative value is monotone), so the
-//    run's last sum exceeds thr exactly when one of its sums does (a NaN sum
-//    carried in from before compares false throughout, as it should);
-//  * otherwise it compares the maximum of the run's sums (fmaxf passes over
-//    NaN and returns one of its operands).
-// The run that crosses is walked again one value at a time.
+// order) exceeds thr (thread 0's value, the one every thread compares
+// with); -1 if none.
 template <typename Q>
-__device__ int seq_cross(int cnt, Q q, float thr, SampleShared& sh) {
-  const int t = threadIdx.x;
+__device__ int seq_cross(int cnt, Q q, float thr0, SampleShared& sh) {
+  if (threadIdx.x == 0) sh.f[0] = thr0;
+  __syncthreads();
+  const float thr = sh.f[0];
+  __syncthreads();
   float cum = 0.0f;
+  int adv = 0;  // the first values one at a time
   for (int b0 = 0; b0 < cnt; b0 += kChunk) {
     const int len = min(kChunk, cnt - b0);
-    const int odd = stage_chunk(q, b0, len, sh);
-    const bool mono = __syncthreads_or(odd) == 0;
-    if (t == 0) {
-      const float4* c4 = reinterpret_cast<const float4*>(sh.chunk);
-      const int runs = len / kRun;
-      int hit = -1, r = 0;
-      float4 v[kRunV], w[kRunV];
-      // cum over one run; true (cum unchanged) when the run crosses thr
-      auto run = [&](const float4(&x)[kRunV]) {
-        float c = cum;
-        if (mono) {
-#pragma unroll
-          for (int u = 0; u < kRunV; u++) {
-            c += x[u].x;
-            c += x[u].y;
-            c += x[u].z;
-            c += x[u].w;
-          }
-          if (c > thr) return true;
-        } else {
-          float m = -__builtin_inff();
-#pragma unroll
-          for (int u = 0; u < kRunV; u++) {
-            const float c0 = c + x[u].x, c1 = c0 + x[u].y, c2 = c1 + x[u].z, c3 = c2 + x[u].w;
-            m = fmaxf(m, fmaxf(fmaxf(c0, c1), fmaxf(c2, c3)));
-            c = c3;
-          }
-          if (m > thr) return true;
-        }
-        cum = c;
-        return false;
-      };
-      if (runs > 0) load_run(v, c4, 0);
-      for (; r < runs;) {
-        if (r + 1 < runs) load_run(w, c4, r + 1);
-        if (run(v)) break;
-        if (++r >= runs) break;
-        if (r + 1 < runs) load_run(v, c4, r + 1);
-        if (run(w)) break;
-        ++r;
-      }
-      for (int j = r * kRun; j < len; j++) {  // the crossing run, or the tail
-        cum += sh.chunk[j];
-        if (cum > thr) {
-          hit = b0 + j;
-          break;
-        }
-      }
-      sh.ired[0] = hit;
-    }
+    stage_chunk(q, b0, len, sh);
     __syncthreads();
-    const int hit = sh.ired[0];
-    __syncthreads();
-    if (hit >= 0) return hit;
+    const int hit = acc_chunk<true>(len, cum, thr, adv, sh);
+    if (hit >= 0) return b0 + hit;
+    if (hit == -2) return -1;  // cum is NaN: it exceeds nothing
   }
   return -1;
 }

@@ -160,6 +160,47 @@ def test_sample_exact_temperature0(env, orc, top_p, top_k):
         assert _gpu_sample(torch, hk, g, 0.0, top_p, top_k, seed) == want, trial
 
 
+def _edge_value_lists():
+    rng = np.random.default_rng(91)
+    f = np.float32
+    out = []
+    # 2^24, then ones: every later addition lies exactly halfway (round to even)
+    out.append(np.concatenate([[2.0 ** 24], np.ones(20000), rng.random(30000)]).astype(f))
+    out.append(np.full(40000, 0.5, f))                    # halves: ties while the sum is small
+    out.append(np.concatenate([rng.random(20000) * 2.0 ** -140,       # subnormal values,
+                               rng.random(20000)]).astype(f))        # then normal ones
+    out.append(np.full(60000, 3.0, f))                    # the sum doubles many times
+    c = rng.random(50000).astype(f)
+    c[::3] = 0.0
+    c[40000] = 1e30                                       # zeros, and one huge value late
+    out.append(c)
+    out.append((rng.integers(0, 8, 50000) * 0.25).astype(f))  # a coarse grid: many ties
+    n = rng.random(30000).astype(f) + 0.5
+    n[[17, 9000, 29000]] = -2.0                           # negative values amid positive ones
+    out.append(n)
+    i = rng.random(20000).astype(f)
+    i[12345] = np.inf                                     # an infinity
+    out.append(i)
+    return out
+
+
+@pytest.mark.parametrize("which", range(8))
+@pytest.mark.parametrize("top_p", [1.0, 0.9])
+def test_sample_exact_sum_edge_values(env, orc, which, top_p):
+    """The sums and walks run as an exact integer emulation of the sequential
+    fp32 additions over runs of values, with the additions it cannot emulate
+    (ties, leaving a binade, negative or non-finite values) done one at a
+    time: values built to hit each of those, at temperature 0 (p = the
+    values), token and generator state bit for bit."""
+    torch, hk, lib = env
+    p = _edge_value_lists()[which]
+    print(f"[case] edge values {which} top_p={top_p}", flush=True)
+    g = torch.from_numpy(p).cuda()
+    for seed in (4544772189918439317, 261738794409030371, 3524332833679783468):  # r 0.13, 0.53, 0.92
+        want = orc.sample_token(p, 0.0, top_p, 0, seed)
+        assert _gpu_sample(torch, hk, g, 0.0, top_p, 0, seed) == want, seed
+
+
 @pytest.mark.parametrize("temperature,top_p,top_k", [
     (0.7, 0.9, 40), (1.0, 1.0, 0), (0.8, 0.95, 0), (1.2, 1.0, 100), (0.3, 0.5, 0)])
 def test_sample_tokens_match(env, orc, temperature, top_p, top_k):
