@@ -148,6 +148,7 @@ struct SampleArgs {
   float* seg_val;
   uint32_t* a_idx;
   float* a_val;
+  double* range_mass;  // without top-k: [parts][kBins1] key-bin masses (planes 1-3)
   uint32_t* k0;
   uint32_t* k1;
 };
@@ -164,6 +165,7 @@ struct SampleShared {
   uint32_t wsum[kSW];
   float fred[kSW];
   int ired[kSW];
+  double dred[kSW];
   uint32_t u[4];
   float f[4];
   alignas(16) uint32_t acc_w[kSW];  // exact accumulation: per-wave increment totals
@@ -688,18 +690,26 @@ __device__ int acc_chunk(int len, float& s, float thr, int& adv, SampleShared& s
 
 // -0.0 + x(0) + x(1) + ... in index order, fp32 (Iterator::sum); every thread
 // gets the result.
-template <typename X>
-__device__ float seq_sum(int cnt, X x, SampleShared& sh) {
+// on_chunk(len) runs on each staged chunk (sh.chunk[0..len)) before it is
+// added; it may read the chunk, not change it.
+template <typename X, typename F>
+__device__ float seq_sum(int cnt, X x, SampleShared& sh, F on_chunk) {
   float s = -0.0f;
   int adv = 0;  // the first values one at a time
   for (int b0 = 0; b0 < cnt; b0 += kChunk) {
     const int len = min(kChunk, cnt - b0);
     stage_chunk(x, b0, len, sh);
     __syncthreads();
-    acc_chunk<false>(len, s, 0.0f, adv, sh);
+    on_chunk(len);
+    acc_chunk<false>(len, s, 0.0f, adv, sh);  // its barriers follow on_chunk's reads
     if (s != s) return s;  // NaN stays NaN
   }
   return s;
+}
+
+template <typename X>
+__device__ float seq_sum(int cnt, X x, SampleShared& sh) {
+  return seq_sum(cnt, x, sh, [](int) {});
 }
 
 // The first j in [0, cnt) at which cum (0.0 + q(0) + ... + q(j), fp32, in
@@ -724,15 +734,28 @@ __device__ int seq_cross(int cnt, Q q, float thr0, SampleShared& sh) {
   return -1;
 }
 
+// Margin of the top-p bins: how far, relative to the total, the fp32 running
+// sums of L values can stray from exact ones (2 (L + 2) 2^-24).
+__device__ __forceinline__ double top_p_margin(int L) { return 2.0 * ((double)L + 2.0) * 0x1p-24; }
+
+// Without top-k, top-p over a long list walks only the key bins from the
+// top down to where their exact mass reaches top_p + margin of the total.
+__device__ __forceinline__ bool top_bins_apply(const SampleArgs& a) {
+  const bool use_k = a.top_k > 0 && a.top_k < a.n;
+  return !use_k && a.top_p < 1.0f && a.n > kChunk && (double)a.top_p + top_p_margin(a.n) < 1.0;
+}
+
 // First kernel, `parts` work-groups over consecutive ranges [lo, hi) of the
-// logits: each range's ArgPart; unless greedy, p_i for its elements and the
-// range's candidates, in index order, at [lo, lo + seg_cnt[g]) of
-// seg_idx / seg_val:
-//  * with top-k, the elements whose key is at least the range's own k-th
-//    largest key (every element of a range of at most k), and every NaN: an
-//    element that top-k keeps is at least the overall k-th largest p, and
-//    fewer than k elements in all (so in its range) exceed it;
-//  * without, the non-zero p (zeros add nothing to the running sums).
+// logits: each range's ArgPart; unless greedy, p_i for its elements, and
+//  * with top-k, the range's candidates, in index order, at
+//    [lo, lo + seg_cnt[g]) of seg_idx / seg_val: the elements whose key is at
+//    least the range's own k-th largest key (every element of a range of at
+//    most k), and every NaN: an element that top-k keeps is at least the
+//    overall k-th largest p, and fewer than k elements in all (so in its
+//    range) exceed it;
+//  * without, when top_bins_apply, the range's mass (double) in each of the
+//    kBins1 key bins, and in seg_cnt[g] whether any p is negative, infinite
+//    or NaN (the bins are then not used).
 __global__ void __launch_bounds__(kST) sample_parts_kernel(const SampleArgs a) {
   __shared__ SampleShared sh;
   const int t = threadIdx.x, g = blockIdx.x;
@@ -741,15 +764,36 @@ __global__ void __launch_bounds__(kST) sample_parts_kernel(const SampleArgs a) {
   const ArgPart ap = argmax_part(lo, hi, [&](int i) { return a.logits[i]; }, sh);
   if (t == 0) a.part[g] = ap;
   if (a.greedy_only) return;
+  const bool use_k = a.top_k > 0 && a.top_k < a.n;
+  const bool bins = top_bins_apply(a);
+  if (bins) {
+    for (int i = t; i < kBins1; i += kST) sh.mass[i] = 0.0;
+    __syncthreads();
+  }
   const bool scale = a.temperature > 0.0f;
+  int bad = 0;
   for (int i = lo + t; i < hi; i += kST) {
     const float l = a.logits[i];
-    a.probs[i] = scale ? (float)exp((double)(l * a.inv_temp)) : l;
+    const float p = scale ? (float)exp((double)(l * a.inv_temp)) : l;
+    a.probs[i] = p;
+    if (bins) {
+      bad |= !(p >= 0.0f && p < __builtin_inff());
+      atomicAdd(&sh.mass[fkey(p) >> 21], (double)p);
+    }
+  }
+  if (!use_k) {
+    if (bins) {
+      bad = __syncthreads_or(bad);
+      static_assert(kBins1 == 2 * kST, "two bins per thread");
+      reinterpret_cast<double2*>(a.range_mass)[(size_t)g * kST + t] =
+          make_double2(sh.mass[2 * t], sh.mass[2 * t + 1]);
+      if (t == 0) a.seg_cnt[g] = bad;
+    }
+    return;
   }
   __syncthreads();
-  const bool use_k = a.top_k > 0 && a.top_k < a.n;
   int cnt;
-  if (use_k) {
+  {
     const uint32_t kth = hi - lo > a.top_k
                              ? kth_largest_key(hi - lo, [&](int j) { return fkey(a.probs[lo + j]); },
                                                (uint32_t)a.top_k, sh)
@@ -758,12 +802,153 @@ __global__ void __launch_bounds__(kST) sample_parts_kernel(const SampleArgs a) {
         lo, hi, [&](int i) { return a.probs[i]; },
         [&](int, float x) { return fkey(x) >= kth || __builtin_isnan(x); }, a.seg_idx + lo,
         a.seg_val + lo, sh);
-  } else {
-    cnt = compact_range(
-        lo, hi, [&](int i) { return a.probs[i]; }, [&](int, float x) { return x != 0.0f; },
-        a.seg_idx + lo, a.seg_val + lo, sh);
   }
   if (t == 0) a.seg_cnt[g] = cnt;
+}
+
+// Appends ~key of every staged value whose key is at least tkey to out, in
+// no particular order, counting in sh.u[3] (one LDS atomic per wave).
+__device__ void gather_top_keys(int len, uint32_t tkey, uint32_t* out, SampleShared& sh) {
+  const int t = threadIdx.x, lane = t & 63;
+  const uint64_t lt = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int e = 0; e < kChunk / kST; e++) {
+    const int j = t + e * kST;
+    const uint32_t k = j < len ? fkey(sh.chunk[j]) : 0u;
+    const bool take = j < len && k >= tkey;
+    const uint64_t m = __ballot(take);
+    if (m) {
+      const int lead = __builtin_ctzll(m);
+      uint32_t base = 0;
+      if (lane == lead) base = atomicAdd(&sh.u[3], (uint32_t)__popcll(m));
+      base = (uint32_t)__builtin_amdgcn_readlane((int)base, lead);
+      if (take) out[base + (uint32_t)__popcll(m & lt)] = ~k;
+    }
+  }
+}
+
+// Without top-k: the top key bin whose mass, added from the top down,
+// reaches (top_p + margin) of the total, from the ranges' bin masses;
+// -1 when a range held a negative, infinite or NaN p, or no bin reaches it
+// (the double sums' order differs from a sequential one: any bin is a
+// correct choice, it only decides how much is sorted before the fallback).
+__device__ int top_mass_bin(const SampleArgs& a, SampleShared& sh) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  // bins 2t and 2t + 1 over the ranges, 16 ranges' loads in flight
+  constexpr int kB = 16;
+  const double2* rm = reinterpret_cast<const double2*>(a.range_mass);
+  double m0 = 0.0, m1 = 0.0;
+  for (int g0 = 0; g0 < a.parts; g0 += kB) {
+    double2 v[kB];
+#pragma unroll
+    for (int u = 0; u < kB; u++) v[u] = rm[(size_t)min(g0 + u, a.parts - 1) * kST + t];
+#pragma unroll
+    for (int u = 0; u < kB; u++) {
+      if (g0 + u < a.parts) {
+        m0 += v[u].x;
+        m1 += v[u].y;
+      }
+    }
+  }
+  const int bad = __syncthreads_or(t < a.parts ? a.seg_cnt[t] : 0);
+  if (bad) return -1;
+  sh.mass[2 * t] = m0;
+  sh.mass[2 * t + 1] = m1;
+  __syncthreads();
+  // top-first: thread t owns bins 2047 - 2t, then 2046 - 2t
+  const double c0 = sh.mass[kBins1 - 1 - 2 * t], c1 = sh.mass[kBins1 - 2 - 2 * t];
+  double incl = c0 + c1;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const double o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  double excl = __shfl_up(incl, 1, 64);
+  if (lane == 0) excl = 0.0;
+  if (lane == 63) sh.dred[w] = incl;
+  __syncthreads();
+  double before = 0.0, tot = 0.0;
+  for (int v = 0; v < kSW; v++) {
+    const double d = sh.dred[v];
+    if (v < w) before += d;
+    tot += d;
+  }
+  const double need = ((double)a.top_p + top_p_margin(a.n)) * tot;
+  const double a0 = before + excl + c0, a1 = a0 + c1;
+  const int cand = a0 >= need ? 2 * t : a1 >= need ? 2 * t + 1 : 0x7FFFFFFF;
+  // the first candidate from the top: that of the lowest such thread
+  const uint64_t cm = __ballot(cand != 0x7FFFFFFF);
+  const int wc = cm ? __builtin_amdgcn_readlane(cand, __builtin_ctzll(cm)) : 0x7FFFFFFF;
+  if (lane == 0) sh.ired[w] = wc;
+  __syncthreads();
+  int first = 0x7FFFFFFF;
+  for (int v = 0; v < kSW; v++) first = min(first, sh.ired[v]);
+  __syncthreads();  // sh.ired / sh.dred read by all before reuse
+  return first == 0x7FFFFFFF ? -1 : kBins1 - 1 - first;
+}
+
+// sample_token without top-k: the sums and walks run over p itself, all n
+// values in index order, zeros included, as the reference's loops do
+// (run.rs:203-251); the draw's index is the token.
+__device__ void sample_no_topk(const SampleArgs& a, SampleShared& sh) {
+  const int t = threadIdx.x;
+  const int n = a.n;
+  const float* p = a.probs;
+  float thr_p = -__builtin_inff();
+  if (a.top_p < 1.0f) {
+    const int top = top_bins_apply(a) ? top_mass_bin(a, sh) : -1;
+    const uint32_t tkey = (uint32_t)(top < 0 ? 0 : top) << 21;
+    if (t == 0) sh.u[3] = 0;
+    __syncthreads();
+    // the sum, gathering the keys of the top bins from its staged chunks
+    const float sum1 = seq_sum(n, [&](int j) { return p[j]; }, sh, [&](int len) {
+      if (top >= 0) gather_top_keys(len, tkey, a.k0, sh);
+    });
+    const int Lc = (int)sh.u[3];
+    if (sum1 > 0.0f) {
+      int at = -1;
+      if (top >= 0) {
+        radix_sort_keys(a.k0, a.k1, Lc, sh);
+        at = seq_cross(Lc, [&](int j) { return funkey(~a.k0[j]) / sum1; }, a.top_p, sh);
+      }
+      if (at < 0) {  // every p, sorted
+        for (int j = t; j < n; j += kST) a.k0[j] = ~fkey(p[j]);
+        __syncthreads();
+        radix_sort_keys(a.k0, a.k1, n, sh);
+        at = seq_cross(n, [&](int j) { return funkey(~a.k0[j]) / sum1; }, a.top_p, sh);
+      }
+      thr_p = at >= 0 ? funkey(~a.k0[at]) : 3.40282347e+38f;
+    }
+    __syncthreads();  // sh.u[3] read by all before reuse
+  }
+  const float tp = thr_p;
+  auto q = [&](int j) {
+    const float x = p[j];
+    return x < tp ? 0.0f : x;
+  };
+  const float sum2 = seq_sum(n, q, sh);
+  if (sum2 <= 0.0f) {
+    if (t == 0) *a.token = argmax_combine(a.part, a.parts, n);
+    return;
+  }
+  // r = next_f32(): xorshift 13, 7, 17, then the top 24 bits / 2^24
+  float r = 0.0f;
+  if (t == 0) {
+    uint64_t x = *a.state;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *a.state = x;
+    r = (float)(x >> 40) / 16777216.0f;
+  }
+  // the first index whose running sum of p / S exceeds r (r < cum)
+  const int at = seq_cross(n, [&](int j) { return q(j) / sum2; }, r, sh);
+  if (at >= 0) {
+    if (t == 0) *a.token = (uint32_t)at;
+    return;
+  }
+  const uint32_t am = argmax_fold(n, q, sh);
+  if (t == 0) *a.token = am;
 }
 
 // Second kernel, one work-group: the rest of sample_token.
@@ -776,9 +961,12 @@ __global__ void __launch_bounds__(kST) sample_token_kernel(const SampleArgs a) {
     return;
   }
   const bool use_k = a.top_k > 0 && a.top_k < n;
-  // the ranges' candidate lists, concatenated in order (index order): into
-  // k0 (indices) / k1 (values) for the top-k pass, else straight into the
-  // non-zero list a_idx / a_val
+  if (!use_k) {
+    sample_no_topk(a, sh);
+    return;
+  }
+  // the ranges' candidate lists, concatenated in order (index order), into
+  // k0 (indices) / k1 (values) for the top-k pass
   if (t == 0) {
     int run = 0;
     for (int g = 0; g < a.parts; g++) {
@@ -789,8 +977,8 @@ __global__ void __launch_bounds__(kST) sample_token_kernel(const SampleArgs a) {
   }
   __syncthreads();
   const int C = (int)sh.u[2];
-  uint32_t* cidx = use_k ? a.k0 : a.a_idx;
-  float* cval = use_k ? reinterpret_cast<float*>(a.k1) : a.a_val;
+  uint32_t* cidx = a.k0;
+  float* cval = reinterpret_cast<float*>(a.k1);
   // Element i of the concatenation is element i - off[g] of range g, g the
   // last range with off[g] <= i (a binary search over the range offsets);
   // each thread reads kPer elements before storing any, so the reads are in
@@ -832,18 +1020,14 @@ __global__ void __launch_bounds__(kST) sample_token_kernel(const SampleArgs a) {
   }
   __syncthreads();
   // top_k: the k-th largest p; the non-zero p not below it, in index order
-  float thr_k = -__builtin_inff();  // p < thr_k -> 0 (nothing when -inf)
-  int L;
-  if (use_k) {
-    thr_k = funkey(kth_largest_key(C, [&](int j) { return fkey(cval[j]); }, (uint32_t)a.top_k, sh));
-    L = compact_range(
-        0, C, [&](int j) { return cval[j]; },
-        [&](int, float x) { return !(x < thr_k) && x != 0.0f; }, a.a_idx, a.a_val, sh);
-    for (int j = t; j < L; j += kST) a.a_idx[j] = a.k0[a.a_idx[j]];  // positions -> tokens
-    __syncthreads();
-  } else {
-    L = C;
-  }
+  // (zeros add nothing to the running sums)
+  const float thr_k =
+      funkey(kth_largest_key(C, [&](int j) { return fkey(cval[j]); }, (uint32_t)a.top_k, sh));
+  const int L = compact_range(
+      0, C, [&](int j) { return cval[j]; },
+      [&](int, float x) { return !(x < thr_k) && x != 0.0f; }, a.a_idx, a.a_val, sh);
+  for (int j = t; j < L; j += kST) a.a_idx[j] = a.k0[a.a_idx[j]];  // positions -> tokens
+  __syncthreads();
   // top_p: walk the p in descending order (sorted keys)
   float thr_p = -__builtin_inff();
   int Lb = L;
@@ -858,21 +1042,16 @@ __global__ void __launch_bounds__(kST) sample_token_kernel(const SampleArgs a) {
       // fp32 sums can stray from exact ones (2 (L + 2) 2^-24 relative);
       // failing that (top_p near 1, negative or non-finite p), or should the
       // walk not cross in them, all of the p.
-      const double margin = 2.0 * ((double)L + 2.0) * 0x1p-24;
+      const double margin = top_p_margin(L);
       int at = -1;
       if (L > kChunk && (double)a.top_p + margin < 1.0) {
-        for (int i = t; i < kBins1; i += kST) {
-          sh.hist[i] = 0;
-          sh.mass[i] = 0.0;
-        }
+        for (int i = t; i < kBins1; i += kST) sh.mass[i] = 0.0;
         __syncthreads();
         int bad = 0;
         for (int j = t; j < L; j += kST) {
           const float x = a.a_val[j];
           bad |= !(x > 0.0f && x < __builtin_inff());
-          const uint32_t b = fkey(x) >> 21;
-          atomicAdd(&sh.hist[b], 1u);
-          atomicAdd(&sh.mass[b], (double)x);
+          atomicAdd(&sh.mass[fkey(x) >> 21], (double)x);
         }
         bad = __syncthreads_or(bad);
         if (t == 0) {
@@ -1014,6 +1193,10 @@ hipError_t launch_sample_token(uint32_t* token, uint64_t* state, const float* lo
   a.a_val = reinterpret_cast<float*>(pl(4));
   a.k0 = reinterpret_cast<uint32_t*>(pl(5));
   a.k1 = reinterpret_cast<uint32_t*>(pl(6));
+  // planes 1-3 (contiguous, 12 n bytes), unused without top-k, hold the
+  // ranges' bin masses: parts * kBins1 * 8 <= (n / kPartElems + 1) * 16 KB,
+  // within 12 n bytes whenever the bins are used (n > kChunk)
+  a.range_mass = reinterpret_cast<double*>(pl(1));
   hipLaunchKernelGGL(sample_parts_kernel, dim3(a.parts), dim3(kST), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

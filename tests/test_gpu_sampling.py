@@ -137,6 +137,9 @@ def test_argmax(env, orc):
 
 EXACT_CASES = [  # (top_p, top_k)
     (1.0, 0), (1.0, 40), (0.9, 0), (0.9, 40), (0.5, 1000), (0.95, 1), (0.999, 50000),
+    # without top-k: the key bins from the top (0.5), and every p sorted
+    # (0.99: top_p plus the margin of the fp32 sums reaches 1)
+    (0.5, 0), (0.99, 0),
     # k around the length of the device's per-range candidate lists (128256
     # logits in 63 ranges of 2035-2036) and k = n - 1
     (0.9, 2035), (1.0, 2036), (0.8, 3000), (1.0, VOCAB - 1),
