@@ -121,6 +121,35 @@ __device__ __forceinline__ float funkey(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
+__device__ __forceinline__ uint32_t usat_add(uint32_t a, uint32_t b) {
+  return __builtin_elementwise_add_sat(a, b);
+}
+
+// d = v / u rounded to the nearest integer for v >= +0 finite, on the grid
+// u = 2^(E - 150) of exponent field E >= 1, with sc = 150 - E: v 2^sc is
+// exact (a power-of-two scaling; an overflow to inf only where v / u >=
+// 2^24, a result below 2^-126 only where v / u < 1/2: d = 0 either way); d
+// >= 2^24 is returned as 2^24 (the sum leaves the binade whatever m is).
+// tie: v / u is exactly halfway between two integers.
+__device__ __forceinline__ uint32_t acc_increment(float v, int sc, bool& tie) {
+  const float q = fminf(ldexpf(v, sc), 16777216.0f);  // NaN v: 2^24 (an event anyway)
+  tie = __builtin_amdgcn_fractf(q) == 0.5f;
+  return (uint32_t)__builtin_rintf(q);
+}
+
+// Inclusive scan of x over the wave (lane order), saturating at 2^32 - 1:
+// sums over 1, 2, 4, 8 lanes within each row of 16, then each row takes the
+// previous rows' total (row_bcast:15, row_bcast:31).
+__device__ __forceinline__ uint32_t wave_scan_sat(uint32_t x) {
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false));
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false));
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false));
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false));
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false));
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false));
+  return x;
+}
+
 // Argmax of one range of the logits: the last NaN in it (-1: none) and the
 // best (value, index) over the elements after that NaN, the later index among
 // equal values (bi = -1: nothing follows the NaN).
@@ -155,13 +184,18 @@ struct SampleArgs {
 
 constexpr int kChunk = 8192;  // floats of a sequential pass staged in LDS at a time
 
+constexpr int kSortCap = 12288;  // keys a sort keeps in LDS
+
 struct SampleShared {
-  float chunk[kChunk];
+  union {
+    float chunk[kChunk];         // staged values of a sequential sum
+    uint32_t sorta[kSortCap];    // an LDS sort's second buffer
+  };
+  uint32_t sortb[kSortCap];      // keys of an LDS sort, in and out
   double mass[kBins1];
   uint32_t hist[kBins1];
   uint32_t cnt[kSW][256];
   uint32_t base[256];
-  uint32_t tot[256];
   uint32_t wsum[kSW];
   float fred[kSW];
   int ired[kSW];
@@ -174,6 +208,7 @@ struct SampleShared {
   int acc_i[4];    // sequential batch: -, first sum above thr, next position; hit flag
   uint32_t acc_s;  // the running sum's bit pattern
 };
+static_assert(sizeof(SampleShared) <= 160 * 1024, "LDS of a work-group");
 
 // In the histogram hist[0..nbins), bins counted from the top: the bin holding
 // the kk-th largest element (1-based) and kk within that bin.  nbins <= 2048.
@@ -328,34 +363,65 @@ __device__ int compact_range(int lo, int hi, V val, K keep, uint32_t* idx, float
   return L;
 }
 
-// Stable LSD radix sort of keys k0[0..L) ascending (four 8-bit passes through
-// k1; the result is back in k0).  Ranks within a wave come from ballots over
-// the digit's bits, across waves from per-digit counts in LDS.
-__device__ void radix_sort_keys(uint32_t* k0, uint32_t* k1, int L, SampleShared& sh) {
+// Stable LSD radix sort of keys ascending, four 8-bit passes: with kLds,
+// sh.sortb[0..L) (L <= kSortCap) through sh.sorta, else k0[0..L) in global
+// memory through k1; the result is back where the keys were.  The four digit
+// histograms come from one read of the keys (a key's digits do not depend on
+// the order); then each pass takes the keys kST at a time (the next kST read
+// while the current ones are placed): ranks within a wave from ballots over
+// the digit's bits, across waves from per-wave digit counts, two barriers
+// per kST keys.
+template <bool kLds>
+__device__ __forceinline__ void radix_sort_impl(uint32_t* g0, uint32_t* g1, int L,
+                                                SampleShared& sh) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const uint64_t lt = (1ull << lane) - 1ull;
   if (L <= 1) return;
-  for (int pass = 0; pass < 4; pass++) {
-    const int sh_bits = 8 * pass;
-    uint32_t* src = (pass & 1) ? k1 : k0;
-    uint32_t* dst = (pass & 1) ? k0 : k1;
-    if (t < 256) sh.hist[t] = 0;
-    __syncthreads();
-    for (int i = t; i < L; i += kST) atomicAdd(&sh.hist[(src[i] >> sh_bits) & 255u], 1u);
-    __syncthreads();
-    if (t == 0) {
-      uint32_t run = 0;
-      for (int d = 0; d < 256; d++) {
-        sh.base[d] = run;
-        run += sh.hist[d];
+  uint32_t* k0 = kLds ? sh.sortb : g0;
+  uint32_t* k1 = kLds ? sh.sorta : g1;
+  // hist[256 p + d]: keys whose digit p is d
+  for (int i = t; i < 4 * 256; i += kST) sh.hist[i] = 0;
+  __syncthreads();
+  {
+    constexpr int kR = 8;
+    for (int b0 = 0; b0 < L; b0 += kR * kST) {
+      uint32_t k[kR];
+#pragma unroll
+      for (int u = 0; u < kR; u++) k[u] = k0[min(b0 + u * kST + t, L - 1)];
+#pragma unroll
+      for (int u = 0; u < kR; u++) {
+        if (b0 + u * kST + t < L) {
+#pragma unroll
+          for (int p = 0; p < 4; p++) atomicAdd(&sh.hist[256 * p + ((k[u] >> (8 * p)) & 255u)], 1u);
+        }
       }
     }
+  }
+  __syncthreads();
+  // exclusive offsets within each histogram: thread t scans entry t of
+  // histogram t / 256 (four waves per histogram)
+  {
+    const uint32_t c = sh.hist[t];
+    const uint32_t inc = wave_scan_sat(c);
+    if (lane == 63) sh.wsum[wave] = inc;
     __syncthreads();
+    uint32_t off = 0;
+    for (int w = wave & ~3; w < wave; w++) off += sh.wsum[w];
+    sh.hist[t] = off + inc - c;
+  }
+  for (int pass = 0; pass < 4; pass++) {
+    const int shb = 8 * pass;
+    const uint32_t* src = (pass & 1) ? k1 : k0;
+    uint32_t* dst = (pass & 1) ? k0 : k1;
+    __syncthreads();  // the offsets, and the previous pass's keys, are complete
+    if (t < 256) sh.base[t] = sh.hist[256 * pass + t];
+    uint32_t key = src[min(t, L - 1)];
     for (int b0 = 0; b0 < L; b0 += kST) {
       const int i = b0 + t;
       const bool valid = i < L;
-      const uint32_t key = valid ? src[i] : 0u;
-      const uint32_t d = (key >> sh_bits) & 255u;
+      const uint32_t cur = key;
+      if (b0 + kST < L) key = src[min(b0 + kST + t, L - 1)];  // the next kST
+      const uint32_t d = (cur >> shb) & 255u;
       uint64_t m = __ballot(valid);
 #pragma unroll
       for (int b = 0; b < 8; b++) {
@@ -363,26 +429,56 @@ __device__ void radix_sort_keys(uint32_t* k0, uint32_t* k1, int L, SampleShared&
         m &= ((d >> b) & 1u) ? bb : ~bb;
       }
       const int rank = __popcll(m & lt);
-      for (int e = t; e < kSW * 256; e += kST) (&sh.cnt[0][0])[e] = 0;
-      __syncthreads();
+      // this wave's digit counts (its own row: zeros, then the counts; one
+      // wave's LDS writes land in order)
+      for (int e = lane; e < 256; e += 64) sh.cnt[wave][e] = 0;
       if (valid && rank == 0) sh.cnt[wave][d] = (uint32_t)__popcll(m);
       __syncthreads();
       if (t < 256) {
-        uint32_t run = 0;
+        uint32_t c[kSW];
+#pragma unroll
+        for (int w = 0; w < kSW; w++) c[w] = sh.cnt[w][t];
+        uint32_t run = sh.base[t];
+#pragma unroll
         for (int w = 0; w < kSW; w++) {
-          const uint32_t c = sh.cnt[w][t];
           sh.cnt[w][t] = run;
-          run += c;
+          run += c[w];
         }
-        sh.tot[t] = run;
+        sh.base[t] = run;
       }
       __syncthreads();
-      if (valid) dst[sh.base[d] + sh.cnt[wave][d] + rank] = key;
-      __syncthreads();
-      if (t < 256) sh.base[t] += sh.tot[t];
-      __syncthreads();
+      if (valid) dst[sh.cnt[wave][d] + rank] = cur;
     }
   }
+  __syncthreads();
+}
+
+__device__ void radix_sort_keys(uint32_t* k0, uint32_t* k1, int L, SampleShared& sh) {
+  radix_sort_impl<false>(k0, k1, L, sh);
+}
+
+__device__ void radix_sort_lds(int L, SampleShared& sh) {
+  radix_sort_impl<true>(nullptr, nullptr, L, sh);
+}
+
+// Sorts keys k0[0..L) ascending; returns where the result is: sh.sortb (the
+// keys copied there, L <= kSortCap) or k0 (a global sort through k1).
+__device__ const uint32_t* sort_keys(uint32_t* k0, uint32_t* k1, int L, SampleShared& sh) {
+  if (L > kSortCap) {
+    radix_sort_keys(k0, k1, L, sh);
+    return k0;
+  }
+  const int t = threadIdx.x;
+  constexpr int kPer = kSortCap / kST;
+  uint32_t v[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; u++) v[u] = k0[min(t + u * kST, max(L - 1, 0))];
+#pragma unroll
+  for (int u = 0; u < kPer; u++)
+    if (t + u * kST < L) sh.sortb[t + u * kST] = v[u];
+  __syncthreads();
+  radix_sort_lds(L, sh);
+  return sh.sortb;
 }
 
 // The k-th largest (1-based, 1 <= kk <= cnt) of the keys key(j), j in
@@ -465,34 +561,6 @@ constexpr int kAccPer = 8;      // consecutive values per thread in a parallel p
 static_assert(kAccPer * kST == kChunk, "a parallel pass covers a chunk");
 constexpr uint32_t kTwo24 = 1u << 24;
 
-__device__ __forceinline__ uint32_t usat_add(uint32_t a, uint32_t b) {
-  return __builtin_elementwise_add_sat(a, b);
-}
-
-// d = v / u rounded to the nearest integer for v >= +0 finite, on the grid
-// u = 2^(E - 150) of exponent field E >= 1, with sc = 150 - E: v 2^sc is
-// exact (a power-of-two scaling; an overflow to inf only where v / u >=
-// 2^24, a result below 2^-126 only where v / u < 1/2: d = 0 either way); d
-// >= 2^24 is returned as 2^24 (the sum leaves the binade whatever m is).
-// tie: v / u is exactly halfway between two integers.
-__device__ __forceinline__ uint32_t acc_increment(float v, int sc, bool& tie) {
-  const float q = ldexpf(v, sc);
-  tie = __builtin_amdgcn_fractf(q) == 0.5f;
-  return q >= 16777216.0f ? kTwo24 : (uint32_t)__builtin_rintf(q);
-}
-
-// Inclusive scan of x over the wave (lane order), saturating at 2^32 - 1:
-// sums over 1, 2, 4, 8 lanes within each row of 16, then each row takes the
-// previous rows' total (row_bcast:15, row_bcast:31).
-__device__ __forceinline__ uint32_t wave_scan_sat(uint32_t x) {
-  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false));
-  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false));
-  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false));
-  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false));
-  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false));
-  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false));
-  return x;
-}
 
 // Bit pattern of m u on the grid of exponent field E (m < 2^24; m < 2^23
 // only with E = 1, the subnormal range).
@@ -572,20 +640,24 @@ __device__ int acc_chunk(int len, float& s, float thr, int& adv, SampleShared& s
 #pragma unroll
       for (int e = 0; e < kAccPer; e++) v[e] = 0.0f;
     }
+    // values outside [pos, len) count as +0 (only thread 0 and the thread
+    // holding position len have any)
+    if (lo < pos || lo + kAccPer > len) {
+#pragma unroll
+      for (int e = 0; e < kAccPer; e++) v[e] = lo + e < pos || lo + e >= len ? 0.0f : v[e];
+    }
     uint32_t d[kAccPer];
     bool ev[kAccPer];
     bool any_ev = false;
     uint32_t tot = 0;
 #pragma unroll
     for (int e = 0; e < kAccPer; e++) {
-      const int j = lo + e;
-      const bool in = j >= pos && j < len;
       bool tie;
       const uint32_t de = acc_increment(v[e], sc, tie);
-      // negative (or -0), infinite or NaN values, and ties, are events
-      const bool odd = __builtin_isinf(v[e]) || __builtin_isnan(v[e]) || __builtin_signbit(v[e]);
-      ev[e] = in && (odd || tie);
-      d[e] = in && !ev[e] ? de : 0u;
+      // negative (or -0), infinite or NaN values, and ties, are events:
+      // classes sNaN, qNaN, -inf, -normal, -subnormal, -0, +inf
+      ev[e] = __builtin_amdgcn_classf(v[e], 0x23F) || tie;
+      d[e] = ev[e] ? 0u : de;
       tot += d[e];  // <= 8 2^24
       any_ev = any_ev || ev[e];
     }
@@ -806,24 +878,32 @@ __global__ void __launch_bounds__(kST) sample_parts_kernel(const SampleArgs a) {
   if (t == 0) a.seg_cnt[g] = cnt;
 }
 
-// Appends ~key of every staged value whose key is at least tkey to out, in
-// no particular order, counting in sh.u[3] (one LDS atomic per wave).
-__device__ void gather_top_keys(int len, uint32_t tkey, uint32_t* out, SampleShared& sh) {
+// Appends ~key of every staged value whose key is at least tkey to
+// sh.sortb, in no particular order, counting in sh.u[3] (one LDS atomic per
+// wave); keys past kSortCap are counted, not stored.
+__device__ void gather_top_keys(int len, uint32_t tkey, SampleShared& sh) {
   const int t = threadIdx.x, lane = t & 63;
   const uint64_t lt = (1ull << lane) - 1ull;
+  constexpr int kPer = kChunk / kST;
+  uint32_t k[kPer];
+  uint64_t m[kPer];
+  uint32_t cnt = 0;
 #pragma unroll
-  for (int e = 0; e < kChunk / kST; e++) {
+  for (int e = 0; e < kPer; e++) {
     const int j = t + e * kST;
-    const uint32_t k = j < len ? fkey(sh.chunk[j]) : 0u;
-    const bool take = j < len && k >= tkey;
-    const uint64_t m = __ballot(take);
-    if (m) {
-      const int lead = __builtin_ctzll(m);
-      uint32_t base = 0;
-      if (lane == lead) base = atomicAdd(&sh.u[3], (uint32_t)__popcll(m));
-      base = (uint32_t)__builtin_amdgcn_readlane((int)base, lead);
-      if (take) out[base + (uint32_t)__popcll(m & lt)] = ~k;
-    }
+    k[e] = j < len ? fkey(sh.chunk[j]) : 0u;
+    m[e] = __ballot(j < len && k[e] >= tkey);
+    cnt += (uint32_t)__popcll(m[e]);
+  }
+  if (cnt == 0) return;  // the whole wave
+  uint32_t base = 0;
+  if (lane == 0) base = atomicAdd(&sh.u[3], cnt);
+  base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+#pragma unroll
+  for (int e = 0; e < kPer; e++) {
+    const uint32_t at = base + (uint32_t)__popcll(m[e] & lt);
+    if (((m[e] >> lane) & 1ull) && at < (uint32_t)kSortCap) sh.sortb[at] = ~k[e];
+    base += (uint32_t)__popcll(m[e]);
   }
 }
 
@@ -898,26 +978,42 @@ __device__ void sample_no_topk(const SampleArgs& a, SampleShared& sh) {
   if (a.top_p < 1.0f) {
     const int top = top_bins_apply(a) ? top_mass_bin(a, sh) : -1;
     const uint32_t tkey = (uint32_t)(top < 0 ? 0 : top) << 21;
-    if (t == 0) sh.u[3] = 0;
+    if (t == 0) {
+      sh.u[2] = 0;
+      sh.u[3] = 0;
+    }
     __syncthreads();
-    // the sum, gathering the keys of the top bins from its staged chunks
+    // the sum, gathering the keys of the top bins (into LDS) from its staged
+    // chunks
     const float sum1 = seq_sum(n, [&](int j) { return p[j]; }, sh, [&](int len) {
-      if (top >= 0) gather_top_keys(len, tkey, a.k0, sh);
+      if (top >= 0) gather_top_keys(len, tkey, sh);
     });
     const int Lc = (int)sh.u[3];
     if (sum1 > 0.0f) {
       int at = -1;
+      const uint32_t* keys = a.k0;
       if (top >= 0) {
-        radix_sort_keys(a.k0, a.k1, Lc, sh);
-        at = seq_cross(Lc, [&](int j) { return funkey(~a.k0[j]) / sum1; }, a.top_p, sh);
+        if (Lc <= kSortCap) {
+          radix_sort_lds(Lc, sh);
+          keys = sh.sortb;
+        } else {  // too many for LDS: gathered again, into global memory
+          for (int j = t; j < n; j += kST) {
+            const uint32_t k = fkey(p[j]);
+            if (k >= tkey) a.k0[atomicAdd(&sh.u[2], 1u)] = ~k;
+          }
+          __syncthreads();
+          radix_sort_keys(a.k0, a.k1, Lc, sh);
+        }
+        at = seq_cross(Lc, [&](int j) { return funkey(~keys[j]) / sum1; }, a.top_p, sh);
       }
       if (at < 0) {  // every p, sorted
         for (int j = t; j < n; j += kST) a.k0[j] = ~fkey(p[j]);
         __syncthreads();
         radix_sort_keys(a.k0, a.k1, n, sh);
-        at = seq_cross(n, [&](int j) { return funkey(~a.k0[j]) / sum1; }, a.top_p, sh);
+        keys = a.k0;
+        at = seq_cross(n, [&](int j) { return funkey(~keys[j]) / sum1; }, a.top_p, sh);
       }
-      thr_p = at >= 0 ? funkey(~a.k0[at]) : 3.40282347e+38f;
+      thr_p = at >= 0 ? funkey(~keys[at]) : 3.40282347e+38f;
     }
     __syncthreads();  // sh.u[3] read by all before reuse
   }
@@ -1044,6 +1140,7 @@ __global__ void __launch_bounds__(kST) sample_token_kernel(const SampleArgs a) {
       // walk not cross in them, all of the p.
       const double margin = top_p_margin(L);
       int at = -1;
+      const uint32_t* keys = a.k0;  // the sorted keys: global, or LDS
       if (L > kChunk && (double)a.top_p + margin < 1.0) {
         for (int i = t; i < kBins1; i += kST) sh.mass[i] = 0.0;
         __syncthreads();
@@ -1082,17 +1179,17 @@ __global__ void __launch_bounds__(kST) sample_token_kernel(const SampleArgs a) {
               [&](int, float x) { return fkey(x) >= tkey; }, a.k1, cv, sh);
           for (int j = t; j < Lc; j += kST) a.k0[j] = ~fkey(cv[j]);  // descending
           __syncthreads();
-          radix_sort_keys(a.k0, a.k1, Lc, sh);
-          at = seq_cross(Lc, [&](int j) { return funkey(~a.k0[j]) / sum1; }, a.top_p, sh);
+          keys = sort_keys(a.k0, a.k1, Lc, sh);
+          at = seq_cross(Lc, [&](int j) { return funkey(~keys[j]) / sum1; }, a.top_p, sh);
         }
       }
       if (at < 0) {
         for (int j = t; j < L; j += kST) a.k0[j] = ~fkey(a.a_val[j]);  // descending
         __syncthreads();
-        radix_sort_keys(a.k0, a.k1, L, sh);
-        at = seq_cross(L, [&](int j) { return funkey(~a.k0[j]) / sum1; }, a.top_p, sh);
+        keys = sort_keys(a.k0, a.k1, L, sh);
+        at = seq_cross(L, [&](int j) { return funkey(~keys[j]) / sum1; }, a.top_p, sh);
       }
-      thr_p = at >= 0 ? funkey(~a.k0[at]) : 3.40282347e+38f;
+      thr_p = at >= 0 ? funkey(~keys[at]) : 3.40282347e+38f;
       // p < thr_p -> 0: keep the survivors of the index-ordered list, in
       // order (k0 / k1 reused as the second list's storage)
       uint32_t* b_idx = a.k1;
