@@ -694,8 +694,9 @@ def next_token(torch, lib):
     ok = ok and want is not None and int(got.item()) == want
     return {"workload": "next token from K=4096 x N=128256 lm_head logits: greedy argmax and "
                         "sample_token (a launch over 63 ranges of the logits, then one "
-                        "work-group; the fp32 sums and walks one lane's sequential "
-                        "additions, as the reference's); GPU us per call", "results": out,
+                        "work-group; the reference's sequential fp32 sums and walks "
+                        "reproduced bit for bit by integer prefix sums on the running "
+                        "sum's binade grid); GPU us per call", "results": out,
             "check": {"checked": bool(ok), "bar": "token equal to a host evaluation"}}
 
 

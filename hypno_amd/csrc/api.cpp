@@ -701,8 +701,8 @@ int hypno_hip_dequantize_q4_0_dev(float* out, const uint8_t* q, size_t q_len, vo
 struct hypno_hip_gemv_plan {
   struct Group {
     GemvGroupGeom geom;
-    GemvJob* d_jobs = nullptr;  // device table (njobs > 1)
-    GemvJob job0;
+    GemvJob* d_jobs = nullptr;  // device table (njobs > kGemvInline)
+    GemvJob inl[kGemvInline];   // the first jobs (all of them up to kGemvInline)
     int njobs = 0;
     int total_steps = 0;
   };
@@ -724,6 +724,14 @@ namespace {
 int close_group(hypno_hip_gemv_plan* pl, hypno_hip_gemv_plan::Group& grp,
                 std::vector<GemvJob>& jobs) {
   if (jobs.empty()) return HYPNO_HIP_OK;
+  {
+    std::vector<int> ns, bs;
+    for (const GemvJob& j : jobs) {
+      ns.push_back(j.n);
+      bs.push_back(j.B);
+    }
+    gemv_group_widen(grp.geom, ns.data(), bs.data(), (int)jobs.size(), pl->cus);
+  }
   long long step = 0;
   for (GemvJob& j : jobs) {
     j.rps = grp.geom.T / j.B;
@@ -733,8 +741,8 @@ int close_group(hypno_hip_gemv_plan* pl, hypno_hip_gemv_plan::Group& grp,
   if (step > 0x7FFFFFFF) return fail(HYPNO_HIP_EINVAL, "plan: too many rows in one group");
   grp.njobs = (int)jobs.size();
   grp.total_steps = (int)step;
-  grp.job0 = jobs[0];
-  if (grp.njobs > 1) {
+  for (int i = 0; i < kGemvInline && i < grp.njobs; i++) grp.inl[i] = jobs[i];
+  if (grp.njobs > kGemvInline) {
     hipError_t e = hipMalloc(&grp.d_jobs, jobs.size() * sizeof(GemvJob));
     if (e != hipSuccess) return hip_fail(e, "plan: job table");
     e = hipMemcpy(grp.d_jobs, jobs.data(), jobs.size() * sizeof(GemvJob), hipMemcpyHostToDevice);
@@ -906,7 +914,7 @@ int hypno_hip_q4_0_gemv_plan_run(const hypno_hip_gemv_plan* plan, void* stream) 
   if (!plan) return fail(HYPNO_HIP_EINVAL, "plan_run: NULL plan");
   hipStream_t s = (hipStream_t)stream;
   for (const auto& g : plan->groups) {
-    hipError_t e = launch_q4_0_gemv_group(g.geom, g.d_jobs, g.job0, g.njobs, g.total_steps,
+    hipError_t e = launch_q4_0_gemv_group(g.geom, g.d_jobs, g.inl, g.njobs, g.total_steps,
                                           plan->cus, s);
     if (e != hipSuccess) return hip_fail(e, "plan_run: GEMV launch");
   }

@@ -272,9 +272,17 @@ struct GemvGroupGeom {
   size_t lds = 0;
 };
 
+// A launch that the staging rule holds to at most one work-group per CU
+// gets wider work-groups (more waves per CU streaming and computing): the
+// largest T (a multiple of Tbase, up to 1024) that still gives every CU a
+// step.  Jobs (n rows, B blocks per row) must take their rps / step0 after.
+void gemv_group_widen(GemvGroupGeom& g, const int* n, const int* B, int count, int num_cus);
+
+constexpr int kGemvInline = 4;  // jobs a launch carries in its arguments
+
 struct GemvLaunch {
-  const GemvJob* jobs;  // device table when njobs > 1
-  GemvJob job0;         // the job when njobs == 1
+  const GemvJob* jobs;           // device table when njobs > kGemvInline
+  GemvJob inl[kGemvInline];      // the jobs when njobs <= kGemvInline
   int njobs;
   int total_steps;
   int S;
@@ -283,8 +291,10 @@ struct GemvLaunch {
 
 // Adds a job with m columns to group g if the shared shape still fits.
 bool gemv_group_add(GemvGroupGeom& g, size_t m);
+// h_jobs: the first min(njobs, kGemvInline) jobs (host memory); d_jobs: all
+// of them in device memory when njobs > kGemvInline.
 hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
-                                  const GemvJob& job0, int njobs, int total_steps, int num_cus,
+                                  const GemvJob* h_jobs, int njobs, int total_steps, int num_cus,
                                   hipStream_t s);
 
 // MFMA prefill GEMM.  Requires m % 64 == 0, w 4-byte aligned, w_len full.

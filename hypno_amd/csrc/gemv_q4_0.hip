@@ -188,9 +188,11 @@ static int job_threads(int B) {
   return l <= 1024 ? l : -1;
 }
 
-static void finish_geometry(GemvGroupGeom& g) {
-  g.T = g.Tbase;
-  while (g.T < 256 && 2 * g.T <= 1024) g.T *= 2;
+// T: the threads per work-group (a multiple of Tbase up to 1024); 0 picks
+// Tbase doubled up to at least 256.
+static void finish_geometry(GemvGroupGeom& g, int T = 0) {
+  g.T = T > 0 ? T : g.Tbase;
+  while (T <= 0 && g.T < 256 && 2 * g.T <= 1024) g.T *= 2;
   g.W = g.T / 64;
   g.S = 64;
   const size_t loop = (size_t)g.S * (g.T / 8) * 4;  // 8-lane group partials
@@ -221,6 +223,38 @@ bool gemv_group_add(GemvGroupGeom& g, size_t m) {
   if (t.lds > kMaxLds) return false;
   g = t;
   return true;
+}
+
+// Work-groups a launch runs at most, per CU, by the staging rule below
+// (launch_q4_0_gemv_group): every work-group stages the whole x, so each
+// should stream at least about twice that in weights.
+static long long gemv_per_cu(const GemvGroupGeom& g, long long wbytes, int num_cus) {
+  const long long stage = 4LL * kBlockElems * g.maxB * (g.pro ? 2 : 1);
+  const long long ws = wbytes / (2 * stage);
+  const long long per = (ws + num_cus / 2) / num_cus;
+  return per > 1 ? per : 1;
+}
+
+void gemv_group_widen(GemvGroupGeom& g, const int* n, const int* B, int count, int num_cus) {
+  const int bytes = g.fmt == kFmtQ8_0 ? Fmt<kFmtQ8_0>::kBytes : kBlockBytes;
+  long long wbytes = 0;
+  for (int i = 0; i < count; i++) wbytes += (long long)n[i] * B[i] * bytes;
+  if (gemv_per_cu(g, wbytes, num_cus) > 1) return;
+  int top = g.Tbase;
+  while (2 * top <= 1024) top *= 2;
+  for (int T = top; T > g.T; T /= 2) {
+    long long steps = 0;
+    for (int i = 0; i < count; i++) {
+      const int rps = T / B[i];
+      steps += (n[i] + rps - 1) / rps;
+    }
+    if (steps < num_cus) continue;
+    GemvGroupGeom t = g;
+    finish_geometry(t, T);
+    if (t.lds > kMaxLds) continue;
+    g = t;
+    return;
+  }
 }
 
 bool q4_0_gemv_fast_ok(const uint8_t* w, size_t w_len, size_t n, size_t m) {
@@ -288,15 +322,21 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
   const int T = blockDim.x;
   const int t = threadIdx.x;
   const int G = L.total_steps;
-  const int s_begin = (int)((long long)G * blockIdx.x / gridDim.x);
-  const int s_end = (int)((long long)G * (blockIdx.x + 1) / gridDim.x);
+  const uint32_t gd = gridDim.x, gb = blockIdx.x;
+  const bool narrow = (uint32_t)G <= 0xFFFFFFFFu / gd;  // G * gd fits 32 bits
+  const int s_begin = narrow ? (int)((uint32_t)G * gb / gd)
+                             : (int)((unsigned long long)G * gb / gd);
+  const int s_end = narrow ? (int)((uint32_t)G * (gb + 1) / gd)
+                           : (int)((unsigned long long)G * (gb + 1) / gd);
   if (s_begin >= s_end) return;  // whole work-group
 
+  // Jobs come from the launch's arguments (up to kGemvInline of them), else
+  // from the device table.
+  const bool inl = L.njobs <= kGemvInline;
   auto get = [&](int j) -> GemvJob {
-    return L.njobs == 1 ? L.job0 : load_const<GemvJob>(L.jobs + j);
+    return inl ? L.inl[j] : load_const<GemvJob>(L.jobs + j);
   };
-  auto cursor_at = [&](int j, int g) {
-    const GemvJob J = get(j);
+  auto cursor_of = [&](const GemvJob& J, int j, int g) {
     const int steps = job_steps(J);
     RingCursor c;
     c.bps = J.rps * J.B * FT::kBytes;
@@ -306,9 +346,15 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
     c.j = j;
     return c;
   };
+  auto cursor_at = [&](int j, int g) { return cursor_of(get(j), j, g); };
   // First job of this work-group's range (binary search on step0).
   int j0 = 0;
-  if (L.njobs > 1) {
+  if (inl) {
+    // step0 rises with the job: j0 counts the later jobs starting at or
+    // before s_begin (constant indices, so the loads go out together)
+#pragma unroll
+    for (int k = 1; k < kGemvInline; k++) j0 += (k < L.njobs && L.inl[k].step0 <= s_begin) ? 1 : 0;
+  } else {
     int lo = 0, hi = L.njobs - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -318,6 +364,34 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
         hi = mid - 1;
     }
     j0 = lo;
+  }
+  // The first job's activations (and prologue operand), element groups
+  // i = t + p T for p < kPre, are read now, before anything waits on memory:
+  // their latency runs alongside the weight ring's first fetches.
+  constexpr int kPre = 2;
+  GemvJob J0;
+  if (inl) {  // constant indices again: no load waits on j0
+    J0 = L.inl[0];
+#pragma unroll
+    for (int k = 1; k < kGemvInline; k++)
+      if (k == j0) J0 = L.inl[k];
+  } else {
+    J0 = load_const<GemvJob>(L.jobs + j0);
+  }
+  float xpre[kPre][8], apre[kPre][8] = {};
+  auto load8 = [&](const float4* p, int i, float* o) __attribute__((always_inline)) {
+    const float4 v0 = load_global<float4>(p + 2 * i);
+    const float4 v1 = load_global<float4>(p + 2 * i + 1);
+    o[0] = v0.x; o[1] = v0.y; o[2] = v0.z; o[3] = v0.w;
+    o[4] = v1.x; o[5] = v1.y; o[6] = v1.z; o[7] = v1.w;
+  };
+#pragma unroll
+  for (int p = 0; p < kPre; p++) {
+    const int i = t + p * T;
+    if (i < J0.B * 4) {
+      load8(reinterpret_cast<const float4*>(J0.x), i, xpre[p]);
+      if (PRO && J0.pro != kProNone) load8(reinterpret_cast<const float4*>(J0.aux), i, apre[p]);
+    }
   }
 
   // The weights stream through a ring of R step spans per wave in LDS, filled
@@ -337,7 +411,7 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
   const int lane = t & 63;
   const int wv = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform
   uint8_t* ring = smem + L.ring_off + (size_t)wv * (R * kSpan);
-  RingCursor pc = cursor_at(j0, s_begin);
+  RingCursor pc = cursor_of(J0, j0, s_begin);
   int pg = s_begin;  // next step the ring fetches
   const uint8_t* wsafe = pc.next;
   const uint32_t dma_off = (uint32_t)(wv * kSpan + 16 * lane);
@@ -444,8 +518,8 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
   // element in registers (the RMS sum: per-thread FMA chains, wave sums, then
   // the waves' sums in a fixed order, so every work-group gets the same
   // scale).
-  auto enter = [&](int j, int g) __attribute__((always_inline)) {
-    J = get(j);
+  auto enter = [&](int j, int g, bool first) __attribute__((always_inline)) {
+    J = first ? J0 : get(j);
     cj = j;
     const int steps = job_steps(J);
     seg_end = min(s_end, J.step0 + steps);
@@ -455,11 +529,19 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
     int* exps = reinterpret_cast<int*>(smem + (size_t)kLimbs * kLD * 4 * B);
     const float4* xv = reinterpret_cast<const float4*>(J.x);
     const float4* av = reinterpret_cast<const float4*>(J.aux);
-    auto load8 = [&](const float4* p, int i, float* o) __attribute__((always_inline)) {
-      const float4 v0 = load_global<float4>(p + 2 * i);
-      const float4 v1 = load_global<float4>(p + 2 * i + 1);
-      o[0] = v0.x; o[1] = v0.y; o[2] = v0.z; o[3] = v0.w;
-      o[4] = v1.x; o[5] = v1.y; o[6] = v1.z; o[7] = v1.w;
+    // element group i's x (and prologue operand): from the registers read
+    // at the start for the first job's first kPre rounds
+    auto get8 = [&](int i, int p, float* xs, float* as) __attribute__((always_inline)) {
+      if (first && p < kPre) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          xs[k] = xpre[p][k];
+          if (PRO) as[k] = apre[p][k];
+        }
+      } else {
+        load8(xv, i, xs);
+        if (PRO && J.pro != kProNone) load8(av, i, as);
+      }
     };
     auto sumsq8 = [&](const float* xs, float ss) __attribute__((always_inline)) {
 #pragma unroll
@@ -495,21 +577,41 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
       uint32_t mb = 0;
 #pragma unroll
       for (int k = 0; k < 8; k++) mb = max(mb, __float_as_uint(xs[k]) & 0x7FFFFFFFu);
-      mb = max(mb, (uint32_t)__shfl_xor((int)mb, 1, 64));
-      mb = max(mb, (uint32_t)__shfl_xor((int)mb, 2, 64));
+      // the block's four lanes (a quad): DPP quad_perm [1,0,3,2], then [2,3,0,1]
+      mb = max(mb, (uint32_t)__builtin_amdgcn_mov_dpp((int)mb, 0xB1, 0xF, 0xF, false));
+      mb = max(mb, (uint32_t)__builtin_amdgcn_mov_dpp((int)mb, 0x4E, 0xF, 0xF, false));
       const int e = __builtin_amdgcn_frexp_expf(__uint_as_float(mb));  // amax < 2^e
       uint32_t u[8];
 #pragma unroll
       for (int k = 0; k < 8; k++)
         u[k] = (uint32_t)((int)rintf(ldexpf(xs[k], kMantBits - e)) + kDigitBias);
       if constexpr (F == kFmtQ4_0) {
+        // Plane l holds digit l (bits 4l..4l+3) of the 8 values, value k in
+        // nibble k.  Per pair (u[2p], u[2p+1]): e_p bytes 0..2 = digits 0, 2,
+        // 4 of both (low nibble the even value), o_p bytes 0..1 = digits 1,
+        // 3; then v_perm_b32 gathers byte b of the four pairs into a plane.
+        static_assert(kLimbs == 5, "five 4-bit digits");
+        uint32_t e[4], o[4];
 #pragma unroll
-        for (int l = 0; l < kLimbs; l++) {
-          uint32_t w = 0;
-#pragma unroll
-          for (int k = 0; k < 8; k++) w |= ((u[k] >> (4 * l)) & 15u) << (4 * k);
-          limbs[(l * B * 4) + i] = w ^ 0x88888888u;
+        for (int q = 0; q < 4; q++) {
+          const uint32_t a = u[2 * q], b = u[2 * q + 1];
+          e[q] = (a & 0x000F0F0Fu) | ((b & 0x000F0F0Fu) << 4);
+          o[q] = ((a >> 4) & 0x00000F0Fu) | (b & 0x0000F0F0u);
         }
+        // bytes [x0.b0, x1.b0, x0.b1, x1.b1] of (x1:x0), and the same of the
+        // odd pair; then [lo.b0, lo.b1, hi.b0, hi.b1] / [lo.b2, lo.b3, hi.b2, hi.b3]
+        const uint32_t ea = __builtin_amdgcn_perm(e[1], e[0], 0x05010400u);
+        const uint32_t eb = __builtin_amdgcn_perm(e[3], e[2], 0x05010400u);
+        const uint32_t ec = __builtin_amdgcn_perm(e[1], e[0], 0x0C0C0602u);
+        const uint32_t ed = __builtin_amdgcn_perm(e[3], e[2], 0x0C0C0602u);
+        const uint32_t oa = __builtin_amdgcn_perm(o[1], o[0], 0x05010400u);
+        const uint32_t ob = __builtin_amdgcn_perm(o[3], o[2], 0x05010400u);
+        const uint32_t plane[kLimbs] = {
+            __builtin_amdgcn_perm(eb, ea, 0x05040100u), __builtin_amdgcn_perm(ob, oa, 0x05040100u),
+            __builtin_amdgcn_perm(eb, ea, 0x07060302u), __builtin_amdgcn_perm(ob, oa, 0x07060302u),
+            __builtin_amdgcn_perm(ed, ec, 0x05040100u)};
+#pragma unroll
+        for (int l = 0; l < kLimbs; l++) limbs[(l * B * 4) + i] = plane[l] ^ 0x88888888u;
       } else {
 #pragma unroll
         for (int l = 0; l < kLimbs; l++) {
@@ -528,23 +630,33 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
     float inv_rms = 1.0f;
     if (PRO && J.pro == kProRmsNorm) {
       float ss = 0.0f;
-      for (int i = t; i < B * 4; i += T) {
+#pragma unroll
+      for (int p = 0; p < kPre; p++) {
+        const int i = t + p * T;
+        if (i < B * 4) {
+          float xs[8], as[8];
+          get8(i, p, xs, as);
+          ss = sumsq8(xs, ss);
+        }
+      }
+      for (int i = t + kPre * T; i < B * 4; i += T) {
         float xs[8];
         load8(xv, i, xs);
         ss = sumsq8(xs, ss);
       }
       inv_rms = inv_rms_of(ss);
     }
-    for (int i = t; i < B * 4; i += T) {  // whole 4-thread groups stay together
-      float xs[8];
-      load8(xv, i, xs);
-      if constexpr (PRO) {
-        float as[8];
-        if (J.pro != kProNone) load8(av, i, as);
-        prologue(xs, as, inv_rms);
-      }
+    // whole 4-thread groups stay together (T is a multiple of 64)
+    auto round = [&](int i, int p) __attribute__((always_inline)) {
+      float xs[8], as[8];
+      get8(i, p, xs, as);
+      if constexpr (PRO) prologue(xs, as, inv_rms);
       convert(i, xs);
-    }
+    };
+#pragma unroll
+    for (int p = 0; p < kPre; p++)
+      if (t + p * T < B * 4) round(t + p * T, p);
+    for (int i = t + kPre * T; i < B * 4; i += T) round(i, kPre);
     __syncthreads();
     const int kb = t % B;
 #pragma unroll
@@ -563,7 +675,7 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
   auto step = [&](int ss, int slot) {
     if (ss == seg_end) {
       flush(ss);
-      enter(cj + 1, ss);
+      enter(cj + 1, ss, false);
     } else if (ss == c0 + L.S) {
       flush(ss);
       c0 = ss;
@@ -618,7 +730,7 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
     if ((t & 7) == 7) part[(ss - c0) * T8 + (t >> 3)] = partial;
   };
 
-  enter(j0, s_begin);
+  enter(j0, s_begin, true);
   int slot = 0;
   for (int ss = s_begin; ss < s_end; ss++) {
     step(ss, slot);
@@ -643,19 +755,31 @@ __global__ void __launch_bounds__(1024) q8_0_gemv_jobs_kernel(GemvLaunch L) {
   gemv_jobs_body<kFmtQ8_0, false, R>(L);
 }
 
+template <int R>
+static const void* gemv_kernel_r(int which) {
+  return which == 2   ? reinterpret_cast<const void*>(q8_0_gemv_jobs_kernel<R>)
+         : which == 1 ? reinterpret_cast<const void*>(q4_0_gemv_jobs_pro_kernel<R>)
+                      : reinterpret_cast<const void*>(q4_0_gemv_jobs_kernel<R>);
+}
+
+// Ring depths built: 2 and 3 for work-groups that share a CU, deeper ones for
+// launches of at most one work-group per CU.
+static const void* gemv_kernel(int which, int R) {
+  switch (R) {
+    case 8: return gemv_kernel_r<8>(which);
+    case 6: return gemv_kernel_r<6>(which);
+    case 4: return gemv_kernel_r<4>(which);
+    case 3: return gemv_kernel_r<3>(which);
+    default: return gemv_kernel_r<2>(which);
+  }
+}
+
 hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
-                                  const GemvJob& job0, int njobs, int total_steps, int num_cus,
+                                  const GemvJob* h_jobs, int njobs, int total_steps, int num_cus,
                                   hipStream_t s) {
   const bool q8 = g.fmt == kFmtQ8_0;
   const int which = q8 ? 2 : (g.pro ? 1 : 0);
-  const bool r3 = g.ring == 3;
-  const void* kern =
-      which == 2 ? (r3 ? reinterpret_cast<const void*>(q8_0_gemv_jobs_kernel<3>)
-                       : reinterpret_cast<const void*>(q8_0_gemv_jobs_kernel<2>))
-      : which == 1 ? (r3 ? reinterpret_cast<const void*>(q4_0_gemv_jobs_pro_kernel<3>)
-                         : reinterpret_cast<const void*>(q4_0_gemv_jobs_pro_kernel<2>))
-                   : (r3 ? reinterpret_cast<const void*>(q4_0_gemv_jobs_kernel<3>)
-                         : reinterpret_cast<const void*>(q4_0_gemv_jobs_kernel<2>));
+  const void* kern = gemv_kernel(which, g.ring);
   {
     hipError_t e = set_lds_limit(kern, (int)kMaxLds);
     if (e != hipSuccess) return e;
@@ -676,21 +800,39 @@ hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
   {
     const long long wbytes =
         (long long)total_steps * g.T * (q8 ? Fmt<kFmtQ8_0>::kBytes : kBlockBytes);
-    const long long stage = 4LL * kBlockElems * g.maxB * (g.pro ? 2 : 1);
-    const long long ws = wbytes / (2 * stage);
-    const int per = (int)((ws + num_cus / 2) / num_cus);
-    const int cap = (per > 1 ? per : 1) * num_cus;
-    if (grid > cap) grid = cap;
+    const long long cap = gemv_per_cu(g, wbytes, num_cus) * num_cus;
+    if (grid > cap) grid = (int)cap;
+  }
+  // At most one work-group per CU: LDS has room for a deeper ring, which
+  // keeps more of the work-group's weights in flight (a small matrix's
+  // stream is otherwise bound by the bytes each CU has in flight); up to one
+  // slot per step the work-group streams.
+  size_t lds = g.lds;
+  if (grid <= num_cus) {
+    const int per_wg = (total_steps + grid - 1) / grid;
+    const size_t span = 64 * (size_t)(q8 ? Fmt<kFmtQ8_0>::kBytes : kBlockBytes);
+    int R = g.ring;
+    for (int cand : {4, 6, 8}) {
+      if (R >= per_wg) break;
+      if (g.ring_off + (size_t)g.W * cand * span > kMaxLds) break;
+      R = cand;
+    }
+    if (R != g.ring) {
+      kern = gemv_kernel(which, R);
+      hipError_t e = set_lds_limit(kern, (int)kMaxLds);
+      if (e != hipSuccess) return e;
+      lds = g.ring_off + (size_t)g.W * R * span;
+    }
   }
   GemvLaunch L;
   L.jobs = d_jobs;
-  L.job0 = job0;
+  for (int i = 0; i < kGemvInline; i++) L.inl[i] = h_jobs[i < njobs ? i : 0];
   L.njobs = njobs;
   L.total_steps = total_steps;
   L.S = g.S;
   L.ring_off = (int)g.ring_off;
   hipLaunchKernelGGL(reinterpret_cast<void (*)(GemvLaunch)>(const_cast<void*>(kern)), dim3(grid),
-                     dim3(g.T), g.lds, s, L);
+                     dim3(g.T), lds, s, L);
   return hipGetLastError();
 }
 
@@ -700,6 +842,10 @@ static hipError_t launch_gemv_fast(int fmt, float* y, const uint8_t* w, const fl
   GemvGroupGeom g;
   g.fmt = fmt;
   gemv_group_add(g, m);
+  {
+    const int nn = (int)n, BB = (int)(m / 32);
+    gemv_group_widen(g, &nn, &BB, 1, num_cus);
+  }
   GemvJob J;
   J.w = w;
   J.x = x;
@@ -713,7 +859,7 @@ static hipError_t launch_gemv_fast(int fmt, float* y, const uint8_t* w, const fl
   J.rps = g.T / J.B;
   J.step0 = 0;
   const int steps = (J.n + J.rps - 1) / J.rps;
-  return launch_q4_0_gemv_group(g, nullptr, J, 1, steps, num_cus, s);
+  return launch_q4_0_gemv_group(g, nullptr, &J, 1, steps, num_cus, s);
 }
 
 hipError_t launch_q4_0_gemv_fast(float* y, const uint8_t* w, const float* x, const float* bias,
