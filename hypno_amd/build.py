@@ -41,6 +41,15 @@ COMMON_FLAGS = [
     f"-I{os.path.join(ROOT, 'include')}",
 ]
 
+# Per-source additions.  The streaming GEMV's leading scalar arguments (the
+# first job and the launch shape, 14 SGPRs) are preloaded into SGPRs, so a
+# work-group starts its first reads without waiting on kernel-argument
+# memory; the compiler keeps a prologue that loads them for firmware that
+# does not preload.
+FILE_FLAGS = {
+    "gemv_q4_0.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=11"],
+}
+
 
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
@@ -58,7 +67,8 @@ def _quiet(text: str) -> str:
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".o")
     lang = ["-x", "hip"]
-    cmd = [hipcc()] + lang + COMMON_FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = ([hipcc()] + lang + COMMON_FLAGS + FILE_FLAGS.get(src, []) +
+           ["-c", os.path.join(CSRC, src), "-o", obj])
     p = subprocess.run(cmd, capture_output=True, text=True)
     out = _quiet(p.stdout + p.stderr)
     if p.returncode != 0:

@@ -311,18 +311,29 @@ __device__ __forceinline__ int sdot8_first(uint32_t a, uint32_t b) {
 
 // PRO: some job of the launch has a prologue (a separate instantiation, so
 // launches without one keep the smaller staging code and register budget).
+// The launch's leading kernel arguments, preloaded into SGPRs (the build
+// preloads this file's first 11 arguments: these, in this order, 14 SGPRs):
+// the launch shape and the first job's streaming fields.  aux0 is null
+// unless job 0 has a prologue.
+struct GemvHead {
+  int total_steps, grid, T, ring_off, njobs, n0, B0, rps0;
+  const uint8_t* w0;
+  const float* x0;
+  const float* aux0;
+};
+
 template <int F, bool PRO, int R>
-__device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
+__device__ __forceinline__ void gemv_jobs_body(const GemvHead& H, const GemvLaunch& L) {
   using FT = Fmt<F>;
   constexpr int kLimbs = FT::kLimbs;
   constexpr int kLD = FT::kLimbDwords;
   constexpr int kMantBits = FT::kMantBits;
   constexpr int kDigitBias = FT::kDigitBias;
   extern __shared__ __align__(16) uint8_t smem[];
-  const int T = blockDim.x;
+  const int T = H.T;
   const int t = threadIdx.x;
-  const int G = L.total_steps;
-  const uint32_t gd = gridDim.x, gb = blockIdx.x;
+  const int G = H.total_steps;
+  const uint32_t gd = (uint32_t)H.grid, gb = blockIdx.x;
   const bool narrow = (uint32_t)G <= 0xFFFFFFFFu / gd;  // G * gd fits 32 bits
   const int s_begin = narrow ? (int)((uint32_t)G * gb / gd)
                              : (int)((unsigned long long)G * gb / gd);
@@ -332,7 +343,7 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
 
   // Jobs come from the launch's arguments (up to kGemvInline of them), else
   // from the device table.
-  const bool inl = L.njobs <= kGemvInline;
+  const bool inl = H.njobs <= kGemvInline;
   auto get = [&](int j) -> GemvJob {
     return inl ? L.inl[j] : load_const<GemvJob>(L.jobs + j);
   };
@@ -353,9 +364,9 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
     // step0 rises with the job: j0 counts the later jobs starting at or
     // before s_begin (constant indices, so the loads go out together)
 #pragma unroll
-    for (int k = 1; k < kGemvInline; k++) j0 += (k < L.njobs && L.inl[k].step0 <= s_begin) ? 1 : 0;
+    for (int k = 1; k < kGemvInline; k++) j0 += (k < H.njobs && L.inl[k].step0 <= s_begin) ? 1 : 0;
   } else {
-    int lo = 0, hi = L.njobs - 1;
+    int lo = 0, hi = H.njobs - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
       if (load_const<int>(&L.jobs[mid].step0) <= s_begin)
@@ -378,6 +389,22 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
   } else {
     J0 = load_const<GemvJob>(L.jobs + j0);
   }
+  // What the first reads need, from the preloaded head for job 0 (a uniform
+  // branch: that path waits on no argument memory)
+  GemvJob F0;
+  const float* aux_first;
+  if (j0 == 0) {
+    F0.w = H.w0;
+    F0.x = H.x0;
+    F0.n = H.n0;
+    F0.B = H.B0;
+    F0.rps = H.rps0;
+    F0.step0 = 0;
+    aux_first = H.aux0;
+  } else {
+    F0 = J0;
+    aux_first = J0.pro != kProNone ? J0.aux : nullptr;
+  }
   float xpre[kPre][8], apre[kPre][8] = {};
   auto load8 = [&](const float4* p, int i, float* o) __attribute__((always_inline)) {
     const float4 v0 = load_global<float4>(p + 2 * i);
@@ -388,9 +415,9 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
 #pragma unroll
   for (int p = 0; p < kPre; p++) {
     const int i = t + p * T;
-    if (i < J0.B * 4) {
-      load8(reinterpret_cast<const float4*>(J0.x), i, xpre[p]);
-      if (PRO && J0.pro != kProNone) load8(reinterpret_cast<const float4*>(J0.aux), i, apre[p]);
+    if (i < F0.B * 4) {
+      load8(reinterpret_cast<const float4*>(F0.x), i, xpre[p]);
+      if (PRO && aux_first != nullptr) load8(reinterpret_cast<const float4*>(aux_first), i, apre[p]);
     }
   }
 
@@ -410,8 +437,8 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
   constexpr int kDmaPerStep = kFull + 1;
   const int lane = t & 63;
   const int wv = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform
-  uint8_t* ring = smem + L.ring_off + (size_t)wv * (R * kSpan);
-  RingCursor pc = cursor_of(J0, j0, s_begin);
+  uint8_t* ring = smem + H.ring_off + (size_t)wv * (R * kSpan);
+  RingCursor pc = cursor_of(F0, j0, s_begin);
   int pg = s_begin;  // next step the ring fetches
   const uint8_t* wsafe = pc.next;
   const uint32_t dma_off = (uint32_t)(wv * kSpan + 16 * lane);
@@ -740,19 +767,25 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvLaunch& L) {
   flush(s_end);
 }
 
+#define GEMV_HEAD_PARAMS                                                                   \
+  int total_steps, int grid, int T, int ring_off, int njobs, int n0, int B0, int rps0,      \
+      const uint8_t *w0, const float *x0, const float *aux0
+#define GEMV_HEAD_ARGS \
+  GemvHead { total_steps, grid, T, ring_off, njobs, n0, B0, rps0, w0, x0, aux0 }
+
 template <int R>
-__global__ void __launch_bounds__(1024) q4_0_gemv_jobs_kernel(GemvLaunch L) {
-  gemv_jobs_body<kFmtQ4_0, false, R>(L);
+__global__ void __launch_bounds__(1024) q4_0_gemv_jobs_kernel(GEMV_HEAD_PARAMS, GemvLaunch L) {
+  gemv_jobs_body<kFmtQ4_0, false, R>(GEMV_HEAD_ARGS, L);
 }
 
 template <int R>
-__global__ void __launch_bounds__(1024) q4_0_gemv_jobs_pro_kernel(GemvLaunch L) {
-  gemv_jobs_body<kFmtQ4_0, true, R>(L);
+__global__ void __launch_bounds__(1024) q4_0_gemv_jobs_pro_kernel(GEMV_HEAD_PARAMS, GemvLaunch L) {
+  gemv_jobs_body<kFmtQ4_0, true, R>(GEMV_HEAD_ARGS, L);
 }
 
 template <int R>
-__global__ void __launch_bounds__(1024) q8_0_gemv_jobs_kernel(GemvLaunch L) {
-  gemv_jobs_body<kFmtQ8_0, false, R>(L);
+__global__ void __launch_bounds__(1024) q8_0_gemv_jobs_kernel(GEMV_HEAD_PARAMS, GemvLaunch L) {
+  gemv_jobs_body<kFmtQ8_0, false, R>(GEMV_HEAD_ARGS, L);
 }
 
 template <int R>
@@ -831,8 +864,12 @@ hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
   L.total_steps = total_steps;
   L.S = g.S;
   L.ring_off = (int)g.ring_off;
-  hipLaunchKernelGGL(reinterpret_cast<void (*)(GemvLaunch)>(const_cast<void*>(kern)), dim3(grid),
-                     dim3(g.T), lds, s, L);
+  const GemvJob& J0 = h_jobs[0];
+  using Kern = void (*)(int, int, int, int, int, int, int, int, const uint8_t*, const float*,
+                        const float*, GemvLaunch);
+  hipLaunchKernelGGL(reinterpret_cast<Kern>(const_cast<void*>(kern)), dim3(grid), dim3(g.T), lds, s,
+                     total_steps, grid, g.T, (int)g.ring_off, njobs, J0.n, J0.B, J0.rps, J0.w, J0.x,
+                     J0.pro != kProNone ? J0.aux : nullptr, L);
   return hipGetLastError();
 }
 
