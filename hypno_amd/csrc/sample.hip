@@ -1047,6 +1047,87 @@ __device__ void sample_no_topk(const SampleArgs& a, SampleShared& sh) {
   if (t == 0) *a.token = am;
 }
 
+// Greedy argmax (Iterator::max_by over partial_cmp, as argmax_combine) in
+// one work-group and one launch: each thread reads the 16-byte pieces
+// r kST + t of the aligned body (coalesced, kB in flight), keeping the best
+// (value, the later index on ties) and whether it met a NaN; thread 0 also
+// takes the elements before the first 16-byte boundary and after the last.
+// A NaN anywhere (rare) sends the work-group to the exact scan: the last
+// NaN, then the best after it.
+__global__ void __launch_bounds__(kST) argmax_one_kernel(const float* __restrict__ x, int n,
+                                                         uint32_t* token) {
+  __shared__ SampleShared sh;
+  const int t = threadIdx.x, lane = t & 63;
+  if (n <= 0) {
+    if (t == 0) *token = 0u;
+    return;
+  }
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(x);
+  const int head = min(n, (int)(((16u - (addr & 15u)) & 15u) >> 2));
+  const int nv = (n - head) >> 2;  // 16-byte pieces
+  const float4* x4 = reinterpret_cast<const float4*>(x + head);
+  float bv = 0.0f;
+  int bi = -1;
+  int nan = 0;
+  auto take = [&](float v, int i) {
+    nan |= v != v;
+    if (bi < 0 || v >= bv) {  // indices grow per thread: ties go to the later
+      bv = v;
+      bi = i;
+    }
+  };
+  if (t == 0)
+    for (int i = 0; i < head; i++) take(x[i], i);
+  constexpr int kB = 16;
+  for (int r0 = 0; r0 * kST < nv; r0 += kB) {
+    float4 v[kB];
+#pragma unroll
+    for (int u = 0; u < kB; u++) v[u] = x4[min((r0 + u) * kST + t, nv - 1)];  // in bounds
+#pragma unroll
+    for (int u = 0; u < kB; u++) {
+      const int p = (r0 + u) * kST + t;
+      if (p < nv) {
+        const int i = head + 4 * p;
+        take(v[u].x, i);
+        take(v[u].y, i + 1);
+        take(v[u].z, i + 2);
+        take(v[u].w, i + 3);
+      }
+    }
+  }
+  if (t == 0)
+    for (int i = head + 4 * nv; i < n; i++) take(x[i], i);
+  if (__syncthreads_or(nan)) {
+    const ArgPart p = argmax_part(0, n, [&](int i) { return x[i]; }, sh);
+    if (t == 0) *token = argmax_combine(&p, 1, n);
+    return;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    if (arg_better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    sh.fred[t >> 6] = bv;
+    sh.ired[t >> 6] = bi;
+  }
+  __syncthreads();
+  if (t == 0) {
+    float fv = 0.0f;
+    int fi = -1;
+    for (int w = 0; w < kSW; w++)
+      if (arg_better(sh.fred[w], sh.ired[w], fv, fi)) {
+        fv = sh.fred[w];
+        fi = sh.ired[w];
+      }
+    *token = (uint32_t)fi;
+  }
+}
+
 // Second kernel, one work-group: the rest of sample_token.
 __global__ void __launch_bounds__(kST) sample_token_kernel(const SampleArgs a) {
   __shared__ SampleShared sh;
@@ -1276,6 +1357,10 @@ hipError_t launch_sample_token(uint32_t* token, uint64_t* state, const float* lo
   a.parts = sample_parts(n);
   a.token = token;
   a.state = state;
+  if (greedy && (reinterpret_cast<uintptr_t>(logits) & 3u) == 0) {
+    hipLaunchKernelGGL(argmax_one_kernel, dim3(1), dim3(kST), 0, s, logits, (int)n, token);
+    return hipGetLastError();
+  }
   uint8_t* w = static_cast<uint8_t*>(ws);
   const size_t parts_b = round_up256(kMaxParts * sizeof(ArgPart));
   const size_t plane = round_up256(n * 4);

@@ -135,6 +135,45 @@ def test_argmax(env, orc):
     assert int(out.item()) == 0
 
 
+
+def test_argmax_unaligned_and_edges(env, orc):
+    """One-launch greedy argmax: starts 0-3 floats past a 16-byte boundary
+    (the leading elements and the tail are read one by one), ties between
+    the leading elements, the 16-byte body and the tail, signed zeros, all
+    -inf, short lengths, and a NaN (the exact scan)."""
+    torch, hk, lib = env
+    rng = np.random.default_rng(66)
+    base = torch.from_numpy(rng.standard_normal(VOCAB + 8).astype(np.float32)).cuda()
+    for off in range(4):
+        for n in (1, 2, 3, 5, 7, 4099, VOCAB):
+            src = base[off:off + n].clone()
+            for variant in range(4):
+                c = src.clone()
+                if variant == 1 and n > 2:   # the same maximum at the start, middle and end
+                    c[[0, n // 2, n - 1]] = 9.0
+                elif variant == 2:           # +0 and -0 tie: the later index
+                    c[:] = -1.0
+                    c[0] = 0.0
+                    c[n - 1] = -0.0
+                elif variant == 3:
+                    c[:] = -float("inf")
+                buf = torch.empty(n + off, device="cuda")
+                buf[off:] = c
+                view = buf[off:]
+                assert view.data_ptr() % 16 == (4 * off) % 16
+                got = hk.argmax(view)
+                torch.cuda.synchronize()
+                want = orc.argmax(view.cpu().numpy())
+                assert int(got.item()) == want, (off, n, variant)
+    c = base[1:VOCAB + 1].clone()
+    c[77777] = float("nan")
+    buf = torch.empty(VOCAB + 1, device="cuda")
+    buf[1:] = c
+    got = hk.argmax(buf[1:])
+    torch.cuda.synchronize()
+    assert int(got.item()) == orc.argmax(c.cpu().numpy())
+
+
 EXACT_CASES = [  # (top_p, top_k)
     (1.0, 0), (1.0, 40), (0.9, 0), (0.9, 40), (0.5, 1000), (0.95, 1), (0.999, 50000),
     # without top-k: the key bins from the top (0.5), and every p sorted
