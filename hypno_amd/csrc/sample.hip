@@ -461,14 +461,33 @@ __device__ void radix_sort_lds(int L, SampleShared& sh) {
   radix_sort_impl<true>(nullptr, nullptr, L, sh);
 }
 
+constexpr int kRankSortMax = 256;  // lists sorted by one rank pass
+
 // Sorts keys k0[0..L) ascending; returns where the result is: sh.sortb (the
-// keys copied there, L <= kSortCap) or k0 (a global sort through k1).
+// keys copied there, L <= kSortCap) or k0 (a global sort through k1).  Up to
+// kRankSortMax keys: thread t takes key t and places it at its rank (the
+// keys below it, and the equal ones before it).
 __device__ const uint32_t* sort_keys(uint32_t* k0, uint32_t* k1, int L, SampleShared& sh) {
   if (L > kSortCap) {
     radix_sort_keys(k0, k1, L, sh);
     return k0;
   }
   const int t = threadIdx.x;
+  if (L <= kRankSortMax) {
+    const uint32_t k = t < L ? k0[t] : 0u;
+    if (t < L) sh.sorta[t] = k;
+    __syncthreads();
+    if (t < L) {
+      int rank = 0;
+      for (int j = 0; j < L; j++) {
+        const uint32_t o = sh.sorta[j];  // the same address across the wave
+        rank += o < k || (o == k && j < t);
+      }
+      sh.sortb[rank] = k;
+    }
+    __syncthreads();
+    return sh.sortb;
+  }
   constexpr int kPer = kSortCap / kST;
   uint32_t v[kPer];
 #pragma unroll
@@ -1143,14 +1162,14 @@ __global__ void __launch_bounds__(kST) sample_token_kernel(const SampleArgs a) {
     return;
   }
   // the ranges' candidate lists, concatenated in order (index order), into
-  // k0 (indices) / k1 (values) for the top-k pass
-  if (t == 0) {
-    int run = 0;
-    for (int g = 0; g < a.parts; g++) {
-      sh.cnt[0][g] = (uint32_t)run;
-      run += a.seg_cnt[g];
-    }
-    sh.u[2] = (uint32_t)run;
+  // k0 (indices) / k1 (values) for the top-k pass; the ranges' offsets by
+  // one wave (lane g reads range g's count: parts <= 64), a DPP scan
+  static_assert(kMaxParts <= 64, "one lane per range");
+  if (t < 64) {
+    const uint32_t c = t < a.parts ? (uint32_t)a.seg_cnt[t] : 0u;
+    const uint32_t inc = wave_scan_sat(c);
+    sh.cnt[0][t] = inc - c;
+    if (t == 63) sh.u[2] = inc;
   }
   __syncthreads();
   const int C = (int)sh.u[2];
