@@ -121,34 +121,6 @@ __device__ __forceinline__ float funkey(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
-__device__ __forceinline__ uint32_t usat_add(uint32_t a, uint32_t b) {
-  return __builtin_elementwise_add_sat(a, b);
-}
-
-// d = v / u rounded to the nearest integer for v >= +0 finite, on the grid
-// u = 2^(E - 150) of exponent field E >= 1, with sc = 150 - E: v 2^sc is
-// exact (a power-of-two scaling; an overflow to inf only where v / u >=
-// 2^24, a result below 2^-126 only where v / u < 1/2: d = 0 either way); d
-// >= 2^24 is returned as 2^24 (the sum leaves the binade whatever m is).
-// tie: v / u is exactly halfway between two integers.
-__device__ __forceinline__ uint32_t acc_increment(float v, int sc, bool& tie) {
-  const float q = fminf(ldexpf(v, sc), 16777216.0f);  // NaN v: 2^24 (an event anyway)
-  tie = __builtin_amdgcn_fractf(q) == 0.5f;
-  return (uint32_t)__builtin_rintf(q);
-}
-
-// Inclusive scan of x over the wave (lane order), saturating at 2^32 - 1:
-// sums over 1, 2, 4, 8 lanes within each row of 16, then each row takes the
-// previous rows' total (row_bcast:15, row_bcast:31).
-__device__ __forceinline__ uint32_t wave_scan_sat(uint32_t x) {
-  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false));
-  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false));
-  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false));
-  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false));
-  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false));
-  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false));
-  return x;
-}
 
 // Argmax of one range of the logits: the last NaN in it (-1: none) and the
 // best (value, index) over the elements after that NaN, the later index among
@@ -210,6 +182,35 @@ struct SampleShared {
 };
 static_assert(sizeof(SampleShared) <= 160 * 1024, "LDS of a work-group");
 
+__device__ __forceinline__ uint32_t usat_add(uint32_t a, uint32_t b) {
+  return __builtin_elementwise_add_sat(a, b);
+}
+
+// d = v / u rounded to the nearest integer for v >= +0 finite, on the grid
+// u = 2^(E - 150) of exponent field E >= 1, with sc = 150 - E: v 2^sc is
+// exact (a power-of-two scaling; an overflow to inf only where v / u >=
+// 2^24, a result below 2^-126 only where v / u < 1/2: d = 0 either way); d
+// >= 2^24 is returned as 2^24 (the sum leaves the binade whatever m is).
+// tie: v / u is exactly halfway between two integers.
+__device__ __forceinline__ uint32_t acc_increment(float v, int sc, bool& tie) {
+  const float q = fminf(ldexpf(v, sc), 16777216.0f);  // NaN v: 2^24 (an event anyway)
+  tie = __builtin_amdgcn_fractf(q) == 0.5f;
+  return (uint32_t)__builtin_rintf(q);
+}
+
+// Inclusive scan of x over the wave (lane order), saturating at 2^32 - 1:
+// sums over 1, 2, 4, 8 lanes within each row of 16, then each row takes the
+// previous rows' total (row_bcast:15, row_bcast:31).
+__device__ __forceinline__ uint32_t wave_scan_sat(uint32_t x) {
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false));
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false));
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false));
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false));
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false));
+  x = usat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false));
+  return x;
+}
+
 // In the histogram hist[0..nbins), bins counted from the top: the bin holding
 // the kk-th largest element (1-based) and kk within that bin.  nbins <= 2048.
 __device__ void select_from_top(SampleShared& sh, int nbins, uint32_t kk, uint32_t* bin,
@@ -218,14 +219,10 @@ __device__ void select_from_top(SampleShared& sh, int nbins, uint32_t kk, uint32
   // thread t owns bins nbins-1-2t (higher) and nbins-2-2t
   const int b0 = nbins - 1 - 2 * t, b1 = b0 - 1;
   const uint32_t c0 = b0 >= 0 ? sh.hist[b0] : 0u, c1 = b1 >= 0 ? sh.hist[b1] : 0u;
-  uint32_t s = c0 + c1;
-  // inclusive scan over threads in order t = 0, 1, ... (wave, then waves)
+  // inclusive scan over threads in order t = 0, 1, ... (DPP within the
+  // wave, then the waves' totals)
   const int lane = t & 63;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t o = (uint32_t)__shfl_up((int)s, off, 64);
-    if (lane >= off) s += o;
-  }
+  const uint32_t s = wave_scan_sat(c0 + c1);
   __syncthreads();
   if (lane == 63) sh.wsum[t >> 6] = s;
   __syncthreads();
@@ -502,31 +499,48 @@ __device__ const uint32_t* sort_keys(uint32_t* k0, uint32_t* k1, int L, SampleSh
 
 // The k-th largest (1-based, 1 <= kk <= cnt) of the keys key(j), j in
 // [0, cnt), by radix select: 11, 11 and 10 bits of the key, one histogram
-// pass per level.
+// pass per level.  Up to kSelReg * kST keys are read once into registers;
+// more are read again at each level.
+constexpr int kSelReg = 4;
+
 template <typename Key>
 __device__ uint32_t kth_largest_key(int cnt, Key key, uint32_t kk, SampleShared& sh) {
   const int t = threadIdx.x;
+  const bool reg = cnt <= kSelReg * kST;
+  uint32_t kr[kSelReg];
+  if (reg) {
+#pragma unroll
+    for (int u = 0; u < kSelReg; u++) kr[u] = key(min(t + u * kST, cnt - 1));  // in bounds
+  }
+  // f(k) for every key this thread owns
+  auto each = [&](auto f) {
+    if (reg) {
+#pragma unroll
+      for (int u = 0; u < kSelReg; u++)
+        if (t + u * kST < cnt) f(kr[u]);
+    } else {
+      for (int j = t; j < cnt; j += kST) f(key(j));
+    }
+  };
   uint32_t b1, b2, b3;
   for (int i = t; i < 2048; i += kST) sh.hist[i] = 0;
   __syncthreads();
-  for (int j = t; j < cnt; j += kST) atomicAdd(&sh.hist[key(j) >> 21], 1u);
+  each([&](uint32_t k) { atomicAdd(&sh.hist[k >> 21], 1u); });
   __syncthreads();
   select_from_top(sh, 2048, kk, &b1, &kk);
   for (int i = t; i < 2048; i += kST) sh.hist[i] = 0;
   __syncthreads();
-  for (int j = t; j < cnt; j += kST) {
-    const uint32_t k = key(j);
+  each([&](uint32_t k) {
     if ((k >> 21) == b1) atomicAdd(&sh.hist[(k >> 10) & 2047u], 1u);
-  }
+  });
   __syncthreads();
   select_from_top(sh, 2048, kk, &b2, &kk);
   for (int i = t; i < 1024; i += kST) sh.hist[i] = 0;
   __syncthreads();
   const uint32_t pre = (b1 << 11) | b2;
-  for (int j = t; j < cnt; j += kST) {
-    const uint32_t k = key(j);
+  each([&](uint32_t k) {
     if ((k >> 10) == pre) atomicAdd(&sh.hist[k & 1023u], 1u);
-  }
+  });
   __syncthreads();
   select_from_top(sh, 1024, kk, &b3, &kk);
   return (pre << 10) | b3;
