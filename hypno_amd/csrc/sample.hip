@@ -567,21 +567,23 @@ __device__ uint32_t kth_largest_key(int cnt, Key key, uint32_t kk, SampleShared&
 // time; the quotients p / S of the walks are computed by the staging
 // threads.
 
-// Stages x(b0 + j), j < len (1 <= len <= kChunk), into sh.chunk: each
-// thread's kChunk / kST values are all read before any is stored, so the
-// reads are in flight together (a loop that stores each value as it arrives
-// waits for the reads one at a time).  Positions past len evaluate x at the
+// Staging of x(b0 + j), j < len (1 <= len <= kChunk), into sh.chunk, in two
+// halves so that the next chunk is read while the current one is added:
+// each thread's kChunk / kST values are all read before any is stored, so
+// the reads are in flight together.  Positions past len evaluate x at the
 // last position (in bounds, unconditionally, so no read sits in a branch)
 // and are not stored.
+constexpr int kStagePer = kChunk / kST;
 template <typename X>
-__device__ __forceinline__ void stage_chunk(X x, int b0, int len, SampleShared& sh) {
+__device__ __forceinline__ void load_chunk(X x, int b0, int len, float (&v)[kStagePer]) {
   const int t = threadIdx.x;
-  constexpr int kPer = kChunk / kST;
-  float v[kPer];
 #pragma unroll
-  for (int u = 0; u < kPer; u++) v[u] = x(b0 + min(t + u * kST, len - 1));
+  for (int u = 0; u < kStagePer; u++) v[u] = x(b0 + min(t + u * kST, len - 1));
+}
+__device__ __forceinline__ void store_chunk(const float (&v)[kStagePer], int len, SampleShared& sh) {
+  const int t = threadIdx.x;
 #pragma unroll
-  for (int u = 0; u < kPer; u++) {
+  for (int u = 0; u < kStagePer; u++) {
     const int j = t + u * kST;
     if (j < len) sh.chunk[j] = v[u];
   }
@@ -801,10 +803,15 @@ template <typename X, typename F>
 __device__ float seq_sum(int cnt, X x, SampleShared& sh, F on_chunk) {
   float s = -0.0f;
   int adv = 0;  // the first values one at a time
+  if (cnt <= 0) return s;
+  float v[kStagePer];
+  load_chunk(x, 0, min(kChunk, cnt), v);
   for (int b0 = 0; b0 < cnt; b0 += kChunk) {
     const int len = min(kChunk, cnt - b0);
-    stage_chunk(x, b0, len, sh);
+    store_chunk(v, len, sh);  // the previous chunk's reads ended at its last barrier
     __syncthreads();
+    // the next chunk's values are read while this one is added
+    if (b0 + kChunk < cnt) load_chunk(x, b0 + kChunk, min(kChunk, cnt - b0 - kChunk), v);
     on_chunk(len);
     acc_chunk<false>(len, s, 0.0f, adv, sh);  // its barriers follow on_chunk's reads
     if (s != s) return s;  // NaN stays NaN
@@ -828,10 +835,14 @@ __device__ int seq_cross(int cnt, Q q, float thr0, SampleShared& sh) {
   __syncthreads();
   float cum = 0.0f;
   int adv = 0;  // the first values one at a time
+  if (cnt <= 0) return -1;
+  float v[kStagePer];
+  load_chunk(q, 0, min(kChunk, cnt), v);
   for (int b0 = 0; b0 < cnt; b0 += kChunk) {
     const int len = min(kChunk, cnt - b0);
-    stage_chunk(q, b0, len, sh);
+    store_chunk(v, len, sh);  // the previous chunk's reads ended at its last barrier
     __syncthreads();
+    if (b0 + kChunk < cnt) load_chunk(q, b0 + kChunk, min(kChunk, cnt - b0 - kChunk), v);
     const int hit = acc_chunk<true>(len, cum, thr, adv, sh);
     if (hit >= 0) return b0 + hit;
     if (hit == -2) return -1;  // cum is NaN: it exceeds nothing
