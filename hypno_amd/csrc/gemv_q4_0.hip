@@ -496,7 +496,7 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvHead& H, const GemvLaun
     if ((B8 & 3) == 0) {
       float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
       const float4* p4 = reinterpret_cast<const float4*>(pr);
-#pragma unroll 1
+#pragma unroll 4
       for (int q = 0; q < (B8 >> 2); q++) {
         const float4 v = p4[q];
         a0 += v.x; a1 += v.y; a2 += v.z; a3 += v.w;
