@@ -268,9 +268,17 @@ struct GemvGroupGeom {
   int maxB = 0;  // largest B (activation staging size)
   int pro = 0;   // some job stages a prologue operand too
   int ring = 0;  // weight steps in flight per wave (LDS ring depth)
+  int rows = 1;  // x rows per pass (the few-row kernels)
   size_t ring_off = 0;  // LDS offset of the weight rings
   size_t lds = 0;
 };
+
+// Few-row GEMV (2 <= rows <= 8, Q4_0): the streaming kernel with every
+// weight block multiplied by `rows` consecutive x rows (K floats apart) in
+// one pass; y rows n floats apart.  Work-groups of at most 512 threads.
+bool q4_0_gemv_rows_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t rows);
+hipError_t launch_q4_0_gemv_rows(float* y, const uint8_t* w, const float* x, const float* bias,
+                                 size_t n, size_t m, int rows, int num_cus, hipStream_t s);
 
 // A launch that the staging rule holds to at most one work-group per CU
 // gets wider work-groups (more waves per CU streaming and computing): the

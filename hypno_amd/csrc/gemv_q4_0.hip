@@ -194,8 +194,8 @@ static void finish_geometry(GemvGroupGeom& g, int T = 0) {
   g.T = T > 0 ? T : g.Tbase;
   while (T <= 0 && g.T < 256 && 2 * g.T <= 1024) g.T *= 2;
   g.W = g.T / 64;
-  g.S = 64;
-  const size_t loop = (size_t)g.S * (g.T / 8) * 4;  // 8-lane group partials
+  g.S = 64 / g.rows;  // steps per partial-sum chunk, per x row
+  const size_t loop = (size_t)g.S * (g.T / 8) * 4 * g.rows;  // 8-lane group partials
   // activation digits and exponents, then one float per wave (prologue sums)
   const size_t digits = g.fmt == kFmtQ8_0 ? 4 * Fmt<kFmtQ8_0>::kLimbs * 8
                                           : 4 * Fmt<kFmtQ4_0>::kLimbs * 4;
@@ -322,8 +322,11 @@ struct GemvHead {
   const float* aux0;
 };
 
-template <int F, bool PRO, int R>
+// MR: rows of x (consecutive, K floats apart) multiplied by the same weights
+// in one pass (y rows n floats apart); only with one plain Q4_0 job.
+template <int F, bool PRO, int R, int MR = 1>
 __device__ __forceinline__ void gemv_jobs_body(const GemvHead& H, const GemvLaunch& L) {
+  static_assert(MR == 1 || (F == kFmtQ4_0 && !PRO), "several rows: plain Q4_0 only");
   using FT = Fmt<F>;
   constexpr int kLimbs = FT::kLimbs;
   constexpr int kLD = FT::kLimbDwords;
@@ -482,9 +485,9 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvHead& H, const GemvLaun
   int cj = j0;
   int seg_end = s_begin;  // end of this work-group's steps of job cj
   int c0 = s_begin;       // first step of the open partial-sum chunk
-  u32x4 xl[kLimbs * kLD / 4];  // this lane's block column of x as digit planes
-  int xe = 0;           // its exponent: x = 2^xe * sum_k base^k * digit_k
-  float xnan = 0.0f;    // NaN when the block holds a non-finite activation
+  u32x4 xl[MR][kLimbs * kLD / 4];  // this lane's block column of each x row as digit planes
+  int xe[MR] = {};       // its exponent: x = 2^xe * sum_k base^k * digit_k
+  float xnan[MR] = {};   // NaN when the block holds a non-finite activation
 
   // Sum the parked partials of steps [c0, c1) into y (one thread per row, in
   // a fixed order).  Row starts in `part` are 16-byte aligned when B8 % 4 == 0
@@ -522,17 +525,21 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvHead& H, const GemvLaun
     const int rps = J.rps, B8 = J.B >> 3;
     const int row0 = (c0 - J.step0) * rps;
     const int nrows = min((c1 - c0) * rps, J.n - row0);
-    float* yr = J.y + row0;
-    if (J.bias == nullptr) {
-      for (int r = t; r < nrows; r += T) {
-        const int sl = r / rps;
-        yr[r] = row_sum(part + sl * T8 + (r - sl * rps) * B8, B8);
-      }
-    } else {
-      const float* br = J.bias + row0;
-      for (int r = t; r < nrows; r += T) {
-        const int sl = r / rps;
-        yr[r] = row_sum(part + sl * T8 + (r - sl * rps) * B8, B8) + br[r];
+#pragma unroll
+    for (int m = 0; m < MR; m++) {  // x row m's partials follow row m-1's S steps
+      float* yr = J.y + (size_t)m * J.n + row0;
+      const float* pm = part + m * L.S * T8;
+      if (J.bias == nullptr) {
+        for (int r = t; r < nrows; r += T) {
+          const int sl = r / rps;
+          yr[r] = row_sum(pm + sl * T8 + (r - sl * rps) * B8, B8);
+        }
+      } else {
+        const float* br = J.bias + row0;
+        for (int r = t; r < nrows; r += T) {
+          const int sl = r / rps;
+          yr[r] = row_sum(pm + sl * T8 + (r - sl * rps) * B8, B8) + br[r];
+        }
       }
     }
     __syncthreads();
@@ -556,10 +563,11 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvHead& H, const GemvLaun
     int* exps = reinterpret_cast<int*>(smem + (size_t)kLimbs * kLD * 4 * B);
     const float4* xv = reinterpret_cast<const float4*>(J.x);
     const float4* av = reinterpret_cast<const float4*>(J.aux);
+    int row = 0;  // the x row being staged (xv points at it)
     // element group i's x (and prologue operand): from the registers read
-    // at the start for the first job's first kPre rounds
+    // at the start for the first job's first kPre rounds (of x row 0)
     auto get8 = [&](int i, int p, float* xs, float* as) __attribute__((always_inline)) {
-      if (first && p < kPre) {
+      if (first && row == 0 && p < kPre) {
 #pragma unroll
         for (int k = 0; k < 8; k++) {
           xs[k] = xpre[p][k];
@@ -680,20 +688,25 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvHead& H, const GemvLaun
       if constexpr (PRO) prologue(xs, as, inv_rms);
       convert(i, xs);
     };
-#pragma unroll
-    for (int p = 0; p < kPre; p++)
-      if (t + p * T < B * 4) round(t + p * T, p);
-    for (int i = t + kPre * T; i < B * 4; i += T) round(i, kPre);
-    __syncthreads();
     const int kb = t % B;
 #pragma unroll
-    for (int v = 0; v < kLimbs * kLD / 4; v++)  // plane v / (kLD / 4), piece v % (kLD / 4)
-      xl[v] = *reinterpret_cast<const u32x4*>(limbs + (v / (kLD / 4)) * B * kLD + kb * kLD +
-                                              (v % (kLD / 4)) * 4);
-    const int ex = exps[kb];
-    xe = ex == kBadExp ? 0 : ex;
-    xnan = ex == kBadExp ? __builtin_nanf("") : 0.0f;
-    __syncthreads();  // the activation region becomes partial space
+    for (int m = 0; m < MR; m++) {
+      row = m;
+      xv = reinterpret_cast<const float4*>(J.x + (size_t)m * B * kBlockElems);
+#pragma unroll
+      for (int p = 0; p < kPre; p++)
+        if (t + p * T < B * 4) round(t + p * T, p);
+      for (int i = t + kPre * T; i < B * 4; i += T) round(i, kPre);
+      __syncthreads();
+#pragma unroll
+      for (int v = 0; v < kLimbs * kLD / 4; v++)  // plane v / (kLD / 4), piece v % (kLD / 4)
+        xl[m][v] = *reinterpret_cast<const u32x4*>(limbs + (v / (kLD / 4)) * B * kLD + kb * kLD +
+                                                   (v % (kLD / 4)) * 4);
+      const int ex = exps[kb];
+      xe[m] = ex == kBadExp ? 0 : ex;
+      xnan[m] = ex == kBadExp ? __builtin_nanf("") : 0.0f;
+      __syncthreads();  // the region is the next row's, then partial space
+    }
   };
 
   // One step: close the chunk / switch job when due (uniform branches), read
@@ -717,26 +730,31 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvHead& H, const GemvLaun
     for (int k = 0; k < FT::kBytes / 4 + 1; k++) d[k] = wp[k];
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot is read out
     issue(slot);
-    float partial;
+    float partial[MR];
     {
       if constexpr (F == kFmtQ4_0) {
         const float scale = f16_bits_to_f32(d[0] >> sh_d);
-        int acc[kLimbs];
+        int acc[MR][kLimbs];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
           const uint32_t q = __builtin_amdgcn_perm(d[j + 1], d[j], sel_q) ^ 0x88888888u;
 #pragma unroll
-          for (int l = 0; l < kLimbs; l++)
-            acc[l] = j == 0 ? sdot8_first(q, xl[l][0])
-                            : __builtin_amdgcn_sdot8((int)q, (int)xl[l][j], acc[l], false);
+          for (int m = 0; m < MR; m++)
+#pragma unroll
+            for (int l = 0; l < kLimbs; l++)
+              acc[m][l] = j == 0 ? sdot8_first(q, xl[m][l][0])
+                                 : __builtin_amdgcn_sdot8((int)q, (int)xl[m][l][j], acc[m][l], false);
         }
         // sum_l 16^l * D_l, exact in int32 (|sum| < 2^28), as a chain of
         // shift-adds (one instruction per limb), then one rounding to fp32.
-        int h = acc[kLimbs - 1];
 #pragma unroll
-        for (int l = kLimbs - 2; l >= 0; l--)
-          asm("v_lshl_add_u32 %0, %1, 4, %2" : "=v"(h) : "v"(h), "v"(acc[l]));
-        partial = ldexpf(scale * (float)h, xe) + xnan;
+        for (int m = 0; m < MR; m++) {
+          int h = acc[m][kLimbs - 1];
+#pragma unroll
+          for (int l = kLimbs - 2; l >= 0; l--)
+            asm("v_lshl_add_u32 %0, %1, 4, %2" : "=v"(h) : "v"(h), "v"(acc[m][l]));
+          partial[m] = ldexpf(scale * (float)h, xe[m]) + xnan[m];
+        }
       } else {
         const float scale = f16_bits_to_f32(d[0] >> sh_d);
         int acc[kLimbs] = {};
@@ -745,16 +763,19 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvHead& H, const GemvLaun
           const uint32_t q = __builtin_amdgcn_perm(d[j + 1], d[j], sel_q) ^ 0x80808080u;
 #pragma unroll
           for (int l = 0; l < kLimbs; l++)
-            acc[l] = __builtin_amdgcn_sdot4((int)q, (int)xl[2 * l + (j >> 2)][j & 3], acc[l],
+            acc[l] = __builtin_amdgcn_sdot4((int)q, (int)xl[0][2 * l + (j >> 2)][j & 3], acc[l],
                                             false);
         }
         const int h = acc[2] * 256 + acc[1];
         const float r = fmaf((float)h, 256.0f, (float)acc[0]);
-        partial = ldexpf(scale * r, xe) + xnan;
+        partial[0] = ldexpf(scale * r, xe[0]) + xnan[0];
       }
     }
-    partial = group8_sum(partial);
-    if ((t & 7) == 7) part[(ss - c0) * T8 + (t >> 3)] = partial;
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      const float ps = group8_sum(partial[m]);
+      if ((t & 7) == 7) part[(m * L.S + (ss - c0)) * T8 + (t >> 3)] = ps;
+    }
   };
 
   enter(j0, s_begin, true);
@@ -786,6 +807,24 @@ __global__ void __launch_bounds__(1024) q4_0_gemv_jobs_pro_kernel(GEMV_HEAD_PARA
 template <int R>
 __global__ void __launch_bounds__(1024) q8_0_gemv_jobs_kernel(GEMV_HEAD_PARAMS, GemvLaunch L) {
   gemv_jobs_body<kFmtQ8_0, false, R>(GEMV_HEAD_ARGS, L);
+}
+
+template <int R, int MR>
+__global__ void __launch_bounds__(512) q4_0_gemv_rows_kernel(GEMV_HEAD_PARAMS, GemvLaunch L) {
+  gemv_jobs_body<kFmtQ4_0, false, R, MR>(GEMV_HEAD_ARGS, L);
+}
+
+template <int R>
+static const void* gemv_rows_kernel_r(int rows) {
+  switch (rows) {
+    case 2: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 2>);
+    case 3: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 3>);
+    case 4: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 4>);
+    case 5: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 5>);
+    case 6: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 6>);
+    case 7: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 7>);
+    default: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 8>);
+  }
 }
 
 template <int R>
@@ -897,6 +936,62 @@ static hipError_t launch_gemv_fast(int fmt, float* y, const uint8_t* w, const fl
   J.step0 = 0;
   const int steps = (J.n + J.rps - 1) / J.rps;
   return launch_q4_0_gemv_group(g, nullptr, &J, 1, steps, num_cus, s);
+}
+
+static bool rows_geometry(GemvGroupGeom& g, size_t m, size_t rows) {
+  if (rows < 2 || rows > 8) return false;
+  g.fmt = kFmtQ4_0;
+  g.rows = (int)rows;
+  return gemv_group_add(g, m) && g.T <= 512;
+}
+
+bool q4_0_gemv_rows_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t rows) {
+  GemvGroupGeom g;
+  return q4_0_gemv_fast_ok(w, w_len, n, m) && rows_geometry(g, m, rows);
+}
+
+hipError_t launch_q4_0_gemv_rows(float* y, const uint8_t* w, const float* x, const float* bias,
+                                 size_t n, size_t m, int rows, int num_cus, hipStream_t s) {
+  GemvGroupGeom g;
+  if (!rows_geometry(g, m, (size_t)rows)) return hipErrorInvalidValue;
+  GemvJob J;
+  J.w = w;
+  J.x = x;
+  J.y = y;
+  J.bias = bias;
+  J.aux = nullptr;
+  J.pro = kProNone;
+  J.eps = 0.0f;
+  J.n = (int)n;
+  J.B = (int)(m / 32);
+  J.rps = g.T / J.B;
+  J.step0 = 0;
+  const int steps = (J.n + J.rps - 1) / J.rps;
+  const void* kern = g.ring == 3 ? gemv_rows_kernel_r<3>(rows) : gemv_rows_kernel_r<2>(rows);
+  {
+    hipError_t e = set_lds_limit(kern, (int)kMaxLds);
+    if (e != hipSuccess) return e;
+  }
+  // Compute-heavier than one row (the dot products scale with the rows):
+  // as many work-groups as are resident.
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, g.T, g.lds) != hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  const int grid = steps < num_cus * per_cu ? steps : num_cus * per_cu;
+  GemvLaunch L;
+  L.jobs = nullptr;
+  for (int i = 0; i < kGemvInline; i++) L.inl[i] = J;
+  L.njobs = 1;
+  L.total_steps = steps;
+  L.S = g.S;
+  L.ring_off = (int)g.ring_off;
+  using Kern = void (*)(int, int, int, int, int, int, int, int, const uint8_t*, const float*,
+                        const float*, GemvLaunch);
+  hipLaunchKernelGGL(reinterpret_cast<Kern>(const_cast<void*>(kern)), dim3(grid), dim3(g.T), g.lds, s,
+                     steps, grid, g.T, (int)g.ring_off, 1, J.n, J.B, J.rps, J.w, J.x,
+                     static_cast<const float*>(nullptr), L);
+  return hipGetLastError();
 }
 
 hipError_t launch_q4_0_gemv_fast(float* y, const uint8_t* w, const float* x, const float* bias,

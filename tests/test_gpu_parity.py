@@ -260,6 +260,52 @@ def test_skinny_split_k_repeat(torch, hk, orc, batch, n, m):
             assert orc.rel_l2(got, ref) <= GEMM_TOL
 
 
+
+@pytest.mark.parametrize("batch,n,m", [
+    (2, 4096, 14336), (2, 4097, 256), (3, 1000, 4096), (4, 1024, 4096), (4, 300, 2048),
+])
+def test_gemv_few_rows(torch, hk, orc, batch, n, m):
+    """Two rows (or up to four on a small matrix) take one pass of the
+    streaming GEMV with every block multiplied by each row: each row's result
+    is bit-identical to that row alone through the one-row GEMV (the same
+    integer digit products, block partials and fixed-order sums), and within
+    the GEMV bar of the oracle's per-token GEMVs (turbo.rs:329-331).  Wide
+    activation ranges, an outlier, a zero row and a NaN row included."""
+    import ctypes
+    from hypno_amd import _lib
+    lib = _lib.load()
+    q = _q4(orc, n, m, seed=batch * 13 + n)
+    x = orc.normal_f32(batch + 300, (batch, m))
+    x[0, 5] = np.float32(1e4)
+    x[1] *= np.float32(1e-5)
+    if batch > 2:
+        x[2] = 0.0
+    if batch > 3:
+        x[3, 77] = np.float32("nan")
+    bias = orc.normal_f32(batch + 400, n)
+    qg, xg, bg = _gpu(torch, q), _gpu(torch, x), _gpu(torch, bias)
+
+    def call(xp, rows):
+        y = torch.empty(rows * n, dtype=torch.float32, device="cuda")
+        st = lib.hypno_hip_matmul_q4_0_dev(ctypes.c_void_p(y.data_ptr()),
+                                           ctypes.c_void_p(qg.data_ptr()), q.size,
+                                           ctypes.c_void_p(xp), ctypes.c_void_p(bg.data_ptr()),
+                                           n, m, rows, None)
+        assert st == 0
+        torch.cuda.synchronize()
+        return y.cpu().numpy().reshape(rows, n)
+
+    got = call(xg.data_ptr(), batch)
+    ref = orc.batch_matmul(q, 3, x, n, m, batch) + bias
+    for t in range(batch):
+        one = call(xg.data_ptr() + 4 * t * m, 1)[0]
+        assert np.array_equal(got[t], one, equal_nan=True), t
+        if t == 3:
+            assert np.isnan(got[t]).all() == np.isnan(ref[t]).all()
+        else:
+            assert orc.normwise_err(got[t], ref[t]) <= GEMV_TOL, t
+    assert np.array_equal(got, call(xg.data_ptr(), batch), equal_nan=True)
+
 def test_skinny_wide_range_activations(torch, hk, orc):
     """Per-token power-of-two scaling: tokens of very different magnitude,
     a 1e4 outlier channel, tiny values and an all-zero token stay within the
