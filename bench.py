@@ -573,14 +573,15 @@ def prefill_gemm(torch, lib):
 
 
 def mistral_m_sweep(torch, lib):
-    """Mistral-7B projections at M in {1, 8, 64, 512, 2048}."""
+    """Mistral-7B projections at M in {1, 8, 64, 512, 2048}, and at
+    M = 2 and 4 (the few-row GEMV's range)."""
     out = {}
     for name, n, m in MISTRAL_SHAPES:
-        for M in (1, 8, 64, 512, 2048):
+        for M in (1, 2, 4, 8, 64, 512, 2048):
             out[f"{name}_M{M}"] = q4_case(torch, lib, n, m, M, seed=n + m + M,
                                           reps=20 if M <= 64 else 4, exact_too=M >= 512)
     return {"workload": "configs[3] Mistral-7B q/o, k/v, gate/up, down at M in "
-                        "{1,8,64,512,2048}; GPU time per call (graph replay); M <= 64 "
+                        "{1,2,4,8,64,512,2048}; GPU time per call (graph replay); M <= 64 "
                         "rotates >= 512 MB of weight copies; M >= 512 also in the "
                         "exact-nibble arithmetic", "results": out}
 
