@@ -5,11 +5,12 @@
 //    q4_0_extract_row quant.rs:139-153 and q8_0_extract_row quant.rs:158-175):
 //    out[t][0..hd) = row ids[t] of an FP32 / FP16 / Q8_0 / Q4_0 table,
 //    dequantised bit-exactly, one work-group per token;
-//  * next-token choice from the lm_head's logits: greedy argmax and
-//    sample_token (run.rs:203-251) with its XorShift64 generator
-//    (run.rs:267-278), in two launches: up to 64 work-groups over
-//    consecutive ranges of the logits (per-range argmax, p_i, top-k level-1
-//    histograms), then one work-group for the rest.
+//  * next-token choice from the lm_head's logits: greedy argmax (one launch
+//    of one work-group) and sample_token (run.rs:203-251) with its
+//    XorShift64 generator (run.rs:267-278), in two launches: up to 64
+//    work-groups over consecutive ranges of the logits (per-range argmax,
+//    p_i, and per range either the top-k candidates or the top-p key-bin
+//    masses), then one work-group for the rest.
 //
 // sample_token, as the reference defines it:
 //   p_i = exp(l_i * (1 / temperature)) if temperature > 0, else l_i;
@@ -25,15 +26,19 @@
 // NaN is passed over by the comparisons (the result is the argmax of what
 // follows the last NaN, or the NaN itself when it is the last element).
 //
-// Here: the k-th largest p comes from a three-level radix select (11 + 11 +
-// 10 bits of an order-preserving key; the first level's histograms come
-// from the first launch); the p left non-zero are compacted in index order
-// -- zeros add nothing to the running sums, so walking only the non-zero p
-// gives the reference's fp32 sums bit for bit; the top-p walk sorts them
-// with a stable LSD radix sort (four 8-bit passes, wave-ballot ranks); the
-// running sums are one lane's sequential fp32 additions, exactly the
-// reference's, of quotients p / S that the other lanes divide out (IEEE
-// division, as the reference's) ahead of it.
+// Here: without top-k the sums and walks run over p itself (all n values in
+// index order, zeros included, as the reference's loops). With top-k, the
+// k-th largest p comes from a three-level radix select (11 + 11 + 10 bits of
+// an order-preserving key) over the ranges' candidates, and the p left
+// non-zero are compacted in index order: adding a zero changes no running sum
+// (at most the sign of a zero sum, which no comparison sees), so the
+// compacted list gives the same sums and crossings. The top-p walk sorts
+// (stable LSD radix, four 8-bit passes; a rank pass for short lists) only the
+// key bins from the top down to where their mass reaches top_p plus the fp32
+// sums' margin. Every running sum reproduces the reference's sequential fp32
+// additions exactly: integer prefix sums on the running sum's binade grid, in
+// parallel, with one fp32 addition for each value the grid cannot take
+// (acc_chunk).
 // exp is computed in fp64 and rounded once to fp32 (the reference calls the
 // platform's expf; the two agree except where a result lies within about
 // 2^-29 of a rounding boundary).
