@@ -23,9 +23,12 @@
  *         value), products with the nibbles are exact in int32, each block's
  *         sum is scaled by d in fp32 and blocks accumulate in fp32.  Other
  *         shapes: fp32 FMAs.  Bar: max|y - r| / max|r| <= 1e-4.
- *       Q4_0, M = 2..16: fp16 hi/lo activation pairs per 256-column stage
- *         (to ~2^-22), exact nibble products on MFMA, fp32 block scale; the
- *         same 1e-4 bar per token.
+ *       Q4_0, M = 2 (and M <= 4 when n * m <= 8M), m % 256 == 0: the
+ *         streaming GEMV with every block multiplied by each token's row, in
+ *         its arithmetic above (each token's y bit-identical to its M = 1
+ *         result).  Otherwise M = 2..16: fp16 hi/lo activation pairs per
+ *         256-column stage (to ~2^-22), exact nibble products on MFMA, fp32
+ *         block scale; the same 1e-4 bar per token.
  *       Q4_0, M = 17..64, and M >= 65 (prefill GEMM): activations rounded to
  *         fp16 after a power-of-two scale per token (undone exactly on the
  *         output), fp32 accumulation on MFMA.  Weights: exact nibbles with
