@@ -1016,6 +1016,60 @@ __device__ int top_mass_bin(const SampleArgs& a, SampleShared& sh) {
   return first == 0x7FFFFFFF ? -1 : kBins1 - 1 - first;
 }
 
+// The elements of p[0..n) not below thr (NaN included), in index order, to
+// (ov, oi); returns their count.  Per pass of kChunk values thread t takes
+// the 8 consecutive values from 8t: the kept count per thread, a DPP wave
+// scan, the waves' totals through LDS (one barrier), then the stores.
+__device__ int compact_kept(const float* p, int n, float thr, float* ov, uint32_t* oi,
+                            SampleShared& sh) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  int base = 0;
+  for (int c0 = 0; c0 < n; c0 += kChunk) {
+    const int lo = c0 + 8 * t;
+    float v[8];
+    if (lo + 8 <= n) {
+      const float4* p4 = reinterpret_cast<const float4*>(p + lo);  // p is 16-byte aligned
+      const float4 a0 = p4[0], a1 = p4[1];
+      v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
+      v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] = lo + e < n ? p[lo + e] : 0.0f;
+    }
+    uint32_t km = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) km |= (lo + e < n && !(v[e] < thr)) ? 1u << e : 0u;
+    const uint32_t cnt = (uint32_t)__popc(km);
+    const uint32_t inc = wave_scan_sat(cnt);
+    if (lane == 63) sh.acc_w[w] = inc;
+    __syncthreads();
+    uint32_t woff = 0, tot = 0;
+    const uint4* w4 = reinterpret_cast<const uint4*>(sh.acc_w);
+#pragma unroll
+    for (int q = 0; q < kSW / 4; q++) {
+      const uint4 x = w4[q];
+      const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        woff += 4 * q + k < w ? xs[k] : 0u;
+        tot += xs[k];
+      }
+    }
+    int pos = base + (int)(woff + inc - cnt);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      if ((km >> e) & 1u) {
+        ov[pos] = v[e];
+        oi[pos] = (uint32_t)(lo + e);
+        pos++;
+      }
+    }
+    base += (int)tot;
+    __syncthreads();  // acc_w is read by all before the next pass
+  }
+  return base;
+}
+
 // sample_token without top-k: the sums and walks run over p itself, all n
 // values in index order, zeros included, as the reference's loops do
 // (run.rs:203-251); the draw's index is the token.
@@ -1071,27 +1125,46 @@ __device__ void sample_no_topk(const SampleArgs& a, SampleShared& sh) {
     const float x = p[j];
     return x < tp ? 0.0f : x;
   };
-  const float sum2 = seq_sum(n, q, sh);
-  if (sum2 <= 0.0f) {
-    if (t == 0) *a.token = argmax_combine(a.part, a.parts, n);
-    return;
+  // With a top-p threshold, the survivors (p not below it) in index order:
+  // the zeros between them change neither the sum nor where the draw's
+  // running sum crosses r, so both run over the short list.  The draw:
+  // len values val(j), the token of position j tok(j); false when the sum
+  // is not positive (the argmax of the logits is the token then) or the
+  // walk does not cross.
+  auto draw = [&](int len, auto val, auto tok) -> bool {
+    const float sum2 = seq_sum(len, val, sh);
+    if (sum2 <= 0.0f) {
+      if (t == 0) *a.token = argmax_combine(a.part, a.parts, n);
+      return true;
+    }
+    // r = next_f32(): xorshift 13, 7, 17, then the top 24 bits / 2^24
+    float r = 0.0f;
+    if (t == 0) {
+      uint64_t x = *a.state;
+      x ^= x << 13;
+      x ^= x >> 7;
+      x ^= x << 17;
+      *a.state = x;
+      r = (float)(x >> 40) / 16777216.0f;
+    }
+    // the first index whose running sum of p / S exceeds r (r < cum)
+    const int at = seq_cross(len, [&](int j) { return val(j) / sum2; }, r, sh);
+    if (at >= 0) {
+      if (t == 0) *a.token = tok(at);
+      return true;
+    }
+    return false;
+  };
+  bool done;
+  if (thr_p > -__builtin_inff()) {
+    const int Lb = compact_kept(p, n, tp, a.a_val, a.a_idx, sh);
+    const float* bv = a.a_val;
+    const uint32_t* bi = a.a_idx;
+    done = draw(Lb, [&](int j) { return bv[j]; }, [&](int j) { return bi[j]; });
+  } else {
+    done = draw(n, [&](int j) { return p[j]; }, [&](int j) { return (uint32_t)j; });
   }
-  // r = next_f32(): xorshift 13, 7, 17, then the top 24 bits / 2^24
-  float r = 0.0f;
-  if (t == 0) {
-    uint64_t x = *a.state;
-    x ^= x << 13;
-    x ^= x >> 7;
-    x ^= x << 17;
-    *a.state = x;
-    r = (float)(x >> 40) / 16777216.0f;
-  }
-  // the first index whose running sum of p / S exceeds r (r < cum)
-  const int at = seq_cross(n, [&](int j) { return q(j) / sum2; }, r, sh);
-  if (at >= 0) {
-    if (t == 0) *a.token = (uint32_t)at;
-    return;
-  }
+  if (done) return;
   const uint32_t am = argmax_fold(n, q, sh);
   if (t == 0) *a.token = am;
 }
