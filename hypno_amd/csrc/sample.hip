@@ -1016,33 +1016,52 @@ __device__ int top_mass_bin(const SampleArgs& a, SampleShared& sh) {
   return first == 0x7FFFFFFF ? -1 : kBins1 - 1 - first;
 }
 
+// A work-group barrier that orders LDS only: __syncthreads() also waits for
+// every global store in flight (a release), which a loop whose stores are
+// read only after it ends need not pay at each step.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // The elements of p[0..n) not below thr (NaN included), in index order, to
-// (ov, oi); returns their count.  Per pass of kChunk values thread t takes
-// the 8 consecutive values from 8t: the kept count per thread, a DPP wave
-// scan, the waves' totals through LDS (one barrier), then the stores.
+// (ov, oi); returns their count.  Per pass thread t takes the kCP
+// consecutive values from kCP t (all its reads in flight together): the
+// kept count per thread, a DPP wave scan, the waves' totals through LDS.
+// The kept values are placed in LDS at their list positions, then copied
+// out contiguously (scattered global stores, one masked instruction per
+// value slot, cost several times more); a pass keeping more than the LDS
+// holds stores them directly.  Uses sh.sorta / sh.sortb.
+constexpr int kCP = 32;
+constexpr int kCStage = kSortCap;  // values a pass stages (sorta as floats, sortb)
+
 __device__ int compact_kept(const float* p, int n, float thr, float* ov, uint32_t* oi,
                             SampleShared& sh) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   int base = 0;
-  for (int c0 = 0; c0 < n; c0 += kChunk) {
-    const int lo = c0 + 8 * t;
-    float v[8];
-    if (lo + 8 <= n) {
+  for (int c0 = 0; c0 < n; c0 += kCP * kST) {
+    const int lo = c0 + kCP * t;
+    float v[kCP];
+    if (lo + kCP <= n) {
       const float4* p4 = reinterpret_cast<const float4*>(p + lo);  // p is 16-byte aligned
-      const float4 a0 = p4[0], a1 = p4[1];
-      v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
-      v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+#pragma unroll
+      for (int q = 0; q < kCP / 4; q++) {
+        const float4 f = p4[q];
+        v[4 * q] = f.x;
+        v[4 * q + 1] = f.y;
+        v[4 * q + 2] = f.z;
+        v[4 * q + 3] = f.w;
+      }
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; e++) v[e] = lo + e < n ? p[lo + e] : 0.0f;
+      for (int e = 0; e < kCP; e++) v[e] = lo + e < n ? p[lo + e] : 0.0f;
     }
     uint32_t km = 0;
 #pragma unroll
-    for (int e = 0; e < 8; e++) km |= (lo + e < n && !(v[e] < thr)) ? 1u << e : 0u;
+    for (int e = 0; e < kCP; e++) km |= (lo + e < n && !(v[e] < thr)) ? 1u << e : 0u;
     const uint32_t cnt = (uint32_t)__popc(km);
     const uint32_t inc = wave_scan_sat(cnt);
     if (lane == 63) sh.acc_w[w] = inc;
-    __syncthreads();
+    lds_barrier();  // the stores of the passes before may still be in flight
     uint32_t woff = 0, tot = 0;
     const uint4* w4 = reinterpret_cast<const uint4*>(sh.acc_w);
 #pragma unroll
@@ -1055,18 +1074,38 @@ __device__ int compact_kept(const float* p, int n, float thr, float* ov, uint32_
         tot += xs[k];
       }
     }
-    int pos = base + (int)(woff + inc - cnt);
+    if (tot <= (uint32_t)kCStage) {
+      float* lv = reinterpret_cast<float*>(sh.sorta);
+      uint32_t* li = sh.sortb;
+      int q = (int)(woff + inc - cnt);
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-      if ((km >> e) & 1u) {
-        ov[pos] = v[e];
-        oi[pos] = (uint32_t)(lo + e);
-        pos++;
+      for (int e = 0; e < kCP; e++) {
+        if ((km >> e) & 1u) {
+          lv[q] = v[e];
+          li[q] = (uint32_t)(lo + e);
+          q++;
+        }
+      }
+      lds_barrier();
+      for (int i = t; i < (int)tot; i += kST) {
+        ov[base + i] = lv[i];
+        oi[base + i] = li[i];
+      }
+    } else {
+      int pos = base + (int)(woff + inc - cnt);
+#pragma unroll
+      for (int e = 0; e < kCP; e++) {
+        if ((km >> e) & 1u) {
+          ov[pos] = v[e];
+          oi[pos] = (uint32_t)(lo + e);
+          pos++;
+        }
       }
     }
     base += (int)tot;
-    __syncthreads();  // acc_w is read by all before the next pass
+    lds_barrier();  // acc_w and the staging are read by all before the next pass
   }
+  __syncthreads();  // the list is complete and visible
   return base;
 }
 
