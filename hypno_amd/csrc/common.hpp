@@ -288,13 +288,12 @@ void gemv_group_widen(GemvGroupGeom& g, const int* n, const int* B, int count, i
 
 constexpr int kGemvInline = 4;  // jobs a launch carries in its arguments
 
+// The job count, step count and ring offset travel in the preloaded scalar
+// arguments ahead of this struct, not in it.
 struct GemvLaunch {
   const GemvJob* jobs;           // device table when njobs > kGemvInline
   GemvJob inl[kGemvInline];      // the jobs when njobs <= kGemvInline
-  int njobs;
-  int total_steps;
-  int S;
-  int ring_off;  // LDS offset of the per-wave weight rings
+  int S;                         // steps per partial-sum chunk, per x row
 };
 
 // Adds a job with m columns to group g if the shared shape still fits.

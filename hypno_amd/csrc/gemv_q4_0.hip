@@ -899,10 +899,7 @@ hipError_t launch_q4_0_gemv_group(const GemvGroupGeom& g, const GemvJob* d_jobs,
   GemvLaunch L;
   L.jobs = d_jobs;
   for (int i = 0; i < kGemvInline; i++) L.inl[i] = h_jobs[i < njobs ? i : 0];
-  L.njobs = njobs;
-  L.total_steps = total_steps;
   L.S = g.S;
-  L.ring_off = (int)g.ring_off;
   const GemvJob& J0 = h_jobs[0];
   using Kern = void (*)(int, int, int, int, int, int, int, int, const uint8_t*, const float*,
                         const float*, GemvLaunch);
@@ -982,10 +979,7 @@ hipError_t launch_q4_0_gemv_rows(float* y, const uint8_t* w, const float* x, con
   GemvLaunch L;
   L.jobs = nullptr;
   for (int i = 0; i < kGemvInline; i++) L.inl[i] = J;
-  L.njobs = 1;
-  L.total_steps = steps;
   L.S = g.S;
-  L.ring_off = (int)g.ring_off;
   using Kern = void (*)(int, int, int, int, int, int, int, int, const uint8_t*, const float*,
                         const float*, GemvLaunch);
   hipLaunchKernelGGL(reinterpret_cast<Kern>(const_cast<void*>(kern)), dim3(grid), dim3(g.T), g.lds, s,
