@@ -751,9 +751,16 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvHead& H, const GemvLaun
         for (int m = 0; m < MR; m++) {
           int h = acc[m][kLimbs - 1];
 #pragma unroll
-          for (int l = kLimbs - 2; l >= 0; l--)
-            asm("v_lshl_add_u32 %0, %1, 4, %2" : "=v"(h) : "v"(h), "v"(acc[m][l]));
-          partial[m] = ldexpf(scale * (float)h, xe[m]) + xnan[m];
+          for (int l = kLimbs - 2; l >= 0; l--) {
+            // one v_lshl_add_u32 per limb (the empty asm keeps the compiler
+            // from re-associating the chain into separate shifts and adds)
+            h = (int)(((uint32_t)h << 4) + (uint32_t)acc[m][l]);
+            asm("" : "+v"(h));
+          }
+          // one rounding of d * h (xnan is +0 or NaN: the +0 turns a -0
+          // product into +0, as a separate addition would), then the exact
+          // power-of-two scale
+          partial[m] = ldexpf(fmaf(scale, (float)h, xnan[m]), xe[m]);
         }
       } else {
         const float scale = f16_bits_to_f32(d[0] >> sh_d);
@@ -768,12 +775,13 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvHead& H, const GemvLaun
         }
         const int h = acc[2] * 256 + acc[1];
         const float r = fmaf((float)h, 256.0f, (float)acc[0]);
-        partial[0] = ldexpf(scale * r, xe[0]) + xnan[0];
+        partial[0] = ldexpf(fmaf(scale, r, xnan[0]), xe[0]);
       }
     }
 #pragma unroll
     for (int m = 0; m < MR; m++) {
-      const float ps = group8_sum(partial[m]);
+      float ps = group8_sum(partial[m]);
+      asm volatile("" : "+v"(ps));  // the last add stays a DPP add, ahead of the store's branch
       if ((t & 7) == 7) part[(m * L.S + (ss - c0)) * T8 + (t >> 3)] = ps;
     }
   };
