@@ -574,7 +574,7 @@ def prefill_gemm(torch, lib):
 
 def mistral_m_sweep(torch, lib):
     """Mistral-7B projections at M in {1, 8, 64, 512, 2048}, and at
-    M = 2 and 4 (the few-row GEMV's range)."""
+    M = 2 and 4 (the few-row GEMV: every matrix at M = 2, q/o and k/v at M = 4)."""
     out = {}
     for name, n, m in MISTRAL_SHAPES:
         for M in (1, 2, 4, 8, 64, 512, 2048):

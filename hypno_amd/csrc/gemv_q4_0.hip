@@ -943,11 +943,20 @@ static hipError_t launch_gemv_fast(int fmt, float* y, const uint8_t* w, const fl
   return launch_q4_0_gemv_group(g, nullptr, &J, 1, steps, num_cus, s);
 }
 
+// Work-groups of 512 threads where the row length allows (twice the steps in
+// flight per work-group of the 256 that the one-row geometry picks for
+// K = 4096; the grid below then needs half the work-groups).
 static bool rows_geometry(GemvGroupGeom& g, size_t m, size_t rows) {
   if (rows < 2 || rows > 8) return false;
   g.fmt = kFmtQ4_0;
   g.rows = (int)rows;
-  return gemv_group_add(g, m) && g.T <= 512;
+  if (!gemv_group_add(g, m) || g.T > 512) return false;
+  if (g.T < 512 && 512 % g.Tbase == 0) {
+    GemvGroupGeom t = g;
+    finish_geometry(t, 512);
+    if (t.lds <= kMaxLds) g = t;
+  }
+  return true;
 }
 
 bool q4_0_gemv_rows_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t rows) {
@@ -977,12 +986,20 @@ hipError_t launch_q4_0_gemv_rows(float* y, const uint8_t* w, const float* x, con
     hipError_t e = set_lds_limit(kern, (int)kMaxLds);
     if (e != hipSuccess) return e;
   }
-  // Compute-heavier than one row (the dot products scale with the rows):
-  // as many work-groups as are resident.
+  // Every work-group converts all rows of x (rows x 16 KB at K = 4096), so,
+  // as for one row, each should stream at least twice that in weights; at
+  // most as many work-groups as are resident.
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, g.T, g.lds) != hipSuccess ||
       per_cu < 1)
     per_cu = 1;
+  {
+    const long long stage = 4LL * kBlockElems * g.maxB * rows;
+    const long long ws = (long long)n * J.B * kBlockBytes / (2 * stage);
+    long long per = (ws + num_cus / 2) / num_cus;
+    if (per < 1) per = 1;
+    if (per < per_cu) per_cu = (int)per;
+  }
   const int grid = steps < num_cus * per_cu ? steps : num_cus * per_cu;
   GemvLaunch L;
   L.jobs = nullptr;

@@ -263,9 +263,11 @@ def test_skinny_split_k_repeat(torch, hk, orc, batch, n, m):
 
 @pytest.mark.parametrize("batch,n,m", [
     (2, 4096, 14336), (2, 4097, 256), (3, 1000, 4096), (4, 1024, 4096), (4, 300, 2048),
+    (5, 4096, 4096), (6, 1024, 4096), (7, 1000, 4096), (7, 257, 2048),
 ])
 def test_gemv_few_rows(torch, hk, orc, batch, n, m):
-    """Two rows (or up to four on a small matrix) take one pass of the
+    """Two rows (up to five on a matrix of at most 16M weights, seven on one
+    of at most 4M) take one pass of the
     streaming GEMV with every block multiplied by each row: each row's result
     is bit-identical to that row alone through the one-row GEMV (the same
     integer digit products, block partials and fixed-order sums), and within
