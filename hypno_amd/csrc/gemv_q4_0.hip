@@ -829,9 +829,7 @@ static const void* gemv_rows_kernel_r(int rows) {
     case 3: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 3>);
     case 4: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 4>);
     case 5: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 5>);
-    case 6: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 6>);
-    case 7: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 7>);
-    default: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 8>);
+    default: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 6>);
   }
 }
 
@@ -947,7 +945,7 @@ static hipError_t launch_gemv_fast(int fmt, float* y, const uint8_t* w, const fl
 // flight per work-group of the 256 that the one-row geometry picks for
 // K = 4096; the grid below then needs half the work-groups).
 static bool rows_geometry(GemvGroupGeom& g, size_t m, size_t rows) {
-  if (rows < 2 || rows > 8) return false;
+  if (rows < 2 || rows > kGemvMaxRows) return false;
   g.fmt = kFmtQ4_0;
   g.rows = (int)rows;
   if (!gemv_group_add(g, m) || g.T > 512) return false;

@@ -5,14 +5,15 @@
 // Q4_0 block of W exactly once, in coalesced 16-byte pieces of contiguous
 // row segments, and does the arithmetic on the matrix cores:
 //
-//  * A work-group owns 64 rows of W and a range of K; K streams through LDS
+//  * A work-group owns 64 rows of W (16 on matrices too small for 64-row
+//    tiles to fill the GPU) and a range of K; K streams through LDS
 //    in stages of 256 (8 blocks): DMA (global_load_lds) of the stage's
 //    activation rows and W row segments into a ring of LDS slots, one
-//    barrier per stage.  Its 16 waves form 4 row groups (16 rows, one MFMA
-//    column tile each) x 4 K-groups (block pair kg of every stage): four
-//    waves per SIMD, so their unpacking overlaps the others' waits; at the
-//    end K-groups 1-3 hand their sums to K-group 0 through LDS (added in
-//    K-group order: deterministic).
+//    barrier per stage.  Its 16 (4) waves form 4 (1) row groups (16 rows,
+//    one MFMA column tile each) x 4 K-groups (block pair kg of every stage):
+//    up to four waves per SIMD, so their unpacking overlaps the others'
+//    waits; at the end K-groups 1-3 hand their sums to K-group 0 through LDS
+//    (added in K-group order: deterministic).
 //  * Lane (n, g) of a wave takes nibble quarter g of row n's block from LDS
 //    (4 bytes), turns it into exact fp16 (nib - 8) in registers and feeds
 //    v_mfma_f32_16x16x32_f16; the block's partial is scaled in fp32.
@@ -110,9 +111,7 @@ x_skinny_kernel(uint8_t* __restrict__ xa, float* __restrict__ inv_s, const float
 // a row's 144 bytes of a stage start 16-byte aligned (rows are K/32*18 =
 // multiples of 144 bytes when K % 256 == 0), so they move as nine 16-byte
 // pieces.
-constexpr int kSkWaves = 4;                    // row groups per work-group, 16 W rows each
 constexpr int kSkKGroups = 4;                  // waves per row group, a quarter of a stage's blocks each
-constexpr int kSkThreads = 64 * kSkWaves * kSkKGroups;
 constexpr int kSkRowBytes = 144;               // W bytes of one row and stage
 constexpr int kSkRowPieces = kSkRowBytes / 16;  // 9
 constexpr int kSkWDma = (16 * kSkRowPieces + 63) / 64;  // 3 DMAs per wave and stage
@@ -120,13 +119,17 @@ constexpr int kSkWBytes = 1024 * kSkWDma;      // LDS per wave and stage (W)
 constexpr int kSkXRowBytes = 512;              // fp16 A-row bytes of one stage
 constexpr int kSkStageK = 256;
 
-template <int MF>
+// RW row groups (16 W rows each) per work-group: 4, or 1 where 64-row tiles
+// would leave the GPU short of work-groups.
+template <int MF, int RW>
 struct SkGeom {
+  static constexpr int kWaves = RW * kSkKGroups;
+  static constexpr int kThreads = 64 * kWaves;
   static constexpr int kRows = 16 * MF;                      // A rows
   static constexpr int kXBytes = kRows * kSkXRowBytes;       // X chunk per stage
   static constexpr int kXTot = kXBytes / 1024;               // X DMAs per stage (8/16/32)
-  static constexpr int kXDma = kXTot >= 16 ? kXTot / 16 : 1;  // per issuing wave
-  static constexpr int kSlot = kXBytes + kSkWaves * kSkWBytes;
+  static constexpr int kXDma = kXTot >= kWaves ? kXTot / kWaves : 1;  // per issuing wave
+  static constexpr int kSlot = kXBytes + RW * kSkWBytes;
   static constexpr int kRing = MF == 4 ? 3 : 4;              // stages in LDS
   static constexpr int kLds = kRing * kSlot;                 // 80 / 112 / 132 KB
   // Per wave and stage: kXDma X DMAs (waves below kXTot / kXDma) and W DMA
@@ -135,6 +138,8 @@ struct SkGeom {
   static_assert(kSkWDma == 3, "W DMA split between the K-groups");
   static_assert(kLds <= 160 * 1024, "LDS budget");
   static_assert((kRing - 2) * (kXDma + 1) <= 63, "vmcnt range");
+  static_assert(kXDma * kWaves >= kXTot, "every X piece has a wave");
+  static_assert(kWaves * MF * 4 * 64 * 4 <= kLds, "K-group hand-over fits the ring");
 };
 
 // Wait until at most N of this wave's global reads are outstanding and its
@@ -166,9 +171,9 @@ struct SkinnyArgs {
   int splits;         // K ranges over blockIdx.y
 };
 
-// A work-group owns 64 rows of W (wave w: rows 16w..16w+15, one MFMA column
-// tile) and a range of whole stages of K; stages stream through a ring of
-// LDS slots:
+// A work-group owns 16 RW rows of W (wave w: rows 16 (w % RW) .. + 15, one
+// MFMA column tile) and a range of whole stages of K; stages stream through
+// a ring of LDS slots:
 //  * X: the stage's 16 MF A rows (512 bytes each), DMA'd by all waves, 16-byte
 //    pieces XOR-swizzled by row (piece c of row r at c ^ (r & 15)) so the
 //    A-operand reads of 16 rows hit 16 different bank groups;
@@ -179,17 +184,17 @@ struct SkinnyArgs {
 // operand of lane (n, g) for a block is its quarter g (4 nibble bytes) of
 // row n; it becomes exact fp16 (nib - 8) in registers, and the block's
 // partial is scaled in fp32.
-template <int MF, bool SPLIT>
-__global__ void __launch_bounds__(kSkThreads) q4_0_skinny_kernel(const SkinnyArgs a) {
-  using G = SkGeom<MF>;
+template <int MF, bool SPLIT, int RW>
+__global__ void __launch_bounds__((SkGeom<MF, RW>::kThreads)) q4_0_skinny_kernel(const SkinnyArgs a) {
+  using G = SkGeom<MF, RW>;
   extern __shared__ __align__(16) uint8_t smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int rw = wave & 3;   // row group: W rows 16 rw .. 16 rw + 15 of the tile
-  const int kg = wave >> 2;  // K-group: blocks 2 kg, 2 kg + 1 of every stage
+  const int rw = wave % RW;  // row group: W rows 16 rw .. 16 rw + 15 of the tile
+  const int kg = wave / RW;  // K-group: blocks 2 kg, 2 kg + 1 of every stage
   const bool xact = wave * G::kXDma < G::kXTot;  // this wave DMAs X pieces
   const int n16 = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * 16 * kSkWaves + 16 * rw;  // this wave's first W row
+  const int n0 = blockIdx.x * 16 * RW + 16 * rw;  // this wave's first W row
   const int gsteps = a.K / kSkStageK;
   const int z = blockIdx.y;
   const int s0 = (int)((long long)gsteps * z / a.splits);
@@ -338,7 +343,7 @@ __global__ void __launch_bounds__(kSkThreads) q4_0_skinny_kernel(const SkinnyArg
   // Trailing DMAs landed and every wave is done with the ring; then K-group 1
   // hands its sums to K-group 0 through LDS (a fixed order: deterministic).
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" : : : "memory");
-  float* red = reinterpret_cast<float*>(smem) + ((size_t)(kg * 4 + rw) * MF * 4) * 64 + lane;
+  float* red = reinterpret_cast<float*>(smem) + ((size_t)(kg * RW + rw) * MF * 4) * 64 + lane;
   if (kg > 0) {
 #pragma unroll
     for (int f = 0; f < MF; f++)
@@ -352,7 +357,7 @@ __global__ void __launch_bounds__(kSkThreads) q4_0_skinny_kernel(const SkinnyArg
 #pragma unroll
     for (int f = 0; f < MF; f++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) acc[f][i] += red[((size_t)g2 * 4 * MF * 4 + (f * 4 + i)) * 64];
+      for (int i = 0; i < 4; i++) acc[f][i] += red[((size_t)g2 * RW * MF * 4 + (f * 4 + i)) * 64];
 
   // lane holds A rows 16 f + 4 g + i of W row n
   const int n = n0 + n16;
@@ -426,14 +431,30 @@ SkinnyShape skinny_shape(size_t batch) {
   return s;
 }
 
+// Row groups per work-group: 64-row tiles (4) when they alone cover three
+// quarters of the CUs.  Otherwise 16-row tiles (1) give four times the
+// work-groups before any K split, and each re-reads the activation stages
+// from L2: 2 N K MF bytes in all, against the reduction launch and the
+// shallow K ranges a split of 64-row tiles costs.  Measured on the
+// Mistral-7B shapes, the 16-row tiles win up to 64 MiB of such reads (q/o
+// up to 32 tokens, k/v up to 64) and lose beyond (q/o at 64 tokens: 134 MB;
+// down, K = 14336: 117 MB from 2 tokens on).
+int skinny_rw(size_t n, size_t m, size_t batch, int num_cus) {
+  if (((n + 63) / 64) * 4 >= (size_t)num_cus * 3) return 4;
+  const size_t xbytes = 2 * n * m * (size_t)skinny_shape(batch).mf;
+  return xbytes <= ((size_t)64 << 20) ? 1 : 4;
+}
+
 // K ranges per row tile: none when the row tiles alone cover three quarters
 // of the CUs (a split costs a reduction launch), else about `target`
-// resident work-groups in all (two per CU when a work-group's LDS allows
-// it), at most one range per stage.
+// resident work-groups in all (as many per CU as a work-group's LDS
+// allows, at most three), at most one range per stage.
 int skinny_splits(size_t n, size_t m, size_t batch, int num_cus) {
   const SkinnyShape sh = skinny_shape(batch);
-  const size_t tiles = (n + 63) / 64;
-  const size_t per_cu = sh.mf == 1 ? 2 : 1;
+  const int rw = skinny_rw(n, m, batch, num_cus);
+  const size_t rows = 16 * (size_t)rw;
+  const size_t tiles = (n + rows - 1) / rows;
+  const size_t per_cu = rw == 4 ? (sh.mf == 1 ? 2 : 1) : (sh.mf == 1 ? 3 : sh.mf == 2 ? 2 : 1);
   const size_t target = (size_t)num_cus * per_cu;
   size_t sp = tiles * 4 >= (size_t)num_cus * 3 ? 1 : (target + tiles / 2) / tiles;
   const size_t gsteps = m / kSkStageK;
@@ -442,14 +463,19 @@ int skinny_splits(size_t n, size_t m, size_t batch, int num_cus) {
   return (int)sp;
 }
 
-template <int MF, bool SPLIT>
+template <int MF, bool SPLIT, int RW>
 hipError_t launch_mf(const SkinnyArgs& a, dim3 grid, hipStream_t s) {
-  hipError_t e = set_lds_limit(reinterpret_cast<const void*>(q4_0_skinny_kernel<MF, SPLIT>),
-                               SkGeom<MF>::kLds);
+  using G = SkGeom<MF, RW>;
+  hipError_t e = set_lds_limit(reinterpret_cast<const void*>(q4_0_skinny_kernel<MF, SPLIT, RW>),
+                               G::kLds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((q4_0_skinny_kernel<MF, SPLIT>), grid, dim3(kSkThreads), SkGeom<MF>::kLds,
-                     s, a);
+  hipLaunchKernelGGL((q4_0_skinny_kernel<MF, SPLIT, RW>), grid, dim3(G::kThreads), G::kLds, s, a);
   return hipGetLastError();
+}
+
+template <int MF, bool SPLIT>
+hipError_t launch_rw(const SkinnyArgs& a, int rw, dim3 grid, hipStream_t s) {
+  return rw == 4 ? launch_mf<MF, SPLIT, 4>(a, grid, s) : launch_mf<MF, SPLIT, 1>(a, grid, s);
 }
 
 }  // namespace
@@ -509,13 +535,14 @@ hipError_t launch_q4_0_skinny(float* y, const uint8_t* w, const float* x, const 
   a.K = (int)m;
   a.split = sh.split;
   a.splits = sp;
-  const dim3 grid((unsigned)((n + 63) / 64), (unsigned)sp);
+  const int rw = skinny_rw(n, m, batch, num_cus);
+  const dim3 grid((unsigned)((n + 16 * rw - 1) / (16 * rw)), (unsigned)sp);
   if (sh.mf == 1)
-    e = launch_mf<1, true>(a, grid, s);
+    e = launch_rw<1, true>(a, rw, grid, s);
   else if (sh.mf == 2)
-    e = sh.split ? launch_mf<2, true>(a, grid, s) : launch_mf<2, false>(a, grid, s);
+    e = sh.split ? launch_rw<2, true>(a, rw, grid, s) : launch_rw<2, false>(a, rw, grid, s);
   else
-    e = launch_mf<4, false>(a, grid, s);
+    e = launch_rw<4, false>(a, rw, grid, s);
   if (e != hipSuccess || sp == 1) return e;
   const size_t mn = batch * n;
   hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, y,

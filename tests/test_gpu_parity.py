@@ -196,11 +196,15 @@ def test_small_batch_matches_per_token(torch, hk, orc, batch):
 @pytest.mark.parametrize("batch,n,m", [
     (2, 37, 512), (7, 1000, 1024), (8, 4096, 4096), (9, 130, 2048), (15, 4097, 256),
     (16, 64, 768), (17, 300, 4096), (32, 1024, 3072), (33, 2048, 1024), (64, 4096, 4096),
+    (6, 3000, 1536), (8, 12288, 512), (12, 12289, 256), (40, 12300, 256),
 ])
 def test_skinny_q4_0(torch, hk, orc, batch, n, m):
     """2..64 tokens: against the oracle's per-token GEMVs (turbo.rs:329-331).
     Up to 15 tokens the bar is the GEMV's (fp32 activations, 1e-4 normwise
-    per token); from 16 the prefill GEMM's (fp16 activations, 2e-3 rel L2)."""
+    per token); from 16 the prefill GEMM's (fp16 activations, 2e-3 rel L2).
+    N >= 12288, or 16-row tiles that would re-read more than 64 MiB of
+    activations (64 tokens at 4096 x 4096), takes 64-row work-groups; the
+    other shapes here 16-row ones."""
     q = _q4(orc, n, m, seed=batch * 7 + n)
     x = orc.normal_f32(batch + 100, (batch, m))
     bias = orc.normal_f32(batch + 200, n)
@@ -263,10 +267,10 @@ def test_skinny_split_k_repeat(torch, hk, orc, batch, n, m):
 
 @pytest.mark.parametrize("batch,n,m", [
     (2, 4096, 14336), (2, 4097, 256), (3, 1000, 4096), (4, 1024, 4096), (4, 300, 2048),
-    (5, 4096, 4096), (6, 1024, 4096), (7, 1000, 4096), (7, 257, 2048),
+    (4, 4096, 4096), (5, 1024, 4096), (6, 1000, 4096), (6, 257, 2048),
 ])
 def test_gemv_few_rows(torch, hk, orc, batch, n, m):
-    """Two rows (up to five on a matrix of at most 16M weights, seven on one
+    """Two rows (up to four on a matrix of at most 16M weights, six on one
     of at most 4M) take one pass of the
     streaming GEMV with every block multiplied by each row: each row's result
     is bit-identical to that row alone through the one-row GEMV (the same
