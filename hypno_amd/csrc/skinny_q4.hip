@@ -403,8 +403,17 @@ skinny_reduce_kernel(float* __restrict__ y, const float* __restrict__ part,
   const size_t mn = (size_t)M * N;
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= mn) return;
+  // Eight planes' loads go out together, then the adds run in split order
+  // (a loop of load-then-add waits a full memory latency per plane).
   float v = 0.0f;
-  for (int z = 0; z < splits; z++) v += part[(size_t)z * mn + i];
+  for (int z0 = 0; z0 < splits; z0 += 8) {
+    float a[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) a[k] = z0 + k < splits ? part[(size_t)(z0 + k) * mn + i] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+      if (z0 + k < splits) v += a[k];
+  }
   if (bias) v += bias[i % N];
   y[i] = v;
 }
