@@ -216,13 +216,12 @@ int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
     return HYPNO_HIP_OK;
   };
   hipError_t e;
-  // Two x rows, up to four on a matrix of at most 16M weights, up to five
-  // on one of at most 4M: one pass of the streaming GEMV with every block
-  // multiplied by each row (measured faster than the few-token kernel's
-  // pre-pass, main and reduction launches there; slower beyond, where the
-  // dot products, which grow with the rows, bound it).
-  const bool few_rows = batch == 2 || (batch <= 4 && n * m <= ((size_t)16 << 20)) ||
-                        (batch <= 5 && n * m <= ((size_t)4 << 20));
+  // Two x rows, up to four on a matrix of at most 16M weights: one pass of
+  // the streaming GEMV with every block multiplied by each row (measured
+  // faster than the few-token kernel's pre-pass, main and reduction launches
+  // there; slower beyond, where the dot products, which grow with the rows,
+  // bound it).
+  const bool few_rows = batch == 2 || (batch <= 4 && n * m <= ((size_t)16 << 20));
   if (batch >= 2 && few_rows && q4_0_gemv_rows_ok(w, w_len, n, m, batch) && aligned16(x)) {
     e = launch_q4_0_gemv_rows(y, w, x, bias, n, m, (int)batch, cus, s);
     if (e != hipSuccess) return hip_fail(e, "q4_0 few-row GEMV launch");

@@ -827,8 +827,7 @@ static const void* gemv_rows_kernel_r(int rows) {
   switch (rows) {
     case 2: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 2>);
     case 3: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 3>);
-    case 4: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 4>);
-    default: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 5>);
+    default: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 4>);
   }
 }
 

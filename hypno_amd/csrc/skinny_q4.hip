@@ -456,14 +456,16 @@ int skinny_rw(size_t n, size_t m, size_t batch, int num_cus) {
 
 // K ranges per row tile: none when the row tiles alone cover three quarters
 // of the CUs (a split costs a reduction launch), else about `target`
-// resident work-groups in all (as many per CU as a work-group's LDS
-// allows, at most three), at most one range per stage.
+// work-groups in all: two per CU for single-fragment tiles, one otherwise
+// (measured on 16-row k/v tiles: 8 splits at M = 8 8.5 µs per call against
+// 9.4 with 12, 4 splits at M = 16 9.4 against 9.7 with 8), at most one range
+// per stage.
 int skinny_splits(size_t n, size_t m, size_t batch, int num_cus) {
   const SkinnyShape sh = skinny_shape(batch);
   const int rw = skinny_rw(n, m, batch, num_cus);
   const size_t rows = 16 * (size_t)rw;
   const size_t tiles = (n + rows - 1) / rows;
-  const size_t per_cu = rw == 4 ? (sh.mf == 1 ? 2 : 1) : (sh.mf == 1 ? 3 : sh.mf == 2 ? 2 : 1);
+  const size_t per_cu = sh.mf == 1 ? 2 : 1;
   const size_t target = (size_t)num_cus * per_cu;
   size_t sp = tiles * 4 >= (size_t)num_cus * 3 ? 1 : (target + tiles / 2) / tiles;
   const size_t gsteps = m / kSkStageK;

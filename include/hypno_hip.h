@@ -23,7 +23,7 @@
  *         value), products with the nibbles are exact in int32, each block's
  *         sum is scaled by d in fp32 and blocks accumulate in fp32.  Other
  *         shapes: fp32 FMAs.  Bar: max|y - r| / max|r| <= 1e-4.
- *       Q4_0, M = 2 (M <= 4 when n * m <= 16M, M <= 5 when n * m <= 4M),
+ *       Q4_0, M = 2 (M <= 4 when n * m <= 16M),
  *         m % 256 == 0: the
  *         streaming GEMV with every block multiplied by each token's row, in
  *         its arithmetic above (each token's y bit-identical to its M = 1
