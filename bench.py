@@ -28,7 +28,11 @@ Also reported, in the same JSON line:
                 the Mistral M-sweep {1, 8, 64, 512, 2048}, configs[4] the
                 lm_head in Q4_0 and FP16 at M = 1 and 128; prefill GEMMs also
                 in the exact-nibble arithmetic (hypno_hip_set_gemm_numerics);
-                model_load, q8_0_decode, col_major.
+                model_load, q8_0_decode, col_major.  The final line holds
+                them as a flat map "workload.case" -> {us, frac, ok} (frac =
+                the binding roofline's fraction, ok = output checked); the
+                full result tree goes to stderr as "[bench] detail {...}"
+                (and to --detail FILE), so the line stays ~6 KB.
 Every workload's output is checked once, untimed, against an fp64 reference
 computed here from the same packed bytes (sampled rows or columns; GEMV
 bar 1e-4 normwise, GEMM bar 2e-3 relative L2): each carries "checked".
@@ -161,6 +165,48 @@ def ref_fields(us, flops, nbytes):
             "bandwidth_gbps": round(nbytes / us * 1e-3, 1)}
 
 
+SHORT = {"c0_single_gemv": "c0", "c1_tinyllama_stream": "c1", "c2_prefill_gemm": "c2",
+         "c3_m_sweep": "c3", "c4_lm_head": "c4", "c4_next_token": "tok", "model_load": "load",
+         "q8_0_decode": "q8", "col_major": "col"}
+
+
+def compact(sec):
+    """Flat map of every timed result in the secondary tree: "path" -> {us,
+    frac, ok}, the compact record the final line carries (one entry per
+    result, like bench.rs:35-46's BenchResult).  frac is the fraction of the
+    roofline that binds the call: the larger of its HBM and fp16-MFMA
+    fractions (the bound whose minimum time is the longer)."""
+    flat = {}
+
+    def walk(o, path):
+        if not isinstance(o, dict):
+            return
+        us = o.get("us")
+        if us is None and "ms_per_step" in o:
+            us = o["ms_per_step"] * 1e3
+        if us is None and "open_upload_ms" in o:
+            us = o["open_upload_ms"] * 1e3
+        if isinstance(us, (int, float)):
+            fr = [o[k] for k in ("frac_hbm_peak", "frac_fp16_peak") if k in o]
+            if not fr and "gbs" in o:
+                fr = [o["gbs"] / HBM_PEAK_GBS]
+            if not fr and isinstance(o.get("roofline"), dict):
+                fr = [o["roofline"]["frac"]]
+            ent = {"us": round(us, 2)}
+            if fr:
+                ent["frac"] = round(max(fr), 4)
+            if isinstance(o.get("check"), dict):
+                ent["ok"] = bool(o["check"].get("checked"))
+            flat[path] = ent
+        for k, v in o.items():
+            if isinstance(v, dict) and k not in ("check", "separate_check", "roofline"):
+                k = "exact" if k == "exact_nibbles" else k
+                walk(v, f"{path}.{k}" if path and k != "results" else (path or k))
+    for key, val in sec.items():
+        walk(val, SHORT.get(key, key))
+    return flat
+
+
 # --- library and inputs ----------------------------------------------------------------
 
 class Lib:
@@ -257,8 +303,7 @@ def launch_stats(per_ms, bytes_per_launch):
     first, last = per_ms[:k], per_ms[-k:]
     us = lambda v: round(v * 1e3, 2)  # noqa: E731
     gbs = lambda ms: round(bytes_per_launch / (ms * 1e-3) / 1e9, 1)  # noqa: E731
-    return {"pass": "after the timed region, an event after every launch (each adds ~6 us of "
-                    "GPU idle between launches)",
+    return {"pass": "after the timed region, one event per launch",
             "launches": len(per_ms), "median_us": us(statistics.median(per_ms)),
             "min_us": us(min(per_ms)), "max_us": us(max(per_ms)),
             f"burst_first{k}_us": us(sum(first) / k), f"sustained_last{k}_us": us(sum(last) / k),
@@ -1087,6 +1132,9 @@ def main():
                          "(c0_single_gemv, c2_prefill_gemm, c3_m_sweep, c4_lm_head, "
                          "c4_next_token, model_load, q8_0_decode, col_major); used to "
                          "profile one workload's kernels")
+    ap.add_argument("--detail", metavar="FILE", default=None,
+                    help="also write every secondary workload's full result tree to FILE "
+                         "(the final stdout line carries a compact us/frac/ok map)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run only a plain 1 GiB device copy, 20 times (HBM counter "
                          "calibration under rocprofv3 --pmc)")
@@ -1185,7 +1233,14 @@ def main():
                 sec[key] = tinyllama_stream(torch, lib, args.steps, args.warmup)
             else:
                 sec[key] = fn(torch, lib)
-        line["secondary"] = sec
+        line["secondary"] = compact(sec)
+        # The full tree goes to stderr (and --detail FILE): the final stdout
+        # line stays a compact record a log tail can hold whole.
+        detail = json.dumps({"secondary": sec})
+        print(f"[bench] detail {detail}", file=sys.stderr, flush=True)
+        if args.detail:
+            with open(args.detail, "w") as f:
+                f.write(detail + "\n")
         checks = []
 
         def walk(o):
