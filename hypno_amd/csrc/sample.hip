@@ -70,7 +70,8 @@ __global__ void __launch_bounds__(256) embed_rows_kernel(const EmbedArgs a) {
   const size_t hd = a.hd;
   if (a.dtype == 0 || a.dtype == 1) {  // FP32 / FP16: [start, start + hd)
     const size_t esz = a.dtype == 0 ? 4 : 2;
-    const bool ok = (id + 1) * hd <= a.table_len / esz;
+    // (id + 1) * hd <= table_len / esz, without a product that can wrap.
+    const bool ok = id < a.table_len / esz / hd;
     for (size_t i = threadIdx.x; i < hd; i += 256) {
       float v = __builtin_nanf("");
       if (ok) {
@@ -86,7 +87,7 @@ __global__ void __launch_bounds__(256) embed_rows_kernel(const EmbedArgs a) {
   // them stay 0.
   const size_t bb = a.dtype == 2 ? kQ8BlockBytes : kBlockBytes;
   const size_t bpr = hd / kBlockElems;
-  const bool ok = (id + 1) * bpr * bb <= a.table_len;
+  const bool ok = bpr != 0 && id < a.table_len / bb / bpr;
   for (size_t i = threadIdx.x; i < hd; i += 256) {
     const size_t b = i / kBlockElems, j = i % kBlockElems;
     float v = 0.0f;

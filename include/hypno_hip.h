@@ -341,8 +341,9 @@ int hypno_hip_embed_tokens_dev(float* out, const uint8_t* table, size_t table_le
 /* Greedy next token: *index = the position of the largest of n logits, as
  * Iterator::max_by with partial_cmp picks it (run.rs:232-234): the last of
  * equal maxima, NaNs passed over by the comparisons; n = 0 gives 0.
- * `index` is device memory.  Two launches; a small part of the stream's
- * workspace. */
+ * `index` is device memory.  4-byte-aligned logits: one launch of one
+ * work-group, no workspace; otherwise two launches and a small part of the
+ * stream's workspace. */
 int hypno_hip_argmax_dev(uint32_t* index, const float* logits, size_t n, void* stream);
 
 /* sample_token(logits, temperature, top_p, top_k, rng) (run.rs:203-251) on
@@ -354,9 +355,12 @@ int hypno_hip_argmax_dev(uint32_t* index, const float* logits, size_t n, void* s
  * reference's libm expf agrees but for results within ~2^-29 of a rounding
  * boundary).  Logits must not hold NaN (the reference's sort is then not
  * total).  Two launches (per-range candidates over up to 64 work-groups,
- * then one work-group); the sums, the top-p walk and the draw are sequential
- * fp32 loops over the tokens left after top-k, like the reference's.  Uses
- * the stream's workspace (about 28 n bytes). */
+ * then one work-group).  The sums, the top-p walk and the draw run in
+ * parallel yet give the reference's sequential fp32 results bit for bit:
+ * integer prefix sums on the running sum's binade grid, with one fp32 add for
+ * each value that grid cannot hold; the top-p walk sorts only the top key
+ * bins down to where their mass reaches top_p (plus the fp32 sums' margin).
+ * Uses the stream's workspace (about 28 n bytes). */
 int hypno_hip_sample_token_dev(uint32_t* token, uint64_t* rng_state, const float* logits,
                                size_t n, float temperature, float top_p, size_t top_k,
                                void* stream);

@@ -114,6 +114,75 @@ def test_mistral_m2048(torch, hk, lib, orc, name, n, m):
         assert orc.rel_l2(got[t], r32) <= GEMM_TOL, t
 
 
+def _check_sampled(orc, got, xh, qh, n, m, cols_seed, tol, norm, tokens):
+    """Sampled columns over every token (fp64 over the dequantised rows),
+    then whole tokens against the oracle's per-token GEMV."""
+    cols = _sample_cols(n, 256, seed=cols_seed)
+    ref = xh.astype(np.float64) @ _q4_rows_f64(orc, qh, cols, m).T
+    metric = orc.normwise_err if norm else orc.rel_l2
+    for t in range(xh.shape[0]):
+        err = metric(got[t, cols], ref[t])
+        assert err <= tol, f"token {t}: {err:.3e} over {len(cols)} sampled columns"
+    for t in tokens:
+        r32 = orc.matmul_q4_0(qh, xh[t], None, n, m)
+        assert metric(got[t], r32) <= tol, t
+
+
+MISTRAL_MLP = [("gate_up", 14336, 4096), ("down", 4096, 14336)]
+
+
+@pytest.mark.parametrize("batch", [8, 64, 512])
+@pytest.mark.parametrize("name,n,m", MISTRAL_MLP)
+def test_mistral_mlp_batches(torch, hk, lib, orc, name, n, m, batch):
+    """configs[3] gate/up and down at 8, 64 and 512 tokens in the default
+    arithmetic: the few-token kernel's 64-row grids (8: hi/lo activation rows,
+    held to the GEMV bar per token; 64: plain fp16 rows) and the 256-row
+    prefill tiles (512), turbo.rs:306-333 semantics."""
+    print(f"[case] mistral {name} n={n} m={m} batch={batch}", flush=True)
+    q, qh = _q4_dev(torch, hk, n, m, seed=n + m + batch)
+    gen = torch.Generator(device="cuda").manual_seed(n * 5 + batch)
+    x = torch.randn(batch, m, generator=gen, device="cuda")
+    y = torch.full((batch, n), float("nan"), device="cuda")
+    _q4_dev_call(lib, y, q, x, n, m, batch)
+    torch.cuda.synchronize()
+    few = batch <= 16
+    _check_sampled(orc, y.cpu().numpy(), x.cpu().numpy(), qh, n, m, cols_seed=n + batch,
+                   tol=GEMV_TOL if few else GEMM_TOL, norm=few,
+                   tokens=(0, batch // 2, batch - 1))
+
+
+EXACT_CASES = [("c2_gate_up", 8192, 3072, 512), ("c2_down", 3072, 8192, 512),
+               ("q_o", 4096, 4096, 512), ("gate_up", 14336, 4096, 512),
+               ("down", 4096, 14336, 512), ("k_v", 1024, 4096, 512),
+               ("q_o", 4096, 4096, 2048), ("gate_up", 14336, 4096, 2048),
+               ("down", 4096, 14336, 2048)]
+
+
+@pytest.mark.parametrize("name,n,m,batch", EXACT_CASES)
+def test_gemm_exact_nibbles(torch, hk, lib, orc, name, n, m, batch):
+    """The north-star prefill arithmetic (exact integer nibbles into the
+    MFMAs, each block's scale applied in fp32; hypno_hip_set_gemm_numerics
+    GEMM_EXACT) at configs[2] and the Mistral-7B shapes at 512 and 2048
+    tokens, where the default arithmetic would fold the scales instead.
+    configs[2]'s activations carry its 1% x20 outlier channels."""
+    print(f"[case] exact {name} n={n} m={m} batch={batch}", flush=True)
+    q, qh = _q4_dev(torch, hk, n, m, seed=n + m + batch + 1)
+    gen = torch.Generator(device="cuda").manual_seed(n * 7 + batch)
+    x = torch.randn(batch, m, generator=gen, device="cuda")
+    if name.startswith("c2"):
+        ch = torch.randperm(m, generator=torch.Generator().manual_seed(m))[: m // 100]
+        x[:, ch.cuda()] *= 20.0
+    y = torch.full((batch, n), float("nan"), device="cuda")
+    prev = hk.set_gemm_numerics(hk.GEMM_EXACT)
+    try:
+        _q4_dev_call(lib, y, q, x, n, m, batch)
+        torch.cuda.synchronize()
+    finally:
+        hk.set_gemm_numerics(prev)
+    _check_sampled(orc, y.cpu().numpy(), x.cpu().numpy(), qh, n, m, cols_seed=n + batch + 3,
+                   tol=GEMM_TOL, norm=False, tokens=(0, batch - 1))
+
+
 # --- configs[4]: the lm_head --------------------------------------------------------
 
 LM_N, LM_M = 128256, 4096

@@ -229,9 +229,10 @@ def test_skinny_q4_0(torch, hk, orc, batch, n, m):
 
 @pytest.mark.parametrize("batch,n,m", [(8, 1000, 4096), (40, 1100, 4096), (16, 4096, 14336)])
 def test_skinny_split_k_repeat(torch, hk, orc, batch, n, m):
-    """Split-K (few row tiles): the work-group finishing a tile adds the
-    partials in split order and re-arms the tile counter, so back-to-back
-    calls with other inputs in between stay bit-identical and correct."""
+    """Split-K (few row tiles): each split writes its own partial plane and a
+    second launch adds the planes in split order (+ bias), so the workspace
+    reused by back-to-back calls with other inputs in between leaves the
+    results bit-identical and correct."""
     import ctypes
     from hypno_amd import _lib
     lib = _lib.load()

@@ -270,3 +270,23 @@ def test_sample_fallbacks(env, orc):
         for args in ((1.0, 1.0, 0), (0.5, 0.5, 1), (1.0, 0.9, n)):
             want = orc.sample_token(lg, *args, 777)
             assert _gpu_sample(torch, hk, torch.from_numpy(lg).cuda(), *args, 777) == want
+
+
+@pytest.mark.parametrize("top_k", [1000, VOCAB - 1])
+@pytest.mark.parametrize("top_p", [0.9, 1.0])
+def test_sample_temperature0_topk_mixed_signs(env, orc, top_k, top_p):
+    """Temperature 0 keeps p = logit: with N(0, 1) logits the k-th largest p
+    is negative for top_k = VOCAB - 1, so negative p stay in the compacted
+    list and its sums add them one at a time (run.rs:212-245); the sum stays
+    positive, so a draw is made.  Token and generator state bit-exact."""
+    torch, hk, lib = env
+    print(f"[case] sample T=0 top_k={top_k} top_p={top_p}", flush=True)
+    rng = np.random.default_rng(top_k + int(top_p * 10))
+    for trial in range(3):
+        # mean 0.05: a positive total (about 6400 +- 360) over mixed signs
+        logits = (rng.standard_normal(VOCAB) + 0.05).astype(np.float32)
+        g = torch.from_numpy(logits).cuda()
+        seed = int(rng.integers(1, 1 << 62))
+        want = orc.sample_token(logits, 0.0, top_p, top_k, seed)
+        assert want[1] != seed   # a draw was made
+        assert _gpu_sample(torch, hk, g, 0.0, top_p, top_k, seed) == want, trial

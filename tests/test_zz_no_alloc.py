@@ -92,3 +92,39 @@ def test_noalloc_rejects_oversized_calls(env):
     assert b"scratch" in lib.hypno_hip_last_error()
     torch.cuda.synchronize()
     assert bool(torch.isnan(y).all())   # nothing was launched
+
+
+def test_noalloc_allocates_nothing(env):
+    """The contract itself: on a stream the library has not seen (whose
+    workspace the allocating entry point would have to create), noalloc
+    calls of the few-token and the prefill families leave the device's free
+    memory unchanged; the allocating entry point on another fresh stream is
+    the control that shows such an allocation would be seen."""
+    torch, hk, lib = env
+    cases = [(64, 4096, 14336), (512, 3072, 8192)]
+    inputs = []
+    for batch, n, m in cases:
+        q, x, b = _case(torch, hk, n, m, batch, seed=batch + 7)
+        y = torch.empty(batch, n, device="cuda")
+        inputs.append((q, x, b, y, n, m, batch))
+
+    def run(fn, stream):
+        for q, x, b, y, n, m, batch in inputs:
+            st = getattr(lib, fn)(_vp(y), _vp(q), q.numel(), _vp(x), _vp(b), n, m, batch,
+                                  ctypes.c_void_p(stream.cuda_stream))
+            assert st == 0, lib.hypno_hip_last_error()
+        torch.cuda.synchronize()
+
+    run("hypno_hip_matmul_q4_0_dev_noalloc", torch.cuda.current_stream())  # library set up
+    fresh, control = torch.cuda.Stream(), torch.cuda.Stream()
+    for s in (fresh, control):   # the streams' own first use, outside the window
+        with torch.cuda.stream(s):
+            inputs[0][3].zero_()
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    run("hypno_hip_matmul_q4_0_dev_noalloc", fresh)
+    free1 = torch.cuda.mem_get_info()[0]
+    assert free1 == free0, f"noalloc calls took {free0 - free1} bytes"
+    run("hypno_hip_matmul_q4_0_dev", control)
+    free2 = torch.cuda.mem_get_info()[0]
+    assert free2 < free1, "the control's workspace allocation was not seen"
