@@ -21,7 +21,7 @@ OBJ_DIR = os.path.join(HERE, "_build")
 LIB_NAME = "libhypno_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 
-SOURCES = ["codec.hip", "gemv_q4_0.hip", "gemv_f16.hip", "gemm.hip", "gemm_q4.hip",
+SOURCES = ["codec.hip", "gemv_q4_0.hip", "gemv_f16.hip", "gemm.hip", "gemm_q4.hip", "gemm_exact.hip",
            "skinny_q4.hip", "prologue.hip", "gemv_col.hip", "gemm_q8_0.hip", "sample.hip", "api.cpp",
            "model.cpp"]
 

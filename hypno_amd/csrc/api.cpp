@@ -236,6 +236,14 @@ int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
     if (e != hipSuccess) return hip_fail(e, "q4_0 skinny launch");
     return HYPNO_HIP_OK;
   }
+  if (batch >= kGemmMinBatch && gemm_force_exact() && q4_0_gemm_exact_ok(w, w_len, n, m, batch)) {
+    WsLock ws;
+    st = scratch_for(q4_0_gemm_exact_workspace_bytes(batch, n, m, cus), ws, "GEMM workspace");
+    if (st) return st;
+    e = launch_q4_0_gemm_exact(y, w, x, bias, n, m, batch, ws.p, cus, s);
+    if (e != hipSuccess) return hip_fail(e, "q4_0 exact GEMM launch");
+    return HYPNO_HIP_OK;
+  }
   const bool v3 = batch >= kGemmMinBatch && q4_0_gemm_v3_ok(w, w_len, n, m, batch);
   if (v3 || (batch >= kGemmMinBatch && q4_0_gemm_ok(w, w_len, n, m, batch))) {
     WsLock ws;

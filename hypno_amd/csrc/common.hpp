@@ -334,6 +334,16 @@ hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const
                                size_t n, size_t m, size_t batch, void* workspace, int num_cus,
                                hipStream_t s);
 
+// MFMA prefill GEMM in the exact-nibble arithmetic (gemm_exact.hip): the
+// integer nibbles as fp16 into the matrix cores, each block's partial sum
+// scaled by its fp32 scale.  Requires m % 256 == 0, w 4-byte aligned, w_len
+// full, W and the fp16 X under 4 GB.
+bool q4_0_gemm_exact_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t batch);
+size_t q4_0_gemm_exact_workspace_bytes(size_t batch, size_t n, size_t m, int num_cus);
+hipError_t launch_q4_0_gemm_exact(float* y, const uint8_t* w, const float* x, const float* bias,
+                                  size_t n, size_t m, size_t batch, void* workspace, int num_cus,
+                                  hipStream_t s);
+
 // A few tokens (2 <= batch <= 64): weight-streaming MFMA kernel (skinny_q4.hip).
 bool q4_0_skinny_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t batch,
                     int num_cus);
