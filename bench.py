@@ -26,8 +26,9 @@ Also reported, in the same JSON line:
                 grouped / fused / per-call decode steps), configs[2] the
                 prefill GEMM at Llama-3.2-3B MLP shapes (M = 512), configs[3]
                 the Mistral M-sweep {1, 8, 64, 512, 2048}, configs[4] the
-                lm_head in Q4_0 and FP16 at M = 1 and 128; prefill GEMMs also
-                in the exact-nibble arithmetic (hypno_hip_set_gemm_numerics);
+                lm_head in Q4_0 and FP16 at M = 1 and 128; prefill GEMMs in
+                the default exact-nibble arithmetic and again with the opt-in
+                folded scales (hypno_hip_set_gemm_numerics FOLDED);
                 model_load, q8_0_decode, col_major.  The final line holds
                 them as a flat map "workload.case" -> {us, frac, ok} (frac =
                 the binding roofline's fraction, ok = output checked); the
@@ -200,7 +201,7 @@ def compact(sec):
             flat[path] = ent
         for k, v in o.items():
             if isinstance(v, dict) and k not in ("check", "separate_check", "roofline"):
-                k = "exact" if k == "exact_nibbles" else k
+                k = "folded" if k == "folded_scales" else k
                 walk(v, f"{path}.{k}" if path and k != "results" else (path or k))
     for key, val in sec.items():
         walk(val, SHORT.get(key, key))
@@ -555,11 +556,11 @@ def result(us, M, n, m, nbytes):
             **ref_fields(us, flops, nbytes)}
 
 
-def q4_case(torch, lib, n, m, M, seed, reps, exact_too=False):
+def q4_case(torch, lib, n, m, M, seed, reps, folded_too=False):
     """GPU us per hypno_hip_matmul_q4_0_dev call of an M x m . (n x m)^T
     product, over >= 512 MB of distinct weight copies when M <= 64 (so the
-    weights stream from HBM), checked once against fp64.  With exact_too, the
-    same call again in the exact-nibble GEMM arithmetic."""
+    weights stream from HBM), checked once against fp64.  With folded_too,
+    the same call again with the opt-in folded-scale GEMM arithmetic."""
     import hypno_amd as hk
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     nb = q4_bytes(n, m)
@@ -584,14 +585,14 @@ def q4_case(torch, lib, n, m, M, seed, reps, exact_too=False):
 
     out = result(time_calls_graph(torch, issue, reps), M, n, m, nb)
     out["check"] = checked()
-    if exact_too:
-        prev = hk.set_gemm_numerics(hk.GEMM_EXACT)
+    if folded_too:
+        prev = hk.set_gemm_numerics(hk.GEMM_FOLDED)
         try:
             ex = result(time_calls_graph(torch, issue, reps), M, n, m, nb)
             ex["check"] = checked()
         finally:
             hk.set_gemm_numerics(prev)
-        out["exact_nibbles"] = ex
+        out["folded_scales"] = ex
     del arena, x, y
     torch.cuda.empty_cache()
     return out
@@ -611,7 +612,7 @@ def prefill_gemm(torch, lib):
     split-K reduction when the tile grid is small)."""
     out = {}
     for name, n, m in (("gate_up", 8192, 3072), ("down", 3072, 8192)):
-        out[name] = q4_case(torch, lib, n, m, 512, seed=7 + n, reps=20, exact_too=True)
+        out[name] = q4_case(torch, lib, n, m, 512, seed=7 + n, reps=20, folded_too=True)
     return {"workload": "configs[2] Llama-3.2-3B MLP, M=512, Q4_0; GPU time per call incl. "
                         "the fp16 activation pre-pass (the BASELINE outlier channels are "
                         "exercised by the parity tests)", "results": out}
@@ -624,11 +625,11 @@ def mistral_m_sweep(torch, lib):
     for name, n, m in MISTRAL_SHAPES:
         for M in (1, 2, 4, 8, 64, 512, 2048):
             out[f"{name}_M{M}"] = q4_case(torch, lib, n, m, M, seed=n + m + M,
-                                          reps=20 if M <= 64 else 4, exact_too=M >= 512)
+                                          reps=20 if M <= 64 else 4, folded_too=M >= 512)
     return {"workload": "configs[3] Mistral-7B q/o, k/v, gate/up, down at M in "
                         "{1,2,4,8,64,512,2048}; GPU time per call (graph replay); M <= 64 "
-                        "rotates >= 512 MB of weight copies; M >= 512 also in the "
-                        "exact-nibble arithmetic", "results": out}
+                        "rotates >= 512 MB of weight copies; M >= 512 also with the "
+                        "opt-in folded scales", "results": out}
 
 
 def lm_head(torch, lib):

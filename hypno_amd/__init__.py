@@ -7,6 +7,7 @@ the reference's function names (see hypno_amd.kernels).
 from .kernels import (  # noqa: F401
     GEMM_AUTO,
     GEMM_EXACT,
+    GEMM_FOLDED,
     DType,
     GemvPlan,
     HypnoHipError,

@@ -236,7 +236,7 @@ int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
     if (e != hipSuccess) return hip_fail(e, "q4_0 skinny launch");
     return HYPNO_HIP_OK;
   }
-  if (batch >= kGemmMinBatch && gemm_force_exact() && q4_0_gemm_exact_ok(w, w_len, n, m, batch)) {
+  if (batch >= kGemmMinBatch && !gemm_folded() && q4_0_gemm_exact_ok(w, w_len, n, m, batch)) {
     WsLock ws;
     st = scratch_for(q4_0_gemm_exact_workspace_bytes(batch, n, m, cus), ws, "GEMM workspace");
     if (st) return st;
@@ -483,7 +483,7 @@ int hip_status(hipError_t e, const char* what) { return hip_fail(e, what); }
 
 static std::atomic<uint32_t> g_gemm_numerics{HYPNO_HIP_GEMM_AUTO};
 
-bool gemm_force_exact() { return g_gemm_numerics.load() == HYPNO_HIP_GEMM_EXACT; }
+bool gemm_folded() { return g_gemm_numerics.load() == HYPNO_HIP_GEMM_FOLDED; }
 
 hipError_t set_lds_limit(const void* kernel, int bytes) {
   static std::mutex mu;
@@ -1072,7 +1072,7 @@ int hypno_hip_sample_token_dev(uint32_t* token, uint64_t* rng_state, const float
 }
 
 int hypno_hip_set_gemm_numerics(uint32_t mode) {
-  if (mode != HYPNO_HIP_GEMM_AUTO && mode != HYPNO_HIP_GEMM_EXACT) {
+  if (mode != HYPNO_HIP_GEMM_AUTO && mode != HYPNO_HIP_GEMM_EXACT && mode != HYPNO_HIP_GEMM_FOLDED) {
     fail(HYPNO_HIP_EINVAL, "set_gemm_numerics: unknown mode %u", mode);
     return -HYPNO_HIP_EINVAL;
   }

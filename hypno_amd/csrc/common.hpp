@@ -409,7 +409,7 @@ int hip_status(hipError_t e, const char* what);
 
 // True when the caller asked for the exact-nibble GEMM arithmetic
 // (hypno_hip_set_gemm_numerics(HYPNO_HIP_GEMM_EXACT)).
-bool gemm_force_exact();
+bool gemm_folded();
 
 // Raises `kernel`'s dynamic-LDS limit to `bytes` on the current device, once
 // per (kernel, device); safe to call from several threads (api.cpp).

@@ -948,7 +948,7 @@ hipError_t launch_q4_0_gemm_v3(float* y, const uint8_t* w, const float* x, const
     if (e != hipSuccess) return e;
   }
   const size_t wbytes = n * (m / kBlockElems) * kBlockBytes;
-  const bool fold = !gemm_force_exact() &&
+  const bool fold = gemm_folded() &&
                     (batch >= kFoldMinBatch ||
                      (batch >= kFoldMinBatchSmallW && wbytes <= kFoldSmallWBytes));
   Args a;

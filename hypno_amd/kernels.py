@@ -33,17 +33,18 @@ __all__ = [
     "dequantize_q4_0", "register_weight", "unregister_weight", "device_count", "GemvPlan",
     "rms_norm", "rms_norm_in_place", "silu_mul", "matmul_q8_0", "quantize_f32_to_q8_0",
     "dequantize_q8_0", "matmul_q4_0_col", "matmul_vec_col", "set_gemm_numerics",
-    "GEMM_AUTO", "GEMM_EXACT", "q4_0_extract_row", "q8_0_extract_row", "embed_tokens",
+    "GEMM_AUTO", "GEMM_EXACT", "GEMM_FOLDED", "q4_0_extract_row", "q8_0_extract_row", "embed_tokens",
     "argmax", "sample_token",
 ]
 
-GEMM_AUTO, GEMM_EXACT = 0, 1  # HYPNO_HIP_GEMM_AUTO / _EXACT
+GEMM_AUTO, GEMM_EXACT, GEMM_FOLDED = 0, 1, 2  # HYPNO_HIP_GEMM_AUTO / _EXACT / _FOLDED
 
 
 def set_gemm_numerics(mode: int) -> int:
-    """Q4_0 prefill GEMM arithmetic: GEMM_AUTO (fastest per shape) or
-    GEMM_EXACT (integer nibbles, each block's scale applied in fp32).
-    Process-wide; returns the previous mode."""
+    """Q4_0 prefill GEMM arithmetic: GEMM_AUTO (the default) and GEMM_EXACT
+    feed the matrix cores the integer nibbles and apply each block's scale in
+    fp32; GEMM_FOLDED opts into fp16 weights with the scale folded in (from
+    128-256 tokens).  Process-wide; returns the previous mode."""
     prev = int(load().hypno_hip_set_gemm_numerics(int(mode)))
     if prev < 0:
         check(-prev, "set_gemm_numerics")

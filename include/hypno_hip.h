@@ -32,11 +32,13 @@
  *         block scale; the same 1e-4 bar per token.
  *       Q4_0, M = 17..64, and M >= 65 (prefill GEMM): activations rounded to
  *         fp16 after a power-of-two scale per token (undone exactly on the
- *         output), fp32 accumulation on MFMA.  Weights: exact nibbles with
- *         each block's d applied to its partial in fp32, except from 256
- *         tokens (from 128 when W is at most 64 MB), where each weight goes
- *         to the MFMA as fp16 (nibble - 8) * d / 2^E_n (one rounding,
- *         relative 2^-11; 2^E_n just above row n's largest |d|).  Bar:
+ *         output), fp32 accumulation on MFMA.  Weights: the exact integer
+ *         nibbles (fp16 -8..7), each block's d applied to its partial sum in
+ *         fp32.  Only under hypno_hip_set_gemm_numerics(HYPNO_HIP_GEMM_FOLDED)
+ *         do the M >= 65 GEMMs from 256 tokens (from 128 when W is at most
+ *         64 MB) instead feed each weight as fp16 (nibble - 8) * d / 2^E_n
+ *         (one rounding, relative 2^-11; 2^E_n just above row n's largest
+ *         |d|), faster on the largest shapes.  Bar:
  *         ||Y - R||_2 / ||R||_2 <= 2e-3.
  *       FP16: M < 16 fp32 FMAs; M >= 16 as the Q4_0 GEMM with fp16 weights.
  *       Q8_0: M < 16 token by token, activations as three exact int8 digit
@@ -301,14 +303,15 @@ int hypno_hip_silu_mul_dev(float* out, const float* gate, const float* up, size_
                            void* stream);
 
 /* How the Q4_0 prefill GEMM applies the block scales (no counterpart in
- * hypno, whose CPU kernel has one arithmetic).  AUTO (the default) picks per
- * call as described at the top of this file; EXACT always feeds the MFMAs
- * the integer nibbles and applies each block's d to its partial in fp32 (the
- * arithmetic the reference's block-at-a-time dequantisation implies), at
- * some speed from 128-256 tokens up.  Process-wide; returns the previous
- * mode, or -EINVAL for an unknown one. */
+ * hypno, whose CPU kernel has one arithmetic).  AUTO (the default) and EXACT
+ * feed the MFMAs the integer nibbles and apply each block's d to its partial
+ * in fp32 (the arithmetic the reference's block-at-a-time dequantisation
+ * implies); FOLDED opts into folding d into fp16 weights from 128-256 tokens
+ * up, as described at the top of this file.  Process-wide; returns the
+ * previous mode, or -EINVAL for an unknown one. */
 #define HYPNO_HIP_GEMM_AUTO 0u
 #define HYPNO_HIP_GEMM_EXACT 1u
+#define HYPNO_HIP_GEMM_FOLDED 2u
 int hypno_hip_set_gemm_numerics(uint32_t mode);
 
 /* ---------------------------------------------------------------------------

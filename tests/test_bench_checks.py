@@ -45,7 +45,7 @@ def test_bench_compact_record():
         for M in (1, 2, 4, 8, 64, 512, 2048):
             r = _fake_result(10.0 + M / 10, M, n, m)
             if M >= 512:
-                r["exact_nibbles"] = _fake_result(20.0 + M / 10, M, n, m, checked=False)
+                r["folded_scales"] = _fake_result(20.0 + M / 10, M, n, m, checked=False)
             sweep[f"{name}_M{M}"] = r
     sec = {"c3_m_sweep": {"workload": "x" * 300, "results": sweep},
            "model_load": {"open_upload_ms": 900.0, "check": {"checked": True}}}
@@ -55,7 +55,7 @@ def test_bench_compact_record():
     r = sweep["gate_up_M512"]
     assert e["us"] == r["us"] and e["ok"] is True
     assert e["frac"] == max(r["frac_hbm_peak"], r["frac_fp16_peak"])
-    assert flat["c3.gate_up_M512.exact"]["ok"] is False
+    assert flat["c3.gate_up_M512.folded"]["ok"] is False
     assert flat["load"]["us"] == 900000.0
     # 61 entries of this form stay far below the ~8 KB a driver log tail keeps.
     import json

@@ -94,9 +94,9 @@ def _q4_dev_call(lib, y, q, x, n, m, batch, bias=None):
 
 @pytest.mark.parametrize("name,n,m", [("q_o", 4096, 4096), ("k_v", 1024, 4096),
                                       ("gate_up", 14336, 4096), ("down", 4096, 14336)])
-def test_mistral_m2048(torch, hk, lib, orc, name, n, m):
+def test_mistral_m2048(torch, hk, lib, orc, name, n, m, gemm_mode):
     batch = 2048
-    print(f"[case] mistral {name} n={n} m={m} batch={batch}", flush=True)
+    print(f"[case] mistral {name} n={n} m={m} batch={batch} {gemm_mode}", flush=True)
     q, qh = _q4_dev(torch, hk, n, m, seed=n + m)
     gen = torch.Generator(device="cuda").manual_seed(n * 3 + 1)
     x = torch.randn(batch, m, generator=gen, device="cuda")
@@ -163,7 +163,7 @@ def test_gemm_exact_nibbles(torch, hk, lib, orc, name, n, m, batch):
     """The north-star prefill arithmetic (exact integer nibbles into the
     MFMAs, each block's scale applied in fp32; hypno_hip_set_gemm_numerics
     GEMM_EXACT) at configs[2] and the Mistral-7B shapes at 512 and 2048
-    tokens, where the default arithmetic would fold the scales instead.
+    tokens (the default arithmetic, set explicitly here).
     configs[2]'s activations carry its 1% x20 outlier channels."""
     print(f"[case] exact {name} n={n} m={m} batch={batch}", flush=True)
     q, qh = _q4_dev(torch, hk, n, m, seed=n + m + batch + 1)
@@ -329,9 +329,9 @@ def _extreme_tokens(orc, batch, m, seed):
 
 
 @pytest.mark.parametrize("batch", [17, 40, 100, 300])
-def test_q4_0_batched_extreme_tokens(torch, lib, orc, hk, batch):
-    """17 and 40 tokens (few-token plain rows), 100 (GEMM, fp32 block scale),
-    300 (GEMM, folded scale): each token is scaled by its own power of two
+def test_q4_0_batched_extreme_tokens(torch, lib, orc, hk, batch, gemm_mode):
+    """17 and 40 tokens (few-token plain rows), 100 and 300 (GEMM, fp32
+    block scale; 300 under the folded mode: folded scale): each token is scaled by its own power of two
     before the fp16 rounding, so every token meets the GEMM bar on its own."""
     n, m = 1024, 2048
     print(f"[case] q4_0 extreme tokens batch={batch}", flush=True)

@@ -482,13 +482,13 @@ def test_gemm_q4_0(torch, hk, orc, batch, n, m):
 
 
 @pytest.mark.parametrize("batch", [96, 300])
-def test_gemm_q4_0_scale_range(torch, hk, orc, batch):
-    """From 128 tokens (this W is small) the GEMM rounds each weight to fp16
-    after dividing its row by a power of two above the row's largest block
-    scale (below that it scales each block's partial sum in fp32): rows of
-    huge scales (whose
-    weights overflow fp16 unnormalised), tiny scales, mixed scales and zero
-    scales each stay within the GEMM bar column by column."""
+def test_gemm_q4_0_scale_range(torch, hk, orc, batch, gemm_mode):
+    """The default GEMM scales each block's partial sum by its d in fp32;
+    the folded mode, from 128 tokens (this W is small), rounds each weight to
+    fp16 after dividing its row by a power of two above the row's largest
+    block scale.  Either way rows of huge scales (whose weights overflow fp16
+    unnormalised), tiny scales, mixed scales and zero scales each stay within
+    the GEMM bar column by column."""
     n, m = 300, 512
     q = _q4(orc, n, m, seed=41)
     blk = q.reshape(n, m // 32, 18)
@@ -511,9 +511,10 @@ def test_gemm_q4_0_scale_range(torch, hk, orc, batch):
 
 
 @pytest.mark.parametrize("batch,n,m", [(500, 12289, 1024), (512, 12300, 512)])
-def test_gemm_q4_0_256_row_tiles(torch, hk, orc, batch, n, m):
-    """Grids of 256-row tiles that fill the GPU take the 256 x 128 tile
-    kernel: an M tail inside the last tile (500 of 512 rows), an N tail (one
+def test_gemm_q4_0_256_row_tiles(torch, hk, orc, batch, n, m, gemm_mode):
+    """Grids of 256-row tiles that fill the GPU take the 256-row tile
+    kernels (the exact kernel's 16 M-tiles per wave; the folded mode's
+    256 x 128 tiles): an M tail inside the last tile (500 of 512 rows), an N tail (one
     column past 96 tiles, or 12 past), a bias, and rows of extreme block
     scales (as test_gemm_q4_0_scale_range); checked on a seeded sample of
     columns plus the special ones against fp64."""
@@ -574,7 +575,7 @@ def test_gemm_bias_and_tails(torch, hk, orc, m):
 
 
 @pytest.mark.parametrize("batch,n,m", [(128, 1024, 4096), (200, 300, 2048), (512, 1024, 4096)])
-def test_gemm_split_k_deterministic(torch, hk, orc, batch, n, m):
+def test_gemm_split_k_deterministic(torch, hk, orc, batch, n, m, gemm_mode):
     """Small tile grids split K over work-groups and add the partial planes in
     a fixed order: within the GEMM bar, bias included, and bitwise equal from
     run to run."""
