@@ -99,23 +99,12 @@ static_assert(kPrefetch == 4, "stage_barrier's vmcnt(3) is one stage of reads");
 __device__ __forceinline__ void stage_barrier() {
   asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
-// The same, for a stage whose wait also covers the W words `rw` read by
-// global_load_w() one stage earlier: rw passes through the statement, so
-// nothing reads those registers before it.
-__device__ __forceinline__ void stage_barrier(u32x3& rw) {
-  asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" : "+v"(rw) : : "memory");
-}
 
-// 12-byte global read into registers, issued from asm so that the compiler
-// adds no wait of its own for the result (its load-counter model treats the
-// LDS DMAs of the same loop as flat accesses and would wait for all reads,
-// draining the X prefetch).  The caller orders every use of the result
-// after a wait that covers it (stage_barrier(rw) or a vmcnt(0) barrier).
-__device__ __forceinline__ u32x3 global_load_w(const uint8_t* p) {
-  u32x3 v;
-  asm volatile("global_load_dwordx3 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
-  return v;
-}
+// 12-byte global read into registers (global_load_dwordx3), an ordinary
+// load: the compiler tracks the registers it fills and places the wait for
+// them before their first use (the weight unpack a stage later), counting
+// the LDS DMAs issued in between.
+__device__ __forceinline__ u32x3 global_load_w(const uint8_t* p) { return load_global<u32x3>(p); }
 
 // Byte offset of 16-byte chunk c (0..7) of tile row r.
 __device__ __forceinline__ uint32_t tile_off(int r, int c) {
@@ -403,7 +392,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
   RawW r0 = raw_load(0), r1 = raw_load(1);
   RawW rwa = raw_load(2), rwb = raw_load(3);
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier"  // all of it landed
-               : "+v"(r0), "+v"(r1), "+v"(rwa), "+v"(rwb) : : "memory");
+               ::: "memory");
   expand(0, r0);
   expand(1, r1);
   stage_barrier();
@@ -440,7 +429,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
     __builtin_amdgcn_sched_barrier(0);
     issue(s + kPrefetch);
     rwa = raw_load(s + 4);
-    stage_barrier(rwb);  // covers rwb, read one stage earlier
+    stage_barrier();
     if constexpr (kFold) {
       mma_fold(fa, fb, s + 2, rwb, s + 3);
     } else {
@@ -450,11 +439,11 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v3_kernel(const Args a)
     __builtin_amdgcn_sched_barrier(0);
     issue(s + 1 + kPrefetch);
     rwb = raw_load(s + 5);
-    stage_barrier(rwa);
+    stage_barrier();
   }
   // The trailing reads (re-loads of the last stage) land before their
   // registers and LDS slots are reused.
-  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" : "+v"(rwa), "+v"(rwb) : : "memory");
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
 
   // K-group 1 -> LDS -> K-group 0 adds (fixed order) and stores.
   float* red = reinterpret_cast<float*>(smem + kOffA);
@@ -629,7 +618,7 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v4_kernel(const Args a)
   issue(0);
   issue(1);
   RawW r0 = raw_load(0), ra = raw_load(1);
-  asm volatile("s_waitcnt vmcnt(0)" : "+v"(r0), "+v"(ra) : : "memory");
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   {
     u32x4 elo, ehi;
     expand_regs(r0, elo, ehi);
@@ -669,13 +658,13 @@ __global__ void __launch_bounds__(kThreads, 1) q4_0_gemm_v4_kernel(const Args a)
   };
   for (int s = 0; s < steps; s += 2) {
     stage(s, ra);
-    asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" : "+v"(rb) : : "memory");
+    asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     stage(s + 1, rb);
-    asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" : "+v"(ra) : : "memory");
+    asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
   // The trailing reads (re-reads of the last stage) land before the
   // work-group's LDS is released.
-  asm volatile("s_waitcnt vmcnt(0)" : "+v"(ra), "+v"(rb) : : "memory");
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // Output column n scaled by D_n = 2^rowexp[n], row m by 2^xexp[m] (exact).
   // Split K: this range's sum goes to its partial plane, the bias is added
