@@ -65,11 +65,12 @@ constexpr int kERowBytes = kEStageK * 2;
 // 16 rows x 36 bytes of a stage, rounded up to three 256-byte DMAs).
 template <int MT>
 struct ExactGeom {
-  static constexpr int kRing = MT == 8 ? 6 : 4;
-  static constexpr int kWRing = MT == 8 ? 8 : 4;
+  static constexpr int kRing = MT == 16 ? 4 : MT == 8 ? 6 : 8;
+  static constexpr int kWRing = MT == 16 ? 4 : MT == 8 ? 8 : 16;
   static constexpr int kXLds = kRing * 16 * MT * kERowBytes;
   static constexpr int kWSlot = 768;
-  static constexpr int kLds = kXLds + kEWaves * kWRing * kWSlot;
+  static constexpr int kSpare = kXLds + kEWaves * kWRing * kWSlot;  // 1 KB (BM < 64)
+  static constexpr int kLds = kSpare + (MT < 4 ? 1024 : 0);
   static_assert(kLds <= 160 * 1024, "LDS budget");
   static_assert(kWRing >= kRing, "the stage wait below counts X(s+2) as the newer read");
 };
@@ -114,7 +115,10 @@ __global__ void __launch_bounds__(kEThreads, 1) q4_0_gemm_exact_kernel(const Exa
   constexpr int kERing = G::kRing;
   constexpr int kWRing = G::kWRing;
   constexpr int kTile = BM * kERowBytes;  // one stage of X in LDS
-  constexpr int kDx = BM / 64;            // X DMA instructions per wave and stage
+  // X DMA instructions per wave and stage; below 64 rows the waves past the
+  // tile's 8-row groups re-read its last group into a spare LDS chunk, so
+  // every wave issues the same count.
+  constexpr int kDx = BM >= 64 ? BM / 64 : 1;
   extern __shared__ __align__(16) uint8_t smem[];
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -145,7 +149,8 @@ __global__ void __launch_bounds__(kEThreads, 1) q4_0_gemm_exact_kernel(const Exa
   uint32_t xvoff[kDx];
 #pragma unroll
   for (int i = 0; i < kDx; i++) {
-    const int row = 8 * (8 * i + wave) + (lane >> 3);
+    const int grp = min(8 * i + wave, BM / 8 - 1);
+    const int row = 8 * grp + (lane >> 3);
     const int c = (lane & 7) ^ ((row >> 1) & 7);
     xvoff[i] = (uint32_t)(m0 + row) * x_row + (uint32_t)c * 16u;
   }
@@ -154,10 +159,12 @@ __global__ void __launch_bounds__(kEThreads, 1) q4_0_gemm_exact_kernel(const Exa
     const int soff = (s0 + sc) * kERowBytes;
     uint8_t* slot = smem + (s % kERing) * kTile;
 #pragma unroll
-    for (int i = 0; i < kDx; i++)
+    for (int i = 0; i < kDx; i++) {
+      const int grp = 8 * i + wave;
+      uint8_t* dst = grp < BM / 8 ? slot + 8 * grp * kERowBytes : smem + G::kSpare;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          xrs, (__attribute__((address_space(3))) void*)(slot + 8 * (8 * i + wave) * kERowBytes),
-          16, xvoff[i], soff, 0, 0);
+          xrs, (__attribute__((address_space(3))) void*)dst, 16, xvoff[i], soff, 0, 0);
+    }
   };
 
   // --- W: each wave DMAs its own 16 rows' 36 stage bytes into its own ring
@@ -257,7 +264,7 @@ __global__ void __launch_bounds__(kEThreads, 1) q4_0_gemm_exact_kernel(const Exa
   for (int i = 0; i < kERing - 1; i++) issue_x(i);
   for (int i = 0; i < kWRing; i++) issue_w(i);
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(3 * (kWRing - 2)) : "memory");
-  half8 fa[MT];
+  half8 fa[MT], fx;
   read_a(0, 0, fa);
   RawW wc = read_w(0);
   Unp ue;
@@ -291,11 +298,20 @@ __global__ void __launch_bounds__(kEThreads, 1) q4_0_gemm_exact_kernel(const Exa
   constexpr int kStageWait = 3 + (kERing - 3) * (kDx + 3);
   static_assert(kStageWait <= 3 * (kWRing - 2) + kDx + 3 && 3 * kWRing + kERing * kDx < 64,
                 "vmcnt");
-  static_assert(MT >= 8, "the unpack steps need 6 slots per block");
+  // The unpack's steps spread over a block's slots (1..MT-1, or slot 0 when
+  // MT = 1): step k of the odd block's 6 in slot kFirst + k * kSl / 6, the
+  // even block's perm and 6 steps likewise over 7.
+  constexpr int kFirst = MT >= 2 ? 1 : 0;
+  constexpr int kSl = MT >= 2 ? MT - 1 : 1;
+  // Partials of the last kLag slots are scaled in the next stage's first
+  // slots, each with the scale of its own block.
   floatx4 carry[kLag];
+  float dcar[kLag];
 #pragma unroll
-  for (int k = 0; k < kLag; k++) carry[k] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-  float dcarry = 0.0f;
+  for (int k = 0; k < kLag; k++) {
+    carry[k] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    dcar[k] = 0.0f;
+  }
   const uint8_t* abase0 = smem + aoff0;
   const uint8_t* abase1 = smem + aoff1;
   for (int s = 0; s < steps; s++) {
@@ -310,9 +326,12 @@ __global__ void __launch_bounds__(kEThreads, 1) q4_0_gemm_exact_kernel(const Exa
 #pragma unroll
     for (int j = 0; j < 2 * MT; j++) {
       const int kb = j / MT, i = j % MT;
-      pr[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], kb ? fbo : fbe,
+      pr[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16((MT == 1 && kb) ? fx : fa[i], kb ? fbo : fbe,
                                                      floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-      if (j >= 1) {
+      if constexpr (MT == 1) {  // one slot per block: block 1's operand has its own register
+        if (j == 0) fx = *reinterpret_cast<const half8*>(a1);
+        if (j == 1) fa[0] = *reinterpret_cast<const half8*>(a0);
+      } else if (j >= 1) {
         const int pj = j - 1;
         fa[pj % MT] = *reinterpret_cast<const half8*>((pj < MT ? a1 : a0) +
                                                       (pj % MT) * 16 * kERowBytes);
@@ -323,23 +342,29 @@ __global__ void __launch_bounds__(kEThreads, 1) q4_0_gemm_exact_kernel(const Exa
 #pragma unroll
         for (int r = 0; r < 4; r++) acc[u % MT][r] = fmaf(d, pr[u][r], acc[u % MT][r]);
       } else {
+        const int t = (2 * MT - kLag + j) % MT;
 #pragma unroll
-        for (int r = 0; r < 4; r++)
-          acc[MT - kLag + j][r] = fmaf(dcarry, carry[j][r], acc[MT - kLag + j][r]);
+        for (int r = 0; r < 4; r++) acc[t][r] = fmaf(dcar[j], carry[j][r], acc[t][r]);
       }
-      if (kb == 0 && i >= 1 && i <= 6) unp_step(uo, i - 1, wc.x4 >> 16);
+#pragma unroll
+      for (int k = 0; k < 6; k++)
+        if (kb == 0 && i == kFirst + k * kSl / 6) unp_step(uo, k, wc.x4 >> 16);
       if (kb == 0 && i == MT - 1) {
         fbo = __builtin_bit_cast(half8, uo.r);
         dod = uo.d;
       }
-      if (kb == 1 && i == 1) un.q = __builtin_amdgcn_perm(wn.e1, wn.e0, 0x05040302u);
-      if (kb == 1 && i >= 2 && i <= 7) unp_step(un, i - 2, wn.d & 0xFFFFu);
+      if (kb == 1 && i == kFirst) un.q = __builtin_amdgcn_perm(wn.e1, wn.e0, 0x05040302u);
+#pragma unroll
+      for (int k = 0; k < 6; k++)
+        if (kb == 1 && i == kFirst + (k + 1) * kSl / 7) unp_step(un, k, wn.d & 0xFFFFu);
       __builtin_amdgcn_sched_barrier(0);
     }
-    fa[MT - 1] = *reinterpret_cast<const half8*>(a0 + (MT - 1) * 16 * kERowBytes);
+    if constexpr (MT > 1) fa[MT - 1] = *reinterpret_cast<const half8*>(a0 + (MT - 1) * 16 * kERowBytes);
 #pragma unroll
-    for (int k = 0; k < kLag; k++) carry[k] = pr[2 * MT - kLag + k];
-    dcarry = dod;
+    for (int k = 0; k < kLag; k++) {
+      carry[k] = pr[2 * MT - kLag + k];
+      dcar[k] = 2 * MT - kLag + k < MT ? de : dod;
+    }
     // The X DMAs go out before the W DMAs (the wait below counts on it).
     asm volatile("" ::: "memory");
     issue_x(s + kERing - 1);
@@ -351,10 +376,11 @@ __global__ void __launch_bounds__(kEThreads, 1) q4_0_gemm_exact_kernel(const Exa
     de = un.d;
   }
 #pragma unroll
-  for (int k = 0; k < kLag; k++)
+  for (int k = 0; k < kLag; k++) {
+    const int t = (2 * MT - kLag + k) % MT;
 #pragma unroll
-    for (int r = 0; r < 4; r++)
-      acc[MT - kLag + k][r] = fmaf(dcarry, carry[k][r], acc[MT - kLag + k][r]);
+    for (int r = 0; r < 4; r++) acc[t][r] = fmaf(dcar[k], carry[k][r], acc[t][r]);
+  }
   // Every DMA into LDS (the trailing re-reads included) has landed before
   // the work-group's LDS is released.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -475,23 +501,25 @@ struct ExactPlan {
 };
 
 // Tile height and K pieces by a cost model of this kernel on the MI355X
-// (microseconds, measured): a stage of 64 K costs 0.79 on a 128-row tile and
-// 1.22 on a 256-row tile (its B operands serve twice the MFMAs); work-groups
-// beyond one per CU run in further rounds; K pieces add the reduction
-// launch (~2.5) and its read of every partial plane (~4 TB/s).
+// (microseconds, measured): a stage of 64 K costs 0.40 / 0.45 / 0.57 / 0.79
+// / 1.22 on tiles of 16 / 32 / 64 / 128 / 256 rows (a B operand serves MT
+// MFMAs), a round of work-groups (one per CU) ~3 more to fill and drain;
+// K pieces add the reduction launch (~2.5) and its read of every partial
+// plane (~4 TB/s).
 ExactPlan exact_plan(size_t batch, size_t n, size_t m, int num_cus) {
   const size_t tn = (n + kEBN - 1) / kEBN;
   const size_t steps = m / kEStageK;
   ExactPlan best{8, 1, (int)tn, 1};
   double best_cost = 1e300;
-  for (int mt : {8, 16}) {
+  for (int mt : {1, 2, 4, 8, 16}) {
+    if (mt > 1 && (size_t)16 * (mt / 2) >= batch) break;  // taller tiles than the rows
     const size_t tm = (batch + 16 * mt - 1) / (16 * mt);
     const size_t tiles = tm * tn;
-    const double stage_us = mt == 16 ? 1.22 : 0.79;
+    const double stage_us = mt == 16 ? 1.22 : mt == 8 ? 0.79 : mt == 4 ? 0.57 : mt == 2 ? 0.45 : 0.40;
     for (size_t sp = 1; sp <= std::min<size_t>(steps, 64); sp++) {
       const size_t wgs = tiles * sp;
       const size_t rounds = (wgs + num_cus - 1) / num_cus;
-      double cost = (double)rounds * (double)((steps + sp - 1) / sp) * stage_us;
+      double cost = (double)rounds * ((double)((steps + sp - 1) / sp) * stage_us + 3.0);
       if (sp > 1) cost += 2.5 + (double)sp * (double)(batch * n * 4) / 4.0e6;
       if (cost < best_cost * 0.999) {
         best_cost = cost;
@@ -558,16 +586,20 @@ hipError_t launch_q4_0_gemm_exact(float* y, const uint8_t* w, const float* x, co
   const int tiles = p.tiles_m * p.tiles_n;
   a.xcd_map = (tiles % 8) == 0 ? 1 : 0;
   a.splits = p.splits;
-  const void* kern = p.mt == 16 ? reinterpret_cast<const void*>(q4_0_gemm_exact_kernel<16>)
-                                : reinterpret_cast<const void*>(q4_0_gemm_exact_kernel<8>);
-  const int lds = p.mt == 16 ? ExactGeom<16>::kLds : ExactGeom<8>::kLds;
-  if ((e = set_lds_limit(kern, lds)) != hipSuccess) return e;
-  if (p.mt == 16)
-    hipLaunchKernelGGL(q4_0_gemm_exact_kernel<16>, dim3(tiles, p.splits), dim3(kEThreads), lds, s,
-                       a);
-  else
-    hipLaunchKernelGGL(q4_0_gemm_exact_kernel<8>, dim3(tiles, p.splits), dim3(kEThreads), lds, s,
-                       a);
+  auto go = [&](auto kernel, int lds) -> hipError_t {
+    hipError_t le = set_lds_limit(reinterpret_cast<const void*>(kernel), lds);
+    if (le != hipSuccess) return le;
+    hipLaunchKernelGGL(kernel, dim3(tiles, p.splits), dim3(kEThreads), lds, s, a);
+    return hipSuccess;
+  };
+  switch (p.mt) {
+    case 16: e = go(q4_0_gemm_exact_kernel<16>, ExactGeom<16>::kLds); break;
+    case 8: e = go(q4_0_gemm_exact_kernel<8>, ExactGeom<8>::kLds); break;
+    case 4: e = go(q4_0_gemm_exact_kernel<4>, ExactGeom<4>::kLds); break;
+    case 2: e = go(q4_0_gemm_exact_kernel<2>, ExactGeom<2>::kLds); break;
+    default: e = go(q4_0_gemm_exact_kernel<1>, ExactGeom<1>::kLds); break;
+  }
+  if (e != hipSuccess) return e;
   if ((e = hipGetLastError()) != hipSuccess || p.splits == 1) return e;
   const size_t mn = batch * n;
   hipLaunchKernelGGL(exact_split_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0,

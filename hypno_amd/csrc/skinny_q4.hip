@@ -386,12 +386,17 @@ __global__ void __launch_bounds__((SkGeom<MF, RW>::kThreads)) q4_0_skinny_kernel
         }
     }
   } else {
+    // The exponents of this lane's 4 MF tokens, all read before any is used
+    // (rows past M hold 0: the activation rows are padded).
+    u32x4 ex[MF];
+#pragma unroll
+    for (int f = 0; f < MF; f++) ex[f] = load_global<u32x4>(a.xexp + 16 * f + 4 * g);
 #pragma unroll
     for (int f = 0; f < MF; f++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int tkn = 16 * f + 4 * g + i;
-        if (nvalid && tkn < a.M) out[(size_t)tkn * a.N + n] = ldexpf(acc[f][i], a.xexp[tkn]) + bv;
+        if (nvalid && tkn < a.M) out[(size_t)tkn * a.N + n] = ldexpf(acc[f][i], (int)ex[f][i]) + bv;
       }
   }
 }
