@@ -1130,7 +1130,7 @@ def main():
                     help="time only the TinyLlama stream plan (profiling its traffic)")
     ap.add_argument("--only", metavar="WORKLOAD", default=None,
                     help="run only this secondary workload and print its result "
-                         "(c0_single_gemv, c2_prefill_gemm, c3_m_sweep, c4_lm_head, "
+                         "(c0_single_gemv, c1_tinyllama_stream, c2_prefill_gemm, c3_m_sweep, c4_lm_head, "
                          "c4_next_token, model_load, q8_0_decode, col_major); used to "
                          "profile one workload's kernels")
     ap.add_argument("--detail", metavar="FILE", default=None,
@@ -1154,6 +1154,10 @@ def main():
         copy_probe(torch)
         return
     lib = Lib()
+    if args.only == "c1_tinyllama_stream":
+        print(json.dumps({args.only: tinyllama_stream(torch, lib, args.steps, args.warmup)}),
+              flush=True)
+        return
     if args.only is not None:
         fns = dict(SECONDARY)
         if fns.get(args.only) is None:
