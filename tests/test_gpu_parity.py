@@ -601,6 +601,62 @@ def test_gemm_split_k_deterministic(torch, hk, orc, batch, n, m, gemm_mode):
     assert orc.rel_l2(outs[0], ref) <= GEMM_TOL
 
 
+SPLIT_CASES = [(8, 4096, 14336), (40, 1024, 4096), (512, 3072, 8192), (128, 1024, 4096)]
+
+
+def test_split_pieces_repeat_and_graph(torch, hk, orc):
+    """Shapes whose K is split over work-groups (partial planes in the
+    stream's workspace, added in split order by a second kernel): few tokens
+    with hi/lo rows (8 x 4096 x 14336) and fp16 rows (40 x 1024 x 4096), the
+    prefill GEMM (512 x 3072 x 8192, 128 x 1024 x 4096).  Three eager calls
+    each, then all four captured in one HIP graph (consecutive kernels reuse
+    one workspace) and replayed three times: every result bit-identical to
+    the first, and the first within its bar against fp64 on sampled
+    columns."""
+    side = torch.cuda.Stream()
+    cases = []
+    for batch, n, m in SPLIT_CASES:
+        print(f"[case] split pieces batch={batch} n={n} m={m}", flush=True)
+        q = _q4(orc, n, m, seed=batch + n + m)
+        x = orc.normal_f32(batch + 5, (batch, m))
+        cases.append((batch, n, m, q, _gpu(torch, q), _gpu(torch, x), x))
+    side.wait_stream(torch.cuda.current_stream())
+    first = []
+    with torch.cuda.stream(side):
+        for batch, n, m, q, qg, xg, x in cases:
+            outs = []
+            for _ in range(3):
+                y = torch.full((batch * n,), float("nan"), device="cuda")
+                hk.batch_matmul(y, qg, hk.DType.Q4_0, xg, n, m, batch)
+                outs.append(y)
+            torch.cuda.synchronize()
+            got = [o.cpu().numpy().reshape(batch, n) for o in outs]
+            assert np.array_equal(got[0], got[1]) and np.array_equal(got[0], got[2])
+            cols = np.random.default_rng(n).choice(n, min(n, 256), replace=False)
+            w = orc.dequantize_q4_0(q).reshape(n, m)[cols].astype(np.float64)
+            ref = x.astype(np.float64) @ w.T
+            if batch < 16:
+                for t in range(batch):
+                    assert orc.normwise_err(got[0][t, cols], ref[t]) <= GEMV_TOL, t
+            else:
+                assert orc.rel_l2(got[0][:, cols], ref) <= GEMM_TOL
+            first.append(got[0])
+    torch.cuda.synchronize()
+    ys = [torch.full((batch * n,), float("nan"), device="cuda") for batch, n, *_ in cases]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        for (batch, n, m, q, qg, xg, x), y in zip(cases, ys):
+            hk.batch_matmul(y, qg, hk.DType.Q4_0, xg, n, m, batch)
+    for rep in range(3):
+        for y in ys:
+            y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for (batch, n, *_), y, ref in zip(cases, ys, first):
+            assert np.array_equal(y.cpu().numpy().reshape(batch, n), ref), (rep, batch, n)
+
+
 # --- FP16 weights (lm_head variant) --------------------------------------------------
 
 def _f16w(orc, n, m, seed):
