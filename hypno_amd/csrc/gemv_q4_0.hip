@@ -115,8 +115,9 @@ hipError_t launch_q8_0_generic(float* y, const uint8_t* w, const float* x, const
 // instruction), running ahead across job boundaries, and each lane reads its
 // block back as the 20-byte window [18 lane & ~3, +20) of the span.  The
 // ring is private to the wave, so no barrier orders it: a wave waits only
-// for its own oldest DMAs.  A lane-dependent byte permute realigns the
-// nibble dwords (a block starts at byte 0 or 2 of its window); nib ^ 8 read
+// for its own oldest DMAs.  A block starts at byte 0 or 2 of its window:
+// three window dwords and one lane-dependent byte permute give its nibble
+// dwords (in an order the activation digits follow); nib ^ 8 read
 // as a signed i4 is nib - 8, and v_dot8_i32_i4
 // multiplies eight of them with eight i4 digits of the block's activations
 // (the limbs below) into an exact int32 sum; the limb sums combine into one
@@ -470,7 +471,9 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvHead& H, const GemvLaun
   for (int k = 0; k < R; k++) issue(k);
 
   // Byte selectors for v_perm_b32: a block starts at byte 0 (t even) or 2
-  // (t odd) of its window; weight dword j is bytes [2+4j, 6+4j) of the block.
+  // (t odd) of its window; weight dword j is bytes [2+4j, 6+4j) of the block
+  // (Q8_0), and (Q4_0) the permute of window dwords 0 and 4 gives nibble
+  // bytes {0, 1, 14, 15} (t even) or 12-15 (t odd).
   const bool odd = (t & 1) != 0;
   const uint32_t sel_q = odd ? 0x07060504u : 0x05040302u;
   const uint32_t sh_d = odd ? 16u : 0u;
@@ -702,6 +705,24 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvHead& H, const GemvLaun
       for (int v = 0; v < kLimbs * kLD / 4; v++)  // plane v / (kLD / 4), piece v % (kLD / 4)
         xl[m][v] = *reinterpret_cast<const u32x4*>(limbs + (v / (kLD / 4)) * B * kLD + kb * kLD +
                                                    (v % (kLD / 4)) * 4);
+      if constexpr (F == kFmtQ4_0) {
+        // The step takes a block's nibble dwords as window dwords 1, 2, 3 and
+        // one permute of dwords 0 and 4: nibble bytes 2-5, 6-9, 10-13 and
+        // {0, 1, 14, 15} when the block starts at byte 0 of its window (even
+        // t), bytes 0-3 .. 12-15 when it starts at byte 2 (odd t).  The digit
+        // planes are put in the same byte order here, once per job (a dot
+        // product does not depend on the order of its terms).
+        const uint32_t s_main = odd ? 0x03020100u : 0x05040302u;
+        const uint32_t s_last = odd ? 0x07060504u : 0x07060100u;
+#pragma unroll
+        for (int v = 0; v < kLimbs; v++) {
+          const u32x4 a = xl[m][v];
+          xl[m][v] = u32x4{__builtin_amdgcn_perm(a[1], a[0], s_main),
+                           __builtin_amdgcn_perm(a[2], a[1], s_main),
+                           __builtin_amdgcn_perm(a[3], a[2], s_main),
+                           __builtin_amdgcn_perm(a[3], a[0], s_last)};
+        }
+      }
       const int ex = exps[kb];
       xe[m] = ex == kBadExp ? 0 : ex;
       xnan[m] = ex == kBadExp ? __builtin_nanf("") : 0.0f;
@@ -737,7 +758,8 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvHead& H, const GemvLaun
         int acc[MR][kLimbs];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          const uint32_t q = __builtin_amdgcn_perm(d[j + 1], d[j], sel_q) ^ 0x88888888u;
+          const uint32_t q =
+              (j < 3 ? d[j + 1] : __builtin_amdgcn_perm(d[4], d[0], sel_q)) ^ 0x88888888u;
 #pragma unroll
           for (int m = 0; m < MR; m++)
 #pragma unroll
