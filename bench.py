@@ -25,7 +25,9 @@ Also reported, in the same JSON line:
                 TinyLlama decode stream (with its own roofline block, and as
                 grouped / fused / per-call decode steps), configs[2] the
                 prefill GEMM at Llama-3.2-3B MLP shapes (M = 512), configs[3]
-                the Mistral M-sweep {1, 8, 64, 512, 2048}, configs[4] the
+                the Mistral M-sweep {1, 2, 4, 8, 64, 512, 2048} and its
+                decode step in dependency order (per layer [q,k,v], [o],
+                [gate,up], [down] plans, one HIP graph), configs[4] the
                 lm_head in Q4_0 and FP16 at M = 1 and 128; prefill GEMMs in
                 the default exact-nibble arithmetic and again with the opt-in
                 folded scales (hypno_hip_set_gemm_numerics FOLDED);
@@ -168,7 +170,7 @@ def ref_fields(us, flops, nbytes):
 
 SHORT = {"c0_single_gemv": "c0", "c1_tinyllama_stream": "c1", "c2_prefill_gemm": "c2",
          "c3_m_sweep": "c3", "c4_lm_head": "c4", "c4_next_token": "tok", "model_load": "load",
-         "q8_0_decode": "q8", "col_major": "col"}
+         "q8_0_decode": "q8", "col_major": "col", "c3_decode_step": "c3.decode_step_grouped"}
 
 
 def compact(sec):
@@ -361,6 +363,39 @@ def mistral_stream(torch, lib, steps, warmup):
            "arena": arena, "offs": offs, "jobs": jobs}
     plan.close()
     return res
+
+
+def mistral_decode_step(torch, d, steps, warmup):
+    """The Mistral stream's weights as a real decode step runs them: per layer
+    the dependency-respecting plans [q,k,v], [o], [gate,up], [down]
+    (transformer.rs:296-453's order), 128 plan launches replayed as one HIP
+    graph; the fraction is the weight bytes over the step time against the
+    HBM peak."""
+    import hypno_amd as hk
+    arena, jobs, wb = d["arena"], d["jobs"], d["weight_bytes"]
+    groups = [plan_of(hk, arena, jobs, names, layer)
+              for layer in range(MISTRAL_LAYERS)
+              for names in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",))]
+
+    def run_groups():
+        for p in groups:
+            p.run()
+
+    ms, g = time_graph(torch, run_groups, steps, warmup)
+    for _, _, y, *_ in jobs:
+        y.fill_(float("nan"))
+    g.replay()
+    torch.cuda.synchronize()
+    del g
+    gbs = wb / (ms * 1e-3) / 1e9
+    out = {"workload": "configs[3] Mistral-7B decode step at M=1 in dependency order: per "
+                       "layer [q,k,v], [o], [gate,up], [down] plans, replayed as one HIP graph",
+           "launches": sum(p.launches for p in groups), "ms_per_step": round(ms, 5),
+           "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+           "check": check_jobs(torch, arena, jobs, seed=13)}
+    for p in groups:
+        p.close()
+    return out
 
 
 def tinyllama_stream(torch, lib, steps, warmup):
@@ -1158,6 +1193,12 @@ def main():
         print(json.dumps({args.only: tinyllama_stream(torch, lib, args.steps, args.warmup)}),
               flush=True)
         return
+    if args.only == "c3_decode_step":
+        arena, offs, xs, jobs = build_stream(torch, lib, MISTRAL, MISTRAL_LAYERS, seed=11)
+        d = {"arena": arena, "jobs": jobs, "weight_bytes": sum(nb for _, nb in offs)}
+        print(json.dumps({args.only: mistral_decode_step(torch, d, args.steps, args.warmup)}),
+              flush=True)
+        return
     if args.only is not None:
         fns = dict(SECONDARY)
         if fns.get(args.only) is None:
@@ -1222,6 +1263,10 @@ def main():
             "per_launch": launch_stats(d["per"], wb),
         },
     }
+    step = None
+    if not args.no_secondary:
+        print("[bench] secondary: c3_decode_step", file=sys.stderr, flush=True)
+        step = mistral_decode_step(torch, d, args.steps, args.warmup)
     cpu_mats = None
     if not args.no_cpu_baseline:
         arena = d["arena"]
@@ -1231,7 +1276,7 @@ def main():
     del d
     torch.cuda.empty_cache()
     if not args.no_secondary:
-        sec = {}
+        sec = {"c3_decode_step": step}
         for key, fn in SECONDARY:
             print(f"[bench] secondary: {key}", file=sys.stderr, flush=True)
             if fn is None:
