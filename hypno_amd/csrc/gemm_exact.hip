@@ -23,12 +23,12 @@
 //    unpacks the 8 nibbles it feeds to the MFMA (one 16-column x 32-K B
 //    operand: 9 VALU ops, v_perm for the even block's 2-byte offset) and
 //    converts its column's scale (1 op); that B operand then serves all MT
-//    MFMAs of the block.  No weight tile goes through LDS, no barrier waits
-//    on another wave's weights.
-//  * W: four buffer loads per lane and stage (two blocks, 36 bytes of a
-//    row), issued four stages ahead into registers that the compiler tracks
-//    (it places the waits); the stage offset is a scalar, so addresses cost
-//    no VALU.
+//    MFMAs of the block.  No barrier waits on another wave's weights.
+//  * W: each wave DMAs its own 16 rows' 36 bytes of a stage (two blocks)
+//    into its own LDS ring (three 4-byte-per-lane buffer_load ... lds, the
+//    stage offset a scalar, so addresses cost no VALU), kWRing stages deep,
+//    and reads its lanes' words back from there; only the wave's own load
+//    counter orders that ring.
 //  * X: the fp16 rows (permuted per group of 8 columns into the order the
 //    unpack emits weights, as x_row_to_f16 writes them) reach a 4-slot LDS
 //    ring by DMA (buffer_load ... lds, scalar stage offset), three stages
