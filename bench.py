@@ -34,8 +34,8 @@ Also reported, in the same JSON line:
                 model_load, q8_0_decode, col_major.  The final line holds
                 them as a flat map "workload.case" -> {us, frac, ok} (frac =
                 the binding roofline's fraction, ok = output checked); the
-                full result tree goes to stderr as "[bench] detail {...}"
-                (and to --detail FILE), so the line stays ~6 KB.
+                full result tree goes to --detail FILE only, so the line
+                stays ~6 KB and stderr a few progress lines.
 Every workload's output is checked once, untimed, against an fp64 reference
 computed here from the same packed bytes (sampled rows or columns; GEMV
 bar 1e-4 normwise, GEMM bar 2e-3 relative L2): each carries "checked".
@@ -1165,11 +1165,12 @@ def main():
                     help="time only the TinyLlama stream plan (profiling its traffic)")
     ap.add_argument("--only", metavar="WORKLOAD", default=None,
                     help="run only this secondary workload and print its result "
-                         "(c0_single_gemv, c1_tinyllama_stream, c2_prefill_gemm, c3_m_sweep, c4_lm_head, "
+                         "(c0_single_gemv, c1_tinyllama_stream, c2_prefill_gemm, c3_m_sweep, "
+                         "c3_decode_step, c4_lm_head, "
                          "c4_next_token, model_load, q8_0_decode, col_major); used to "
                          "profile one workload's kernels")
     ap.add_argument("--detail", metavar="FILE", default=None,
-                    help="also write every secondary workload's full result tree to FILE "
+                    help="write every secondary workload's full result tree to FILE "
                          "(the final stdout line carries a compact us/frac/ok map)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run only a plain 1 GiB device copy, 20 times (HBM counter "
@@ -1284,13 +1285,12 @@ def main():
             else:
                 sec[key] = fn(torch, lib)
         line["secondary"] = compact(sec)
-        # The full tree goes to stderr (and --detail FILE): the final stdout
-        # line stays a compact record a log tail can hold whole.
-        detail = json.dumps({"secondary": sec})
-        print(f"[bench] detail {detail}", file=sys.stderr, flush=True)
+        # The full tree goes only to --detail FILE: the final stdout line and
+        # the few progress lines on stderr stay small enough for a log tail
+        # of stdout and stderr together to hold the line whole.
         if args.detail:
             with open(args.detail, "w") as f:
-                f.write(detail + "\n")
+                f.write(json.dumps({"secondary": sec}) + "\n")
         checks = []
 
         def walk(o):
