@@ -3,9 +3,10 @@
 //  * f16_generic_kernel: any m, any alignment, any number of tokens; one wave
 //    per (token, row).
 //  * f16_gemv_fast_kernel: one token; each wave owns kRows consecutive rows and
-//    its lanes stream 16-byte chunks (8 weights) of all kRows rows together,
-//    so every activation chunk loaded from cache feeds kRows rows.  Weights
-//    are widened exactly to fp32 and accumulated in fp32.
+//    its lanes stream 16-byte chunks (8 weights) of all kRows rows together
+//    (non-temporal loads), so every activation chunk loaded from cache feeds
+//    kRows rows.  Weights are widened exactly to fp32 and accumulated in
+//    fp32.
 #include "common.hpp"
 
 namespace hypno {
@@ -64,15 +65,18 @@ f16_gemv_fast_kernel(float* __restrict__ y, const uint8_t* __restrict__ w,
   float acc[kF16Rows];
 #pragma unroll
   for (int r = 0; r < kF16Rows; r++) acc[r] = 0.0f;
-#pragma unroll 2
+  // Weights are read once: non-temporal loads (measured on the lm_head, 1.05
+  // GB: 159 us per call against 177 with ordinary loads and the loop
+  // unrolled twice).
+#pragma unroll 1
   for (int c = lane; c < chunks; c += 64) {
     const float4 xa = xv[2 * c];
     const float4 xb = xv[2 * c + 1];
     const float xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
 #pragma unroll
     for (int r = 0; r < kF16Rows; r++) {
-      const uint4 v = wr[r][c];
-      const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+      const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr[r]) + c);
+      const uint32_t u[4] = {v[0], v[1], v[2], v[3]};
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         acc[r] = fmaf(f16_bits_to_f32(u[j] & 0xFFFFu), xs[2 * j], acc[r]);
