@@ -60,3 +60,12 @@ def test_bench_compact_record():
     # 61 entries of this form stay far below the ~8 KB a driver log tail keeps.
     import json
     assert len(json.dumps(flat)) < 3000
+
+
+def test_bench_compact_decode_step():
+    """The Mistral decode step (one dict with ms_per_step and gbs) appears in
+    the flat map under its short name, with its HBM fraction."""
+    step = {"workload": "x", "launches": 128, "ms_per_step": 1.25, "gbs": 3140.7,
+            "frac_hbm_peak": 0.3926, "check": {"checked": True}}
+    flat = bench.compact({"c3_decode_step": step})
+    assert flat == {"c3.decode_step_grouped": {"us": 1250.0, "frac": 0.3926, "ok": True}}
