@@ -32,6 +32,9 @@
 //      - 16 < M <= 64: one fp16 row per token (the prefill GEMM's rounding),
 //        scaled by a power of two per token (x_row_to_f16) that the epilogue
 //        undoes.
+//    On 16-row tiles whose K is split into ranges of at most 8 stages (up to
+//    8 tokens), each work-group converts its own stages the same way into
+//    LDS instead (no pre-pass launch).
 //
 // Requirements (q4_0_skinny_ok): K % 256 == 0, w 16-byte aligned (row
 // segments of a stage are then 16-byte aligned), W and X under 4 GB, w
@@ -163,6 +166,7 @@ struct SkinnyArgs {
   float* part;        // [splits][M][N] partial sums when splits > 1
   const uint8_t* w;
   const uint8_t* xa;
+  const float* x;     // fp32 activations (read by the kernel itself with INX)
   const float* inv_s;
   const int* xexp;    // without SPLIT: token t's row holds x_t times 2^-xexp[t]
   const float* bias;
@@ -184,15 +188,28 @@ struct SkinnyArgs {
 // operand of lane (n, g) for a block is its quarter g (4 nibble bytes) of
 // row n; it becomes exact fp16 (nib - 8) in registers, and the block's
 // partial is scaled in fp32.
-template <int MF, bool SPLIT, int RW>
+// INX (one A fragment, hi/lo rows, K split into ranges of at most
+// kInxStages stages): the work-group converts its own stages of X (fp32)
+// into the hi/lo rows and 1/s, the x_skinny_kernel arithmetic, straight
+// into an LDS region ahead of the ring, instead of a pre-pass launch; the
+// ring then carries W only.
+constexpr int kInxStages = 8;
+
+template <int MF, bool SPLIT, int RW, bool INX>
 __global__ void __launch_bounds__((SkGeom<MF, RW>::kThreads)) q4_0_skinny_kernel(const SkinnyArgs a) {
   using G = SkGeom<MF, RW>;
+  static_assert(!INX || (MF == 1 && SPLIT), "in-kernel X: one fragment, hi/lo rows");
+  // INX: converted stage ls at ls * kXStride (A rows, then 16 floats of 1/s);
+  // the ring follows at kXOff with slots of W only.
+  constexpr int kXStride = G::kXBytes + 64;
+  constexpr int kXOff = INX ? kInxStages * kXStride : 0;
+  constexpr int kSlotB = INX ? RW * kSkWBytes : G::kSlot;
   extern __shared__ __align__(16) uint8_t smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rw = wave % RW;  // row group: W rows 16 rw .. 16 rw + 15 of the tile
   const int kg = wave / RW;  // K-group: blocks 2 kg, 2 kg + 1 of every stage
-  const bool xact = wave * G::kXDma < G::kXTot;  // this wave DMAs X pieces
+  const bool xact = !INX && wave * G::kXDma < G::kXTot;  // this wave DMAs X pieces
   const int n16 = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 16 * RW + 16 * rw;  // this wave's first W row
   const int gsteps = a.K / kSkStageK;
@@ -219,8 +236,8 @@ __global__ void __launch_bounds__((SkGeom<MF, RW>::kThreads)) q4_0_skinny_kernel
   constexpr int kWLast = 16 * kSkRowPieces - 64 * (kSkWDma - 1);
   constexpr int kMh = MF == 1 ? 8 : 16;
   constexpr int kInvOff = 16 * kSkRowPieces * 16;  // 2304
-  const int w_active = kWLast + (SPLIT ? kMh / 4 : 0);
-  const bool inv_lane = SPLIT && lane >= kWLast;
+  const int w_active = kWLast + (SPLIT && !INX ? kMh / 4 : 0);
+  const bool inv_lane = SPLIT && !INX && lane >= kWLast;
   // X DMA i of this wave (0..15; only waves below kXTot / kXDma issue any)
   // covers pieces p = 64 (wave * kXDma + i) + lane of the chunk: row p / 32,
   // slot p % 32 holding logical piece (p % 32) ^ (row & 15).
@@ -235,14 +252,14 @@ __global__ void __launch_bounds__((SkGeom<MF, RW>::kThreads)) q4_0_skinny_kernel
   // slots no later stage reads) into ring slot s % kRing.
   auto issue = [&](int s) {
     const int gs = s0 + (s < steps ? s : steps - 1);
-    uint8_t* slot = smem + (s % G::kRing) * G::kSlot;
+    uint8_t* slot = smem + kXOff + (s % G::kRing) * kSlotB;
     const uint8_t* xsrc = a.xa + (size_t)gs * kSkXRowBytes;
     if (xact) {
 #pragma unroll
       for (int i = 0; i < G::kXDma; i++) dma16(xsrc + xoff[i], slot + (wave * G::kXDma + i) * 1024);
     }
     const uint8_t* wsrc = a.w + (size_t)gs * kSkRowBytes;
-    uint8_t* wdst = slot + G::kXBytes + rw * kSkWBytes;
+    uint8_t* wdst = slot + (INX ? 0 : G::kXBytes) + rw * kSkWBytes;
     if (kg == 0) {
       dma16(wsrc + woff[0], wdst);
     } else if (kg == 1) {
@@ -260,13 +277,15 @@ __global__ void __launch_bounds__((SkGeom<MF, RW>::kThreads)) q4_0_skinny_kernel
   for (int f = 0; f < MF; f++) acc[f] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
   // All LDS operands of a stage are read first (one wait), then the four
   // block pairs are unpacked and multiplied.
-  auto compute = [&](int slot_i) {
+  auto compute = [&](int slot_i, int ls) {
     floatx4 st_[MF];
 #pragma unroll
     for (int f = 0; f < MF; f++) st_[f] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     floatx4(&st)[MF] = SPLIT ? st_ : acc;  // stage sums (SPLIT) or the totals
-    const uint8_t* xs = smem + slot_i * G::kSlot;
-    const uint32_t* wr = reinterpret_cast<const uint32_t*>(xs + G::kXBytes + rw * kSkWBytes +
+    // A rows and (SPLIT) 1/s of the stage; its W area
+    const uint8_t* xs = INX ? smem + ls * kXStride : smem + slot_i * G::kSlot;
+    const uint8_t* ws = INX ? smem + kXOff + slot_i * kSlotB : xs + G::kXBytes;
+    const uint32_t* wr = reinterpret_cast<const uint32_t*>(ws + rw * kSkWBytes +
                                                            n16 * kSkRowBytes);
     // this K-group's block pairs jp = 2 kg, 2 kg + 1 of the stage: blocks 2 jp
     // (byte 36 jp of the row) and 2 jp + 1 (byte 36 jp + 18)
@@ -313,8 +332,9 @@ __global__ void __launch_bounds__((SkGeom<MF, RW>::kThreads)) q4_0_skinny_kernel
     // SPLIT: this lane's tokens (4 g + i, hi and lo alike; g mod 2 when the hi
     // and lo rows share one frag) were scaled by s of this stage.
     if (SPLIT) {
-      const floatx4 inv = *reinterpret_cast<const floatx4*>(
-          xs + G::kXBytes + rw * kSkWBytes + kInvOff + 16 * (MF == 1 ? (g & 1) : g));
+      const uint8_t* ip = INX ? xs + G::kXBytes : ws + rw * kSkWBytes + kInvOff;
+      const floatx4 inv =
+          *reinterpret_cast<const floatx4*>(ip + 16 * (MF == 1 ? (g & 1) : g));
 #pragma unroll
       for (int f = 0; f < MF; f++)
 #pragma unroll
@@ -322,7 +342,69 @@ __global__ void __launch_bounds__((SkGeom<MF, RW>::kThreads)) q4_0_skinny_kernel
     }
   };
 
-  for (int s = 0; s < G::kRing - 1; s++) issue(s);
+  if constexpr (INX) {
+    // (token t < 8, local stage ls) pairs, 32 lanes each: lane gi takes
+    // columns 8 gi .. 8 gi + 7 of the stage.  All x reads go out first, then
+    // the ring's first W DMAs, then the conversion (which waits on the x
+    // reads only).
+    constexpr int kGroups = G::kThreads / 32;
+    constexpr int kRounds = (kMh * kInxStages + kGroups - 1) / kGroups;
+    const int gi = threadIdx.x & 31;
+    const int pairs = kMh * steps;
+    float v[kRounds][8];
+#pragma unroll
+    for (int r = 0; r < kRounds; r++) {
+      const int p = (int)(threadIdx.x >> 5) + r * kGroups;
+      const int t = p % kMh, ls = p / kMh;
+      if (p < pairs && t < a.M) {
+        const float* xp = a.x + (size_t)t * a.K + (size_t)(s0 + ls) * kSkStageK + 8 * gi;
+        const float4 v0 = load_global<float4>(xp);
+        const float4 v1 = load_global<float4>(xp + 4);
+        v[r][0] = v0.x; v[r][1] = v0.y; v[r][2] = v0.z; v[r][3] = v0.w;
+        v[r][4] = v1.x; v[r][5] = v1.y; v[r][6] = v1.z; v[r][7] = v1.w;
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[r][k] = 0.0f;
+      }
+    }
+    for (int s = 0; s < G::kRing - 1; s++) issue(s);
+#pragma unroll
+    for (int r = 0; r < kRounds; r++) {
+      const int p = (int)(threadIdx.x >> 5) + r * kGroups;
+      if (p < pairs) {  // whole 32-lane groups
+        const int t = p % kMh, ls = p / kMh;
+        // the stage's largest |x| (bit pattern; NaN and inf above finite)
+        uint32_t mb = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) mb = max(mb, __float_as_uint(v[r][k]) & 0x7FFFFFFFu);
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, o, 64));
+        const float amax = __uint_as_float(mb);
+        float sc = 1.0f;
+        if (amax > 0.0f && amax < __builtin_inff())
+          sc = ldexpf(1.0f, min(15 - __builtin_amdgcn_frexp_expf(amax), 126));
+        float w8[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) w8[k] = v[r][k] * sc;
+        constexpr int perm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+        u32x4 h, l;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const float pp = w8[perm[2 * j]], qq = w8[perm[2 * j + 1]];
+          h[j] = pack2h(pp, qq);
+          const float ph = (float)(_Float16)pp, qh = (float)(_Float16)qq;
+          l[j] = pack2h(pp - ph, qq - qh);
+        }
+        uint8_t* xs = smem + ls * kXStride;
+        const int rh = t, rl = kMh + t;  // hi and lo A rows; piece gi at slot gi ^ (row & 15)
+        *reinterpret_cast<u32x4*>(xs + rh * kSkXRowBytes + ((gi ^ (rh & 15)) << 4)) = h;
+        *reinterpret_cast<u32x4*>(xs + rl * kSkXRowBytes + ((gi ^ (rl & 15)) << 4)) = l;
+        if (gi == 0) reinterpret_cast<float*>(xs + G::kXBytes)[t] = 1.0f / sc;
+      }
+    }
+  } else {
+    for (int s = 0; s < G::kRing - 1; s++) issue(s);
+  }
   for (int s = 0; s < steps; s++) {
     // stage s landed (each wave waits for its own DMAs), slot of s-1 free
     // this wave's reads per stage: X pieces (xact) + one W DMA (K-groups 0-2)
@@ -338,7 +420,7 @@ __global__ void __launch_bounds__((SkGeom<MF, RW>::kThreads)) q4_0_skinny_kernel
         wait_reads_barrier<0>();
     }
     issue(s + G::kRing - 1);
-    compute(s % G::kRing);
+    compute(s % G::kRing, s);
   }
   // Trailing DMAs landed and every wave is done with the ring; then K-group 1
   // hands its sums to K-group 0 through LDS (a fixed order: deterministic).
@@ -479,13 +561,16 @@ int skinny_splits(size_t n, size_t m, size_t batch, int num_cus) {
   return (int)sp;
 }
 
-template <int MF, bool SPLIT, int RW>
+template <int MF, bool SPLIT, int RW, bool INX = false>
 hipError_t launch_mf(const SkinnyArgs& a, dim3 grid, hipStream_t s) {
   using G = SkGeom<MF, RW>;
-  hipError_t e = set_lds_limit(reinterpret_cast<const void*>(q4_0_skinny_kernel<MF, SPLIT, RW>),
-                               G::kLds);
+  constexpr int kInxLds = kInxStages * (G::kXBytes + 64) + G::kRing * RW * kSkWBytes;
+  constexpr int lds = INX ? kInxLds : G::kLds;
+  static_assert(lds <= 160 * 1024 && G::kWaves * MF * 4 * 64 * 4 <= lds, "LDS budget");
+  hipError_t e = set_lds_limit(
+      reinterpret_cast<const void*>(q4_0_skinny_kernel<MF, SPLIT, RW, INX>), lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((q4_0_skinny_kernel<MF, SPLIT, RW>), grid, dim3(G::kThreads), G::kLds, s, a);
+  hipLaunchKernelGGL((q4_0_skinny_kernel<MF, SPLIT, RW, INX>), grid, dim3(G::kThreads), lds, s, a);
   return hipGetLastError();
 }
 
@@ -528,7 +613,20 @@ hipError_t launch_q4_0_skinny(float* y, const uint8_t* w, const float* x, const 
                                      round256(m / kSkStageK * 16 * 4));
   float* part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(xexp) + 256);
   hipError_t e;
-  if (sh.split) {
+  const int sp = skinny_splits(n, m, batch, num_cus);
+  const size_t gsteps = m / kSkStageK;
+  // 16-row tiles whose K is split into ranges of a few stages: the kernel
+  // converts its own stages of X (no pre-pass launch).  Measured on the
+  // Mistral shapes at 5-8 tokens: k/v (16-row tiles, 2 stages per range) 7.7
+  // against 8.5 us per call; q/o (64-row tiles, 2 stages) unchanged, down
+  // (64-row tiles, 7 stages) 2.5 us slower, so 64-row tiles keep the
+  // pre-pass.
+  const int rw = skinny_rw(n, m, batch, num_cus);
+  const bool inx = sh.split && sh.mf == 1 && sp > 1 && rw == 1 &&
+                   (gsteps + sp - 1) / sp <= (size_t)kInxStages && ((uintptr_t)x & 15) == 0;
+  if (inx) {
+    e = hipSuccess;
+  } else if (sh.split) {
     const int stages = (int)(m / kSkStageK);
     hipLaunchKernelGGL(x_skinny_kernel, dim3((unsigned)((stages + 7) / 8), (unsigned)sh.mh),
                        dim3(256), 0, s, xa, inv_s, x, (int)batch, (int)m, sh.mh, sh.split);
@@ -537,12 +635,12 @@ hipError_t launch_q4_0_skinny(float* y, const uint8_t* w, const float* x, const 
     e = launch_x_rows_f16(x, batch, (size_t)sh.rows, m, xa, xexp, true, s);
   }
   if (e != hipSuccess) return e;
-  const int sp = skinny_splits(n, m, batch, num_cus);
   SkinnyArgs a;
   a.y = y;
   a.part = part;
   a.w = w;
   a.xa = xa;
+  a.x = x;
   a.inv_s = inv_s;
   a.xexp = xexp;
   a.bias = bias;
@@ -551,9 +649,10 @@ hipError_t launch_q4_0_skinny(float* y, const uint8_t* w, const float* x, const 
   a.K = (int)m;
   a.split = sh.split;
   a.splits = sp;
-  const int rw = skinny_rw(n, m, batch, num_cus);
   const dim3 grid((unsigned)((n + 16 * rw - 1) / (16 * rw)), (unsigned)sp);
-  if (sh.mf == 1)
+  if (inx)
+    e = launch_mf<1, true, 1, true>(a, grid, s);
+  else if (sh.mf == 1)
     e = launch_rw<1, true>(a, rw, grid, s);
   else if (sh.mf == 2)
     e = sh.split ? launch_rw<2, true>(a, rw, grid, s) : launch_rw<2, false>(a, rw, grid, s);
