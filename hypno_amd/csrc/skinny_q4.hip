@@ -618,9 +618,8 @@ hipError_t launch_q4_0_skinny(float* y, const uint8_t* w, const float* x, const 
   // 16-row tiles whose K is split into ranges of a few stages: the kernel
   // converts its own stages of X (no pre-pass launch).  Measured on the
   // Mistral shapes at 5-8 tokens: k/v (16-row tiles, 2 stages per range) 7.7
-  // against 8.5 us per call; q/o (64-row tiles, 2 stages) unchanged, down
-  // (64-row tiles, 7 stages) 2.5 us slower, so 64-row tiles keep the
-  // pre-pass.
+  // against 8.5 us per call; down (64-row tiles, 7 stages per range) 2.5 us
+  // slower, so 64-row tiles keep the pre-pass.
   const int rw = skinny_rw(n, m, batch, num_cus);
   const bool inx = sh.split && sh.mf == 1 && sp > 1 && rw == 1 &&
                    (gsteps + sp - 1) / sp <= (size_t)kInxStages && ((uintptr_t)x & 15) == 0;
