@@ -216,12 +216,14 @@ int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
     return HYPNO_HIP_OK;
   };
   hipError_t e;
-  // Two x rows, up to four on a matrix of at most 16M weights: one pass of
-  // the streaming GEMV with every block multiplied by each row (measured
-  // faster than the few-token kernel's pre-pass, main and reduction launches
-  // there; slower beyond, where the dot products, which grow with the rows,
-  // bound it).
-  const bool few_rows = batch == 2 || (batch <= 4 && n * m <= ((size_t)16 << 20));
+  // Two x rows, three on a matrix of at most 16M weights: one pass of the
+  // streaming GEMV with every block multiplied by each row (measured faster
+  // than the few-token kernel's launches there; slower beyond, where the dot
+  // products, which grow with the rows, bound it).  At four rows the
+  // few-token kernel wins or ties on the Mistral-7B and TinyLlama shapes
+  // (k/v 7.8 against 8.3 and 5.9 against 6.8 us per call, TinyLlama gate/up
+  // 8.7 against 9.3) but for TinyLlama q/o (7.7 against 7.5).
+  const bool few_rows = batch == 2 || (batch == 3 && n * m <= ((size_t)16 << 20));
   if (batch >= 2 && few_rows && q4_0_gemv_rows_ok(w, w_len, n, m, batch) && aligned16(x)) {
     e = launch_q4_0_gemv_rows(y, w, x, bias, n, m, (int)batch, cus, s);
     if (e != hipSuccess) return hip_fail(e, "q4_0 few-row GEMV launch");

@@ -267,13 +267,12 @@ def test_skinny_split_k_repeat(torch, hk, orc, batch, n, m):
 
 
 @pytest.mark.parametrize("batch,n,m", [
-    (2, 4096, 14336), (2, 4097, 256), (3, 1000, 4096), (4, 1024, 4096), (4, 300, 2048),
-    (4, 4096, 4096), (3, 257, 2048),
+    (2, 4096, 14336), (2, 4097, 256), (3, 1000, 4096), (3, 1024, 4096), (3, 300, 2048),
+    (3, 4096, 4096), (3, 257, 2048),
 ])
 def test_gemv_few_rows(torch, hk, orc, batch, n, m):
-    """Two rows (up to four on a matrix of at most 16M weights) take one
-    pass of the
-    streaming GEMV with every block multiplied by each row: each row's result
+    """Two rows (three on a matrix of at most 16M weights) take one pass of
+    the streaming GEMV with every block multiplied by each row: each row's result
     is bit-identical to that row alone through the one-row GEMV (the same
     integer digit products, block partials and fixed-order sums), and within
     the GEMV bar of the oracle's per-token GEMVs (turbo.rs:329-331).  Wide
@@ -285,10 +284,12 @@ def test_gemv_few_rows(torch, hk, orc, batch, n, m):
     x = orc.normal_f32(batch + 300, (batch, m))
     x[0, 5] = np.float32(1e4)
     x[1] *= np.float32(1e-5)
+    nan_row = 2 if batch > 2 and n % 2 == 1 else -1
     if batch > 2:
-        x[2] = 0.0
-    if batch > 3:
-        x[3, 77] = np.float32("nan")
+        if nan_row == 2:
+            x[2, 77] = np.float32("nan")
+        else:
+            x[2] = 0.0
     bias = orc.normal_f32(batch + 400, n)
     qg, xg, bg = _gpu(torch, q), _gpu(torch, x), _gpu(torch, bias)
 
@@ -307,11 +308,41 @@ def test_gemv_few_rows(torch, hk, orc, batch, n, m):
     for t in range(batch):
         one = call(xg.data_ptr() + 4 * t * m, 1)[0]
         assert np.array_equal(got[t], one, equal_nan=True), t
-        if t == 3:
+        if t == nan_row:
             assert np.isnan(got[t]).all() == np.isnan(ref[t]).all()
         else:
             assert orc.normwise_err(got[t], ref[t]) <= GEMV_TOL, t
     assert np.array_equal(got, call(xg.data_ptr(), batch), equal_nan=True)
+
+
+@pytest.mark.parametrize("batch,n,m", [(4, 1024, 4096), (8, 1024, 4096), (5, 256, 2048),
+                                        (8, 2000, 2048), (6, 4096, 14336)])
+def test_skinny_own_activation_stages(torch, hk, orc, batch, n, m):
+    """Few tokens on 16-row tiles with K split into short ranges: each
+    work-group converts its own activation stages (hi/lo rows, 1/s per
+    stage) instead of a pre-pass.  Wide ranges, a 1e4 outlier, a zero token
+    and a NaN in the last token's last stage; bit-identical repeats;
+    every token within the GEMV bar of the oracle (the NaN token: NaN where
+    the oracle's is)."""
+    q = _q4(orc, n, m, seed=batch * 7 + n)
+    x = orc.normal_f32(batch + 900, (batch, m))
+    x[0] *= np.float32(3e3)
+    x[1, 3] = np.float32(1e4)
+    if batch > 3:
+        x[2] = 0.0
+    x[batch - 1, m - 5] = np.float32("nan")
+    qg, xg = _gpu(torch, q), _gpu(torch, x)
+    got = _run_q4(torch, hk, qg, xg, None, n, m, batch)
+    again = _run_q4(torch, hk, qg, xg, None, n, m, batch)
+    assert np.array_equal(got, again, equal_nan=True)
+    ref = orc.batch_matmul(q, 3, x, n, m, batch)
+    for t in range(batch - 1):
+        if t == 2 and batch > 3:
+            assert np.all(got[t] == 0.0)
+        else:
+            assert orc.normwise_err(got[t], ref[t]) <= GEMV_TOL, t
+    assert np.array_equal(np.isnan(got[batch - 1]), np.isnan(ref[batch - 1]))
+
 
 def test_skinny_wide_range_activations(torch, hk, orc):
     """Per-token power-of-two scaling: tokens of very different magnitude,
