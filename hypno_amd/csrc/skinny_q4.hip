@@ -53,6 +53,46 @@ __device__ __forceinline__ uint32_t pack2h(float a, float b) {
          ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
 }
 
+// The pre-pass arithmetic for lane gi's 8 columns of one token's stage
+// (32-lane groups): s = 2^(15 - e) with max |x| < 2^e over the group, so
+// max |x| s < 2^15 (zero, inf and NaN stages keep s = 1: their products
+// propagate as the reference's would); hi = fp16(x s), lo = fp16(x s - hi),
+// columns permuted per group of 8 to the unpack order.
+struct StagePieces {
+  u32x4 h, l;
+  float inv;
+};
+__device__ __forceinline__ StagePieces split_stage8(const float (&v)[8]) {
+  uint32_t mb = 0;  // largest |x| of the stage by bit pattern (NaN and inf above finite)
+#pragma unroll
+  for (int k = 0; k < 8; k++) mb = max(mb, __float_as_uint(v[k]) & 0x7FFFFFFFu);
+  // over the 32 lanes: DPP quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror,
+  // row_mirror (all 16 lanes of a row), then the other row of the group
+  mb = max(mb, (uint32_t)__builtin_amdgcn_mov_dpp((int)mb, 0xB1, 0xF, 0xF, false));
+  mb = max(mb, (uint32_t)__builtin_amdgcn_mov_dpp((int)mb, 0x4E, 0xF, 0xF, false));
+  mb = max(mb, (uint32_t)__builtin_amdgcn_mov_dpp((int)mb, 0x141, 0xF, 0xF, false));
+  mb = max(mb, (uint32_t)__builtin_amdgcn_mov_dpp((int)mb, 0x140, 0xF, 0xF, false));
+  mb = max(mb, (uint32_t)__shfl_xor((int)mb, 16, 64));
+  const float amax = __uint_as_float(mb);
+  float sc = 1.0f;
+  if (amax > 0.0f && amax < __builtin_inff())
+    sc = ldexpf(1.0f, min(15 - __builtin_amdgcn_frexp_expf(amax), 126));
+  float w8[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) w8[k] = v[k] * sc;
+  constexpr int perm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+  StagePieces r;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const float pp = w8[perm[2 * j]], qq = w8[perm[2 * j + 1]];
+    r.h[j] = pack2h(pp, qq);
+    const float ph = (float)(_Float16)pp, qh = (float)(_Float16)qq;
+    r.l[j] = pack2h(pp - ph, qq - qh);
+  }
+  r.inv = 1.0f / sc;
+  return r;
+}
+
 // Pre-pass: X fp32 [M][K] -> A rows fp16 [rows][K], in stages of 256 K
 // (the main kernel's stage), plus 1/s per token and stage when split.
 // 32 lanes per (row, stage): lane i converts K elements 8i .. 8i+7 of the
@@ -80,34 +120,19 @@ x_skinny_kernel(uint8_t* __restrict__ xa, float* __restrict__ inv_s, const float
   const float* xr = x + (size_t)r * K + 8 * g;
   const float4 a0 = load_global<float4>(xr);
   const float4 a1 = load_global<float4>(xr + 4);
-  float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+  const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
   if (split) {
-    uint32_t mb = 0;  // largest |x| of the stage by bit pattern (NaN/inf above finite)
-#pragma unroll
-    for (int k = 0; k < 8; k++) mb = max(mb, __float_as_uint(v[k]) & 0x7FFFFFFFu);
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, o, 64));
-    const float amax = __uint_as_float(mb);
-    // s = 2^(15 - e) with amax < 2^e, so amax * s < 2^15; zero, inf and NaN
-    // stages keep s = 1 (their products propagate as the reference's would)
-    float s = 1.0f;
-    if (amax > 0.0f && amax < __builtin_inff())
-      s = ldexpf(1.0f, min(15 - __builtin_amdgcn_frexp_expf(amax), 126));
-#pragma unroll
-    for (int k = 0; k < 8; k++) v[k] *= s;
-    if (gi == 0) inv_s[(size_t)c * Mh + r] = 1.0f / s;
+    const StagePieces q = split_stage8(v);
+    hi_row[g] = q.h;
+    lo_row[g] = q.l;
+    if (gi == 0) inv_s[(size_t)c * Mh + r] = q.inv;
+    return;
   }
   constexpr int perm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
-  u32x4 h, l;
+  u32x4 h;
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const float p = v[perm[2 * j]], q = v[perm[2 * j + 1]];
-    h[j] = pack2h(p, q);
-    const float ph = (float)(_Float16)p, qh = (float)(_Float16)q;
-    l[j] = pack2h(p - ph, q - qh);
-  }
+  for (int j = 0; j < 4; j++) h[j] = pack2h(v[perm[2 * j]], v[perm[2 * j + 1]]);
   hi_row[g] = h;
-  if (split) lo_row[g] = l;
 }
 
 // Stage geometry.  A stage is 256 K (8 Q4_0 blocks) of every row and token:
@@ -373,33 +398,12 @@ __global__ void __launch_bounds__((SkGeom<MF, RW>::kThreads)) q4_0_skinny_kernel
       const int p = (int)(threadIdx.x >> 5) + r * kGroups;
       if (p < pairs) {  // whole 32-lane groups
         const int t = p % kMh, ls = p / kMh;
-        // the stage's largest |x| (bit pattern; NaN and inf above finite)
-        uint32_t mb = 0;
-#pragma unroll
-        for (int k = 0; k < 8; k++) mb = max(mb, __float_as_uint(v[r][k]) & 0x7FFFFFFFu);
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, o, 64));
-        const float amax = __uint_as_float(mb);
-        float sc = 1.0f;
-        if (amax > 0.0f && amax < __builtin_inff())
-          sc = ldexpf(1.0f, min(15 - __builtin_amdgcn_frexp_expf(amax), 126));
-        float w8[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) w8[k] = v[r][k] * sc;
-        constexpr int perm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
-        u32x4 h, l;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const float pp = w8[perm[2 * j]], qq = w8[perm[2 * j + 1]];
-          h[j] = pack2h(pp, qq);
-          const float ph = (float)(_Float16)pp, qh = (float)(_Float16)qq;
-          l[j] = pack2h(pp - ph, qq - qh);
-        }
+        const StagePieces q = split_stage8(v[r]);
         uint8_t* xs = smem + ls * kXStride;
         const int rh = t, rl = kMh + t;  // hi and lo A rows; piece gi at slot gi ^ (row & 15)
-        *reinterpret_cast<u32x4*>(xs + rh * kSkXRowBytes + ((gi ^ (rh & 15)) << 4)) = h;
-        *reinterpret_cast<u32x4*>(xs + rl * kSkXRowBytes + ((gi ^ (rl & 15)) << 4)) = l;
-        if (gi == 0) reinterpret_cast<float*>(xs + G::kXBytes)[t] = 1.0f / sc;
+        *reinterpret_cast<u32x4*>(xs + rh * kSkXRowBytes + ((gi ^ (rh & 15)) << 4)) = q.h;
+        *reinterpret_cast<u32x4*>(xs + rl * kSkXRowBytes + ((gi ^ (rl & 15)) << 4)) = q.l;
+        if (gi == 0) reinterpret_cast<float*>(xs + G::kXBytes)[t] = q.inv;
       }
     }
   } else {

@@ -316,11 +316,13 @@ def test_gemv_few_rows(torch, hk, orc, batch, n, m):
 
 
 @pytest.mark.parametrize("batch,n,m", [(4, 1024, 4096), (8, 1024, 4096), (5, 256, 2048),
-                                        (8, 2000, 2048), (6, 4096, 14336)])
+                                        (8, 2000, 2048), (6, 4096, 14336), (8, 14336, 4096),
+                                        (4, 14336, 4096), (7, 4096, 4096), (8, 300, 8192)])
 def test_skinny_own_activation_stages(torch, hk, orc, batch, n, m):
-    """Few tokens on 16-row tiles with K split into short ranges: each
-    work-group converts its own activation stages (hi/lo rows, 1/s per
-    stage) instead of a pre-pass.  Wide ranges, a 1e4 outlier, a zero token
+    """Up to 8 tokens, activations as hi/lo rows with 1/s per stage: converted
+    by the work-groups themselves (16-row tiles whose K is split into short
+    ranges) or by the pre-pass launch (64-row tiles: gate/up, down; 16-row
+    tiles without such a split: q/o).  Wide ranges, a 1e4 outlier, a zero token
     and a NaN in the last token's last stage; bit-identical repeats;
     every token within the GEMV bar of the oracle (the NaN token: NaN where
     the oracle's is)."""
