@@ -373,6 +373,15 @@ int f16_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const floa
     cus = ds->cus;
   }
   hipError_t e;
+  if (f16_gemm_stream_ok(w, x, n, m, batch)) {
+    WsLock ws;
+    st = lock_workspace(ds, s, f16_gemm_stream_workspace_bytes(batch, n, m, cus), ws,
+                        "GEMM workspace");
+    if (st) return st;
+    e = launch_f16_gemm_stream(y, w, x, bias, n, m, batch, ws.p, cus, s);
+    if (e != hipSuccess) return hip_fail(e, "f16 GEMM launch");
+    return HYPNO_HIP_OK;
+  }
   if (batch >= kGemmMinBatch && f16_gemm_v2_ok(w, n, m, batch)) {
     WsLock ws;
     st = lock_workspace(ds, s, f16_gemm_v2_workspace_bytes(batch, n, m, cus), ws,

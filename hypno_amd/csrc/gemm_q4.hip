@@ -738,6 +738,7 @@ struct F16Args {
   float* part;
   const float* colscale;  // optional: output column n multiplied by colscale[n]
   const int* xexp;        // [Mp]: row m of xh holds X row m times 2^-xexp[m]
+  uint32_t w_bytes, xh_bytes, xe_bytes;  // buffer ranges (streaming kernel)
 };
 
 __device__ __forceinline__ void dma16_nt(const void* src, uint8_t* lds_wave_base) {
@@ -838,6 +839,283 @@ __global__ void __launch_bounds__(F16Geom<NW>::kThreads, 1) f16_gemm_v2_kernel(c
   }
 }
 
+// ---------------------------------------------------------------------------
+// FP16 weights, up to 128 tokens: the weight stream is the bound (2 bytes per
+// weight against 2 M flop), so W never passes through LDS and no barrier
+// waits on it.  A work-group of 8 waves owns 256 columns of W (wave w:
+// columns 32 w .. 32 w + 31, two MFMA column tiles) and all 16 MT rows of X;
+// K streams in stages of 64.  Each wave loads its 32 rows' 128-byte stage
+// segments straight from HBM into registers (non-temporal: read once), P
+// stages ahead, as whole lines: 8 rows x 128 bytes per instruction (reading
+// the MFMA operand shape directly, 16 rows x 64 bytes per instruction, ran
+// the weight stream 20-25% slower); at its use the wave passes the stage
+// through its own LDS area (swizzled rows, no barrier: a wave's LDS accesses
+// run in order) into MFMA B operands.  X (16 MT rows x 128 bytes a stage,
+// shared by the 8 waves) moves in groups of P stages: a group is loaded
+// into registers one group ahead and written into one half of a 2 P-slot
+// LDS ring while the other half is read; one barrier per group orders those
+// writes and reads (it waits on LDS only; one per stage held every wave to
+// the slowest wave's weights, stage by stage).  Every wait on a global read
+// is the compiler's own, before the register's first use: with stage j's W
+// issued P stages before its use, the P later stages stay in flight.  The
+// loads are buffer loads issued
+// on every iteration (stages past the range aim past the buffer and read
+// zeros without touching memory), so the count of reads in flight is the
+// same on every path and the compiler's waits stay exact.
+constexpr int kFsWaves = 8;
+constexpr uint32_t kFsOob = 0xFFFFFFF0u;  // an offset past every buffer range
+
+// Hi/lo rows for the streaming kernel at 2..15 tokens: token r < M becomes
+// hi = fp16(x 2^sh) in row r and lo = fp16(x 2^sh - hi) in row 16 + r (sh as
+// in x_row_to_f16: the row's largest |x| 2^sh lies in [2^14, 2^15); 0 for a
+// zero row or one holding inf or NaN), xexp[r] = -sh; rows r >= M are zero.
+// hi + lo is x 2^sh to about 2^-22 of the row's largest value and its
+// products with fp16 weights are exact in fp32, so the sum of the two rows'
+// dot products is as accurate as an fp32 GEMV (where hi is not finite, lo is
+// 0: the product keeps its inf or NaN).  One 256-thread work-group per hi
+// row (16); natural column order; x 16-byte aligned, K % 8 == 0.
+__global__ void __launch_bounds__(256)
+x_rows_hilo_kernel(u32x4* __restrict__ xh, int* __restrict__ xexp, const float* __restrict__ x,
+                   int M, int K) {
+  __shared__ uint32_t red[4];
+  const int r = blockIdx.x, t = threadIdx.x, groups = K / 8;
+  u32x4* hi = xh + (size_t)r * groups;
+  u32x4* lo = xh + (size_t)(16 + r) * groups;
+  if (r >= M) {
+    for (int g = t; g < groups; g += 256) hi[g] = lo[g] = u32x4{0u, 0u, 0u, 0u};
+    if (t == 0) xexp[r] = 0;
+    return;
+  }
+  const float4* src = reinterpret_cast<const float4*>(x + (size_t)r * K);
+  uint32_t mb = 0;  // largest |x| by bit pattern (inf and NaN above every finite value)
+  for (int g = t; g < groups; g += 256) {
+    const float4 a = src[2 * g], b = src[2 * g + 1];
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++) mb = max(mb, __float_as_uint(v[i]) & 0x7FFFFFFFu);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, off, 64));
+  if ((t & 63) == 0) red[t >> 6] = mb;
+  __syncthreads();
+  mb = max(max(red[0], red[1]), max(red[2], red[3]));
+  const float amax = __uint_as_float(mb);
+  int sh = 0;
+  if (amax > 0.0f && amax < __builtin_inff()) sh = 15 - __builtin_amdgcn_frexp_expf(amax);
+  for (int g = t; g < groups; g += 256) {
+    const float4 a = src[2 * g], b = src[2 * g + 1];
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    u32x4 h, l;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float p = ldexpf(v[2 * j], sh), q = ldexpf(v[2 * j + 1], sh);
+      const _Float16 ph = (_Float16)p, qh = (_Float16)q;
+      const float pl = __builtin_isfinite((float)ph) ? p - (float)ph : 0.0f;
+      const float ql = __builtin_isfinite((float)qh) ? q - (float)qh : 0.0f;
+      h[j] = (uint32_t)__builtin_bit_cast(uint16_t, ph) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, qh) << 16);
+      l[j] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)pl) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)ql) << 16);
+    }
+    hi[g] = h;
+    lo[g] = l;
+  }
+  if (t == 0) xexp[r] = -sh;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t fs_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+constexpr int kFsBN = 32 * kFsWaves;  // 256 columns per work-group
+
+// HL: rows 0..15 hold the tokens' hi rows and 16..31 their lo rows (MT = 2);
+// token t's output is the sum of rows t and 16 + t.
+template <int MT, int P, bool HL>
+__global__ void __launch_bounds__(64 * kFsWaves, 1) f16_gemm_stream_kernel(const F16Args a) {
+  static_assert(!HL || MT == 2, "hi/lo rows: two row tiles");
+  constexpr int kRows = 16 * MT;
+  constexpr int kSlotBytes = kRows * kRowBytes;  // one X stage
+  constexpr int kChunks = kRows * 8;             // its 16-byte chunks
+  constexpr int kThr = 64 * kFsWaves;
+  constexpr int kXPer = (kChunks + kThr - 1) / kThr;  // per thread
+  extern __shared__ __align__(16) uint8_t xs[];  // X ring (2 P slots), then the W areas
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int lr = lane & 15, lq = lane >> 4;
+  const int n0 = blockIdx.x * kFsBN + 32 * wave;
+  const int gsteps = a.K / BK;
+  const int z = blockIdx.y;
+  const int s0 = (int)((long long)gsteps * z / a.splits);
+  const int steps = (int)((long long)gsteps * (z + 1) / a.splits) - s0;
+  const uint32_t row_bytes = (uint32_t)a.K * 2;
+  // W read i of a stage: row n0 + 8 i + (lane >> 3) (past N: row N - 1,
+  // never stored), 16-byte piece lane & 7 of its 128-byte segment; it lands
+  // in the wave's LDS area at tile_off(8 i + (lane >> 3), lane & 7)
+  const __amdgpu_buffer_rsrc_t wrs = fs_rsrc(a.w, a.w_bytes);
+  uint8_t* wl = xs + 2 * P * kSlotBytes + wave * 32 * kRowBytes;
+  uint32_t wo[4], wlo[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int r = 8 * i + (lane >> 3);
+    wo[i] = (uint32_t)min(n0 + r, a.N - 1) * row_bytes + (uint32_t)s0 * kRowBytes +
+            16 * (lane & 7);
+    wlo[i] = tile_off(r, lane & 7);
+  }
+  // X chunk q = t + 512 i of a stage: row q >> 3, chunk q & 7 (threads past
+  // the chunks read zeros and store nothing)
+  const __amdgpu_buffer_rsrc_t xrs = fs_rsrc(a.xh, a.xh_bytes);
+  uint32_t xg[kXPer], xo[kXPer];
+  bool xv[kXPer];
+#pragma unroll
+  for (int i = 0; i < kXPer; i++) {
+    const int q = t + kThr * i;
+    xv[i] = q < kChunks;
+    const int row = xv[i] ? q >> 3 : 0;
+    xg[i] = xv[i] ? (uint32_t)row * row_bytes + (uint32_t)s0 * kRowBytes + 16 * (q & 7) : kFsOob;
+    xo[i] = tile_off(row, q & 7);
+  }
+  u32x4 wr[P][4];
+  u32x4 xr[P][kXPer];
+  auto load_w = [&](int s, u32x4(&d)[4]) {  // non-temporal: read once
+    const bool in = s < steps;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      d[i] = __builtin_amdgcn_raw_buffer_load_b128(
+          wrs, in ? wo[i] + (uint32_t)s * kRowBytes : kFsOob, 0, 2);
+  };
+  auto load_x = [&](int s, u32x4(&d)[kXPer]) {
+    const bool in = s < steps;
+#pragma unroll
+    for (int i = 0; i < kXPer; i++)
+      d[i] = __builtin_amdgcn_raw_buffer_load_b128(
+          xrs, in && xv[i] ? xg[i] + (uint32_t)s * kRowBytes : kFsOob, 0, 0);
+  };
+  // Threads past the chunks store their zeros into their wave's W area,
+  // which compute() rewrites before reading (no branch around the stores).
+  auto store_x = [&](int slot, const u32x4(&d)[kXPer]) {
+#pragma unroll
+    for (int i = 0; i < kXPer; i++) {
+      uint8_t* dst = xv[i] ? xs + slot * kSlotBytes + xo[i] : wl + 16 * lane;
+      *reinterpret_cast<u32x4*>(dst) = d[i];
+    }
+  };
+  auto barrier = [&]() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); };
+
+  floatx4 acc[MT][2];
+#pragma unroll
+  for (int i = 0; i < MT; i++)
+#pragma unroll
+    for (int c = 0; c < 2; c++) acc[i][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto compute = [&](int slot, const u32x4(&w)[4]) {
+    const uint8_t* xt = xs + slot * kSlotBytes;
+#pragma unroll
+    for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4*>(wl + wlo[i]) = w[i];
+    // B operand of column tile c: row 16 c + lr, K 32 kh + 8 lq
+    half8 bw[2][2];
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+#pragma unroll
+      for (int kh = 0; kh < 2; kh++)
+        bw[c][kh] = *reinterpret_cast<const half8*>(wl + tile_off(16 * c + lr, 4 * kh + lq));
+#pragma unroll
+    for (int kh = 0; kh < 2; kh++) {
+      const half8 b0 = bw[0][kh];
+      const half8 b1 = bw[1][kh];
+#pragma unroll
+      for (int i = 0; i < MT; i++) {
+        const half8 av = *reinterpret_cast<const half8*>(xt + tile_off(16 * i + lr, 4 * kh + lq));
+        acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, acc[i][0], 0, 0, 0);
+        acc[i][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, acc[i][1], 0, 0, 0);
+      }
+    }
+  };
+
+  // Stage j's W in wr[j % P], its X in xr[j % P] until written to slot j & 1.
+  // Group g: X in ring half g & 1 (slots P (g & 1) + u), W of stage j in
+  // wr[j % P].  The prologue ends in the loop's own issue order (the next
+  // group's X, then W stage by stage), so the loop's waits hold from its
+  // start; group 0's X comes first, into registers of its own.
+  {
+    u32x4 x0[P][kXPer];
+#pragma unroll
+    for (int u = 0; u < P; u++) load_x(u, x0[u]);
+#pragma unroll
+    for (int u = 0; u < P; u++) load_x(P + u, xr[u]);
+#pragma unroll
+    for (int u = 0; u < P; u++) load_w(u, wr[u]);
+#pragma unroll
+    for (int u = 0; u < P; u++) store_x(u, x0[u]);
+  }
+  barrier();
+  // Whole groups (no exit inside the unrolled group, so every path has the
+  // same reads in flight): stages past the range multiply zero X by zero W.
+  const int groups = (steps + P - 1) / P;
+  for (int g = 0; g < groups; g++) {
+    const int h = g & 1;
+#pragma unroll
+    for (int u = 0; u < P; u++) store_x(P * (1 - h) + u, xr[u]);  // group g + 1
+#pragma unroll
+    for (int u = 0; u < P; u++) load_x(P * (g + 2) + u, xr[u]);
+    // the reads go out where they stand (the scheduler would sink them to
+    // the group's end, and the next group's first wait would then drain them)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < P; u++) {
+      const int s = P * g + u;
+      compute(P * h + u, wr[u]);
+      load_w(s + P, wr[u]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    barrier();
+  }
+
+  // acc[i][c][r]: row 16 i + 4 lq + r, column n0 + 16 c + lr.  The row
+  // exponents, bias and column scales are read together before any store.
+  const __amdgpu_buffer_rsrc_t ers = fs_rsrc(a.xexp, a.xe_bytes);
+  u32x4 ex[MT];
+#pragma unroll
+  for (int i = 0; i < MT; i++)
+    ex[i] = __builtin_amdgcn_raw_buffer_load_b128(ers, (uint32_t)(16 * i + 4 * lq) * 4u, 0, 0);
+  float bv[2], cs[2];
+#pragma unroll
+  for (int c = 0; c < 2; c++) {
+    const int n = min(n0 + 16 * c + lr, a.N - 1);
+    bv[c] = (a.splits == 1 && a.bias) ? a.bias[n] : 0.0f;
+    cs[c] = a.colscale ? a.colscale[n] : 1.0f;
+  }
+  float* out = a.splits > 1 ? a.part + (size_t)z * a.M * a.N : a.y;
+  if constexpr (HL) {
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const int n = n0 + 16 * c + lr;
+      if (n >= a.N) continue;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int m = 4 * lq + r;
+        if (m < a.M)
+          out[(size_t)m * a.N + n] =
+              ldexpf(acc[0][c][r] + acc[1][c][r], (int)ex[0][r]) * cs[c] + bv[c];
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int c = 0; c < 2; c++) {
+    const int n = n0 + 16 * c + lr;
+    if (n >= a.N) continue;
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int m = 16 * i + 4 * lq + r;
+        if (m < a.M)
+          out[(size_t)m * a.N + n] = ldexpf(acc[i][c][r], (int)ex[i][r]) * cs[c] + bv[c];
+      }
+  }
+}
+
 // K splits: when the tile grid leaves CUs idle, each tile's K range is cut
 // into `splits` pieces (each at least kMinSplitStages stages) so the grid
 // nearly fills the chip.
@@ -920,6 +1198,89 @@ hipError_t launch_f16_gemm_v2(float* y, const uint8_t* w, const float* x, const 
   hipLaunchKernelGGL(f16_gemm_v2_kernel<kF16NW>, dim3(tiles, a.splits), dim3(G::kThreads), G::kLds,
                      s, a);
   e = hipGetLastError();
+  if (e != hipSuccess || a.splits == 1) return e;
+  const size_t mn = batch * n;
+  hipLaunchKernelGGL(split_k_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, y,
+                     a.part, bias, mn, (int)n, a.splits);
+  return hipGetLastError();
+}
+
+// The streaming FP16 GEMM (2..128 tokens; hi/lo rows below 16): same
+// workspace layout as the DMA-fed kernel (fp16 X rows, exponents, K-split
+// planes over 256-column tiles).
+namespace {
+constexpr int kFsP = 4;  // stages of W and X in registers ahead of their use
+int f16_stream_splits(size_t n, size_t m, int num_cus) {
+  return pick_splits((n + kFsBN - 1) / kFsBN, m, num_cus);
+}
+template <int MT, bool HL = false>
+hipError_t launch_fs(const F16Args& a, dim3 grid, hipStream_t s) {
+  constexpr int lds = 2 * kFsP * 16 * MT * kRowBytes + kFsWaves * 32 * kRowBytes;
+  static_assert(lds <= 160 * 1024, "LDS budget");
+  const void* k = reinterpret_cast<const void*>(f16_gemm_stream_kernel<MT, kFsP, HL>);
+  hipError_t e = set_lds_limit(k, lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((f16_gemm_stream_kernel<MT, kFsP, HL>), grid, dim3(64 * kFsWaves), lds, s,
+                     a);
+  return hipGetLastError();
+}
+}  // namespace
+
+bool f16_gemm_stream_ok(const uint8_t* w, const float* x, size_t n, size_t m, size_t batch) {
+  if (batch < 2 || batch > 128 || m == 0 || m % BK != 0 || n == 0) return false;
+  if (((uintptr_t)w & 15) != 0) return false;
+  if (batch < 16 && ((uintptr_t)x & 15) != 0) return false;  // the hi/lo pre-pass reads float4
+  // 32-bit buffer offsets, with kFsOob past every valid one
+  return n <= (size_t)0x7FFFFFFF && m <= (size_t)0x7FFFFFF && 2 * n * m <= 0xFFFFFF00ull &&
+         (size_t)128 * m * 2 <= 0xFFFFFF00ull;
+}
+
+size_t f16_gemm_stream_workspace_bytes(size_t batch, size_t n, size_t m, int num_cus) {
+  const int splits = f16_stream_splits(n, m, num_cus);
+  const size_t xb = round256(gemm_workspace_bytes(batch, m));
+  return splits > 1 ? xb + (size_t)splits * batch * n * 4 : xb;
+}
+
+hipError_t launch_f16_gemm_stream(float* y, const uint8_t* w, const float* x, const float* bias,
+                                  size_t n, size_t m, size_t batch, void* ws, int num_cus,
+                                  hipStream_t s) {
+  hipError_t e;
+  if (batch < 16) {
+    hipLaunchKernelGGL(x_rows_hilo_kernel, dim3(16), dim3(256), 0, s, static_cast<u32x4*>(ws),
+                       gemm_x_exponents(ws, batch, m), x, (int)batch, (int)m);
+    e = hipGetLastError();
+  } else {
+    e = launch_x_f16_plain(x, batch, m, ws, s);
+  }
+  if (e != hipSuccess) return e;
+  F16Args a{};
+  a.y = y;
+  a.w = w;
+  a.xh = static_cast<const uint8_t*>(ws);
+  a.bias = bias;
+  a.M = (int)batch;
+  a.N = (int)n;
+  a.K = (int)m;
+  a.splits = f16_stream_splits(n, m, num_cus);
+  a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) +
+                                    round256(gemm_workspace_bytes(batch, m)));
+  a.colscale = nullptr;
+  a.xexp = gemm_x_exponents(ws, batch, m);
+  const size_t mp = (batch + 127) / 128 * 128;  // the pre-pass's padded rows
+  a.w_bytes = (uint32_t)(2 * n * m);
+  a.xh_bytes = (uint32_t)(mp * m * 2);
+  a.xe_bytes = (uint32_t)(mp * 4);
+  const dim3 grid((unsigned)((n + kFsBN - 1) / kFsBN), (unsigned)a.splits);
+  if (batch < 16)
+    e = launch_fs<2, true>(a, grid, s);
+  else if (batch == 16)
+    e = launch_fs<1>(a, grid, s);
+  else if (batch <= 32)
+    e = launch_fs<2>(a, grid, s);
+  else if (batch <= 64)
+    e = launch_fs<4>(a, grid, s);
+  else
+    e = launch_fs<8>(a, grid, s);
   if (e != hipSuccess || a.splits == 1) return e;
   const size_t mn = batch * n;
   hipLaunchKernelGGL(split_k_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, y,

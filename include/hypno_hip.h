@@ -40,7 +40,11 @@
  *         (one rounding, relative 2^-11; 2^E_n just above row n's largest
  *         |d|), faster on the largest shapes.  Bar:
  *         ||Y - R||_2 / ||R||_2 <= 2e-3.
- *       FP16: M < 16 fp32 FMAs; M >= 16 as the Q4_0 GEMM with fp16 weights.
+ *       FP16: M = 1 fp32 FMAs; M = 2..15 each token as two fp16 rows, hi and
+ *         lo (x 2^s = hi + lo to ~2^-22), on MFMA against the fp16 weights
+ *         with fp32 accumulation (the 1e-4 bar per token; fp32 FMAs token by
+ *         token if x is not 16-byte aligned); M >= 16 as the Q4_0 GEMM with
+ *         fp16 weights.
  *       Q8_0: M < 16 token by token, activations as three exact int8 digit
  *         planes per block (to 2^-23); M >= 16 weights expanded once to fp16
  *         (row-normalised, relative 2^-11) and the FP16 GEMM.

@@ -750,6 +750,86 @@ def test_gemm_f16_bias_tails_and_repeat(torch, hk, orc, batch, n, m):
     assert orc.rel_l2(y1, ref) <= GEMM_TOL
 
 
+def _f16_dev(torch, wb, x, bias, n, m, batch):
+    import ctypes
+    from hypno_amd import _lib
+    lib = _lib.load()
+    y = torch.full((batch * n,), float("nan"), dtype=torch.float32, device="cuda")
+    st = lib.hypno_hip_matmul_f16_dev(ctypes.c_void_p(y.data_ptr()),
+                                      ctypes.c_void_p(wb.data_ptr()), wb.numel(),
+                                      ctypes.c_void_p(x.data_ptr()),
+                                      None if bias is None else ctypes.c_void_p(bias.data_ptr()),
+                                      n, m, batch, None)
+    assert st == 0
+    torch.cuda.synchronize()
+    return y.cpu().numpy().reshape(batch, n)
+
+
+@pytest.mark.parametrize("batch,n,m", [(2, 4097, 4096), (5, 1000, 4160), (15, 513, 2048),
+                                        (3, 300, 8192)])
+def test_f16_few_tokens_hilo(torch, hk, orc, batch, n, m):
+    """FP16 weights at 2..15 tokens: one pass of the streaming FP16 GEMM over
+    hi/lo fp16 rows (x 2^s = hi + lo per token), held to the GEMV bar of
+    each token's fp32 matmul_f16 (kernels.rs:543-586).  A 1e4 outlier, a
+    tiny token, a zero token, a NaN token; N tails, a K split (n = 300),
+    bias; bit-identical repeats."""
+    w = _f16w(orc, n, m, seed=n + 5)
+    wb = _gpu(torch, w.view(np.uint8).ravel())
+    x = orc.normal_f32(40 + batch, (batch, m))
+    x[0, 7] = np.float32(1e4)
+    x[1] *= np.float32(1e-6)
+    if batch > 2:
+        x[2] = 0.0
+    if batch > 3:
+        x[3, m - 1] = np.float32("nan")
+    bias = orc.normal_f32(41, n)
+    xg, bg = _gpu(torch, x), _gpu(torch, bias)
+    got = _f16_dev(torch, wb, xg, bg, n, m, batch)
+    assert np.array_equal(got, _f16_dev(torch, wb, xg, bg, n, m, batch), equal_nan=True)
+    wbytes = w.view(np.uint8).ravel()
+    for t in range(batch):
+        ref = orc.matmul_f16(wbytes, x[t], bias, n, m)
+        if t == 3:
+            assert np.isnan(got[t]).all() and np.isnan(ref).all()
+        else:
+            assert orc.normwise_err(got[t], ref) <= GEMV_TOL, t
+
+
+def test_f16_few_tokens_inf(torch, hk, orc):
+    """An inf activation: every output of its token is the inf (or NaN for a
+    zero weight) the fp32 reference gives, with its sign; other tokens are
+    unaffected."""
+    batch, n, m = 4, 700, 1024
+    w = _f16w(orc, n, m, seed=9)
+    w[5, 100] = 0.0
+    x = orc.normal_f32(10, (batch, m))
+    x[1, 100] = np.float32("inf")
+    got = _f16_dev(torch, _gpu(torch, w.view(np.uint8).ravel()), _gpu(torch, x), None, n, m, batch)
+    wbytes = w.view(np.uint8).ravel()
+    ref = orc.matmul_f16(wbytes, x[1], None, n, m)
+    assert np.array_equal(np.isnan(got[1]), np.isnan(ref))
+    assert np.array_equal(got[1][np.isinf(ref)], ref[np.isinf(ref)])
+    for t in (0, 2, 3):
+        assert orc.normwise_err(got[t], orc.matmul_f16(wbytes, x[t], None, n, m)) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("batch,n,m", [(16, 4097, 4096), (17, 1000, 2048), (33, 2000, 4160),
+                                        (64, 300, 8192), (100, 4097, 1024), (128, 256, 4096)])
+def test_f16_stream_gemm(torch, hk, orc, batch, n, m):
+    """FP16 weights at 16..128 tokens (the streaming FP16 GEMM, all four tile
+    heights): N tails, K % 256 != 0, a K split with the split-order
+    reduction (n = 300), bias; GEMM bar against fp64; bit-identical repeats."""
+    w = _f16w(orc, n, m, seed=n + 7)
+    wb = _gpu(torch, w.view(np.uint8).ravel())
+    x = orc.normal_f32(50 + batch, (batch, m))
+    bias = orc.normal_f32(51, n)
+    xg, bg = _gpu(torch, x), _gpu(torch, bias)
+    got = _f16_dev(torch, wb, xg, bg, n, m, batch)
+    assert np.array_equal(got, _f16_dev(torch, wb, xg, bg, n, m, batch))
+    ref = x.astype(np.float64) @ w.astype(np.float64).T + bias
+    assert orc.rel_l2(got, ref) <= GEMM_TOL
+
+
 # --- host-slice ABI (drop-in for the &[f32]/&[u8] signature) --------------------------
 
 def test_host_slice_entry_points(hk, orc):
