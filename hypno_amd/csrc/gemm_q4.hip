@@ -842,8 +842,9 @@ __global__ void __launch_bounds__(F16Geom<NW>::kThreads, 1) f16_gemm_v2_kernel(c
 // ---------------------------------------------------------------------------
 // FP16 weights, up to 128 tokens: the weight stream is the bound (2 bytes per
 // weight against 2 M flop), so W never passes through LDS and no barrier
-// waits on it.  A work-group of 8 waves owns 256 columns of W (wave w:
-// columns 32 w .. 32 w + 31, two MFMA column tiles) and all 16 MT rows of X;
+// waits on it.  A work-group of NW waves (8 or 16) owns 32 NW columns of W
+// (wave w: columns 32 w .. 32 w + 31, two MFMA column tiles) and all 16 MT
+// rows of X;
 // K streams in stages of 64.  Each wave loads its 32 rows' 128-byte stage
 // segments straight from HBM into registers (non-temporal: read once), P
 // stages ahead, as whole lines: 8 rows x 128 bytes per instruction (reading
@@ -862,7 +863,6 @@ __global__ void __launch_bounds__(F16Geom<NW>::kThreads, 1) f16_gemm_v2_kernel(c
 // on every iteration (stages past the range aim past the buffer and read
 // zeros without touching memory), so the count of reads in flight is the
 // same on every path and the compiler's waits stay exact.
-constexpr int kFsWaves = 8;
 constexpr uint32_t kFsOob = 0xFFFFFFF0u;  // an offset past every buffer range
 
 // Hi/lo rows for the streaming kernel at 2..15 tokens: token r < M becomes
@@ -927,24 +927,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t fs_rsrc(const void* base, uint
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
 }
-constexpr int kFsBN = 32 * kFsWaves;  // 256 columns per work-group
 
 // HL: rows 0..15 hold the tokens' hi rows and 16..31 their lo rows (MT = 2);
 // token t's output is the sum of rows t and 16 + t.
-template <int MT, int P, bool HL>
-__global__ void __launch_bounds__(64 * kFsWaves, 1) f16_gemm_stream_kernel(const F16Args a) {
+template <int MT, int P, bool HL, int NW>
+__global__ void __launch_bounds__(64 * NW, 1) f16_gemm_stream_kernel(const F16Args a) {
   static_assert(!HL || MT == 2, "hi/lo rows: two row tiles");
   constexpr int kRows = 16 * MT;
   constexpr int kSlotBytes = kRows * kRowBytes;  // one X stage
   constexpr int kChunks = kRows * 8;             // its 16-byte chunks
-  constexpr int kThr = 64 * kFsWaves;
+  constexpr int kThr = 64 * NW;
   constexpr int kXPer = (kChunks + kThr - 1) / kThr;  // per thread
   extern __shared__ __align__(16) uint8_t xs[];  // X ring (2 P slots), then the W areas
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int lr = lane & 15, lq = lane >> 4;
-  const int n0 = blockIdx.x * kFsBN + 32 * wave;
+  const int n0 = blockIdx.x * 32 * NW + 32 * wave;
   const int gsteps = a.K / BK;
   const int z = blockIdx.y;
   const int s0 = (int)((long long)gsteps * z / a.splits);
@@ -1210,19 +1209,39 @@ hipError_t launch_f16_gemm_v2(float* y, const uint8_t* w, const float* x, const 
 // planes over 256-column tiles).
 namespace {
 constexpr int kFsP = 4;  // stages of W and X in registers ahead of their use
-int f16_stream_splits(size_t n, size_t m, int num_cus) {
-  return pick_splits((n + kFsBN - 1) / kFsBN, m, num_cus);
+// Waves per work-group (32 columns each): as many as the tile height leaves
+// registers for — 16 up to 32 tokens (four waves per SIMD), 12 up to 64
+// (three) — where those wider tiles alone cover three quarters of the CUs;
+// else 8.  More reads in flight per CU: lm_head at 4-32 tokens 160-167 us
+// per call with 16 against 212-247 with 8, at 48-64 tokens 226-231 with 12
+// against 240-244 (16 waves there spill registers: 326 us); on the Mistral
+// shapes the wider tiles leave too few work-groups (10-30% slower).
+int f16_stream_waves(size_t n, size_t batch, int num_cus) {
+  const int nw = batch <= 32 ? 16 : batch <= 64 ? 12 : 8;
+  const size_t bn = 32 * (size_t)nw;
+  return (n + bn - 1) / bn * 4 >= (size_t)num_cus * 3 ? nw : 8;
 }
-template <int MT, bool HL = false>
-hipError_t launch_fs(const F16Args& a, dim3 grid, hipStream_t s) {
-  constexpr int lds = 2 * kFsP * 16 * MT * kRowBytes + kFsWaves * 32 * kRowBytes;
+int f16_stream_splits(size_t n, size_t m, size_t batch, int num_cus) {
+  const size_t bn = 32 * (size_t)f16_stream_waves(n, batch, num_cus);
+  return pick_splits((n + bn - 1) / bn, m, num_cus);
+}
+template <int MT, bool HL, int NW>
+hipError_t launch_fs_w(const F16Args& a, dim3 grid, hipStream_t s) {
+  constexpr int lds = 2 * kFsP * 16 * MT * kRowBytes + NW * 32 * kRowBytes;
   static_assert(lds <= 160 * 1024, "LDS budget");
-  const void* k = reinterpret_cast<const void*>(f16_gemm_stream_kernel<MT, kFsP, HL>);
+  const void* k = reinterpret_cast<const void*>(f16_gemm_stream_kernel<MT, kFsP, HL, NW>);
   hipError_t e = set_lds_limit(k, lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((f16_gemm_stream_kernel<MT, kFsP, HL>), grid, dim3(64 * kFsWaves), lds, s,
-                     a);
+  hipLaunchKernelGGL((f16_gemm_stream_kernel<MT, kFsP, HL, NW>), grid, dim3(64 * NW), lds, s, a);
   return hipGetLastError();
+}
+template <int MT, bool HL = false>
+hipError_t launch_fs(const F16Args& a, int nw, dim3 grid, hipStream_t s) {
+  if constexpr (MT <= 2)
+    if (nw == 16) return launch_fs_w<MT, HL, 16>(a, grid, s);
+  if constexpr (MT == 4)
+    if (nw == 12) return launch_fs_w<MT, HL, 12>(a, grid, s);
+  return launch_fs_w<MT, HL, 8>(a, grid, s);
 }
 }  // namespace
 
@@ -1236,7 +1255,7 @@ bool f16_gemm_stream_ok(const uint8_t* w, const float* x, size_t n, size_t m, si
 }
 
 size_t f16_gemm_stream_workspace_bytes(size_t batch, size_t n, size_t m, int num_cus) {
-  const int splits = f16_stream_splits(n, m, num_cus);
+  const int splits = f16_stream_splits(n, m, batch, num_cus);
   const size_t xb = round256(gemm_workspace_bytes(batch, m));
   return splits > 1 ? xb + (size_t)splits * batch * n * 4 : xb;
 }
@@ -1261,7 +1280,8 @@ hipError_t launch_f16_gemm_stream(float* y, const uint8_t* w, const float* x, co
   a.M = (int)batch;
   a.N = (int)n;
   a.K = (int)m;
-  a.splits = f16_stream_splits(n, m, num_cus);
+  const int nw = f16_stream_waves(n, batch, num_cus);
+  a.splits = f16_stream_splits(n, m, batch, num_cus);
   a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) +
                                     round256(gemm_workspace_bytes(batch, m)));
   a.colscale = nullptr;
@@ -1270,17 +1290,18 @@ hipError_t launch_f16_gemm_stream(float* y, const uint8_t* w, const float* x, co
   a.w_bytes = (uint32_t)(2 * n * m);
   a.xh_bytes = (uint32_t)(mp * m * 2);
   a.xe_bytes = (uint32_t)(mp * 4);
-  const dim3 grid((unsigned)((n + kFsBN - 1) / kFsBN), (unsigned)a.splits);
+  const size_t bn = 32 * (size_t)nw;
+  const dim3 grid((unsigned)((n + bn - 1) / bn), (unsigned)a.splits);
   if (batch < 16)
-    e = launch_fs<2, true>(a, grid, s);
+    e = launch_fs<2, true>(a, nw, grid, s);
   else if (batch == 16)
-    e = launch_fs<1>(a, grid, s);
+    e = launch_fs<1>(a, nw, grid, s);
   else if (batch <= 32)
-    e = launch_fs<2>(a, grid, s);
+    e = launch_fs<2>(a, nw, grid, s);
   else if (batch <= 64)
-    e = launch_fs<4>(a, grid, s);
+    e = launch_fs<4>(a, nw, grid, s);
   else
-    e = launch_fs<8>(a, grid, s);
+    e = launch_fs<8>(a, nw, grid, s);
   if (e != hipSuccess || a.splits == 1) return e;
   const size_t mn = batch * n;
   hipLaunchKernelGGL(split_k_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, y,

@@ -766,13 +766,14 @@ def _f16_dev(torch, wb, x, bias, n, m, batch):
 
 
 @pytest.mark.parametrize("batch,n,m", [(2, 4097, 4096), (5, 1000, 4160), (15, 513, 2048),
-                                        (3, 300, 8192)])
+                                        (3, 300, 8192), (8, 98305, 512)])
 def test_f16_few_tokens_hilo(torch, hk, orc, batch, n, m):
     """FP16 weights at 2..15 tokens: one pass of the streaming FP16 GEMM over
     hi/lo fp16 rows (x 2^s = hi + lo per token), held to the GEMV bar of
     each token's fp32 matmul_f16 (kernels.rs:543-586).  A 1e4 outlier, a
     tiny token, a zero token, a NaN token; N tails, a K split (n = 300),
-    bias; bit-identical repeats."""
+    16-wave work-groups (n = 98305: 512-column tiles fill the GPU), bias;
+    bit-identical repeats."""
     w = _f16w(orc, n, m, seed=n + 5)
     wb = _gpu(torch, w.view(np.uint8).ravel())
     x = orc.normal_f32(40 + batch, (batch, m))
@@ -814,11 +815,13 @@ def test_f16_few_tokens_inf(torch, hk, orc):
 
 
 @pytest.mark.parametrize("batch,n,m", [(16, 4097, 4096), (17, 1000, 2048), (33, 2000, 4160),
+                                        (24, 98305, 1024), (16, 98305, 512), (48, 98305, 512),
                                         (64, 300, 8192), (100, 4097, 1024), (128, 256, 4096)])
 def test_f16_stream_gemm(torch, hk, orc, batch, n, m):
     """FP16 weights at 16..128 tokens (the streaming FP16 GEMM, all four tile
-    heights): N tails, K % 256 != 0, a K split with the split-order
-    reduction (n = 300), bias; GEMM bar against fp64; bit-identical repeats."""
+    heights, 8-, 12- and 16-wave work-groups): N tails, K % 256 != 0, a K split
+    with the split-order reduction (n = 300), bias; GEMM bar against fp64;
+    bit-identical repeats."""
     w = _f16w(orc, n, m, seed=n + 7)
     wb = _gpu(torch, w.view(np.uint8).ravel())
     x = orc.normal_f32(50 + batch, (batch, m))
