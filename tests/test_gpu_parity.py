@@ -796,6 +796,21 @@ def test_f16_few_tokens_hilo(torch, hk, orc, batch, n, m):
             assert orc.normwise_err(got[t], ref) <= GEMV_TOL, t
 
 
+def test_f16_few_tokens_unaligned_x(torch, hk, orc):
+    """Below 16 tokens with activations not 16-byte aligned: the FP16 arm
+    runs the fp32 GEMV token by token (the hi/lo pre-pass reads float4);
+    each token within the GEMV bar."""
+    batch, n, m = 5, 600, 1024
+    w = _f16w(orc, n, m, seed=21)
+    x = orc.normal_f32(22, (batch, m))
+    buf = torch.zeros(batch * m + 1, dtype=torch.float32, device="cuda")
+    buf[1:] = _gpu(torch, x.ravel())
+    got = _f16_dev(torch, _gpu(torch, w.view(np.uint8).ravel()), buf[1:], None, n, m, batch)
+    wbytes = w.view(np.uint8).ravel()
+    for t in range(batch):
+        assert orc.normwise_err(got[t], orc.matmul_f16(wbytes, x[t], None, n, m)) <= GEMV_TOL, t
+
+
 def test_f16_few_tokens_inf(torch, hk, orc):
     """An inf activation: every output of its token is the inf (or NaN for a
     zero weight) the fp32 reference gives, with its sign; other tokens are
