@@ -73,6 +73,39 @@ hipError_t ensure(DevBuf& b, size_t bytes, hipStream_t sync) {
   return hipSuccess;
 }
 
+// Grow-only page-locked host buffer (hipHostMalloc).  Host-slice calls stage
+// x, bias and y through it: a copy from page-locked memory is a plain DMA,
+// where the runtime stages a pageable one itself with host-side waits.
+constexpr size_t kPinnedMax = (size_t)8 << 20;  // larger slices are copied directly
+hipError_t ensure_host(DevBuf& b, size_t bytes, hipStream_t sync) {
+  if (b.cap >= bytes && b.p) return hipSuccess;
+  if (b.p) {
+    hipError_t e = hipStreamSynchronize(sync);
+    if (e != hipSuccess) return e;
+    (void)hipHostFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+  }
+  const size_t want = (bytes < 65536 ? 65536 : bytes + 4095) / 4096 * 4096;
+  hipError_t e = hipHostMalloc(&b.p, want, hipHostMallocMapped);
+  if (e != hipSuccess) {
+    b.p = nullptr;
+    return e;
+  }
+  b.cap = want;
+  return hipSuccess;
+}
+
+// Host -> device copy of a host slice on stream s, through the page-locked
+// buffer `pin` when it is small enough.
+hipError_t upload(void* dst, const void* src, size_t bytes, DevBuf& pin, hipStream_t s) {
+  if (bytes > kPinnedMax) return hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s);
+  hipError_t e = ensure_host(pin, bytes, s);
+  if (e != hipSuccess) return e;
+  memcpy(pin.p, src, bytes);
+  return hipMemcpyAsync(dst, pin.p, bytes, hipMemcpyHostToDevice, s);
+}
+
 // Workspace of one (device, stream).  Its mutex is held from the size check
 // through the last launch of a call, so two threads calling on one stream
 // neither free a buffer the other is about to launch with nor interleave
@@ -88,6 +121,7 @@ struct DeviceState {
   int cus = 256;
   hipStream_t stream = nullptr;  // used by the host-slice entry points
   DevBuf w, x, y, bias;          // host-slice staging
+  DevBuf hx, hy, hbias;          // page-locked host staging of x, y, bias
   std::map<hipStream_t, std::unique_ptr<StreamWs>> workspaces;
 };
 
@@ -454,30 +488,50 @@ int host_matmul(float* y, const uint8_t* w, size_t w_len, uint32_t dtype, const 
   const size_t xb = m * batch * 4, yb = n * batch * 4;
   if ((e = ensure(ds->x, xb, s)) != hipSuccess) return hip_fail(e, "x staging");
   if ((e = ensure(ds->y, yb, s)) != hipSuccess) return hip_fail(e, "y staging");
-  if (xb && (e = hipMemcpyAsync(ds->x.p, x, xb, hipMemcpyHostToDevice, s)) != hipSuccess)
-    return hip_fail(e, "x upload");
+  // Every call ends with the stream drained, so the page-locked buffers are
+  // free again when the next call (serialised by g_host_mu) fills them.
+  if (xb && (e = upload(ds->x.p, x, xb, ds->hx, s)) != hipSuccess) return hip_fail(e, "x upload");
+  const bool ypin = yb <= kPinnedMax;
+  if (ypin && (e = ensure_host(ds->hy, yb, s)) != hipSuccess) return hip_fail(e, "y staging");
+  // One token, row-major: the GEMV writes y straight into the mapped
+  // page-locked buffer (plain stores of finished rows, nothing read back),
+  // which saves the device-to-host copy.
+  float* dy = (float*)ds->y.p;
+  bool ydirect = false;
+  if (ypin && batch == 1 && !col) {
+    void* dp = nullptr;
+    if (hipHostGetDevicePointer(&dp, ds->hy.p, 0) == hipSuccess && dp) {
+      dy = (float*)dp;
+      ydirect = true;
+    }
+  }
   float* db = nullptr;
   if (bias) {
     if ((e = ensure(ds->bias, n * 4, s)) != hipSuccess) return hip_fail(e, "bias staging");
-    if ((e = hipMemcpyAsync(ds->bias.p, bias, n * 4, hipMemcpyHostToDevice, s)) != hipSuccess)
+    if ((e = upload(ds->bias.p, bias, n * 4, ds->hbias, s)) != hipSuccess)
       return hip_fail(e, "bias upload");
     db = (float*)ds->bias.p;
   }
   if (dtype == HYPNO_DTYPE_Q4_0 && col)
-    st = q4_0_col_dev((float*)ds->y.p, dw, w_len, (const float*)ds->x.p, db, n, m, batch, s);
+    st = q4_0_col_dev(dy, dw, w_len, (const float*)ds->x.p, db, n, m, batch, s);
   else if (dtype == HYPNO_DTYPE_Q4_0)
-    st = q4_0_dev((float*)ds->y.p, dw, w_len, (const float*)ds->x.p, db, n, m, batch, s);
+    st = q4_0_dev(dy, dw, w_len, (const float*)ds->x.p, db, n, m, batch, s);
   else if (dtype == HYPNO_DTYPE_Q8_0)
-    st = q8_0_dev((float*)ds->y.p, dw, w_len, (const float*)ds->x.p, db, n, m, batch, s);
+    st = q8_0_dev(dy, dw, w_len, (const float*)ds->x.p, db, n, m, batch, s);
   else
-    st = f16_dev((float*)ds->y.p, dw, w_len, (const float*)ds->x.p, db, n, m, batch, s);
+    st = f16_dev(dy, dw, w_len, (const float*)ds->x.p, db, n, m, batch, s);
   if (st) {
     (void)hipStreamSynchronize(s);
     return st;
   }
-  if ((e = hipMemcpyAsync(y, ds->y.p, yb, hipMemcpyDeviceToHost, s)) != hipSuccess)
+  if (!ydirect &&
+      (e = hipMemcpyAsync(ypin ? ds->hy.p : y, ds->y.p, yb, hipMemcpyDeviceToHost, s)) !=
+          hipSuccess) {
+    (void)hipStreamSynchronize(s);
     return hip_fail(e, "y download");
+  }
   if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "stream synchronize");
+  if (ypin && yb) memcpy(y, ds->hy.p, yb);
   return HYPNO_HIP_OK;
 }
 
