@@ -378,7 +378,7 @@ bool f16_gemm_stream_ok(const uint8_t* w, const float* x, size_t n, size_t m, si
 size_t f16_gemm_stream_workspace_bytes(size_t batch, size_t n, size_t m, int num_cus);
 hipError_t launch_f16_gemm_stream(float* y, const uint8_t* w, const float* x, const float* bias,
                                   size_t n, size_t m, size_t batch, void* ws, int num_cus,
-                                  hipStream_t s);
+                                  hipStream_t s, const float* colscale = nullptr);
 
 // Column-major Q4_0 (gemv_col.hip): y[n] = W_col[m][n]^T x[m] (+ bias);
 // the workspace holds the split partial planes (0 bytes: none needed).

@@ -1262,7 +1262,7 @@ size_t f16_gemm_stream_workspace_bytes(size_t batch, size_t n, size_t m, int num
 
 hipError_t launch_f16_gemm_stream(float* y, const uint8_t* w, const float* x, const float* bias,
                                   size_t n, size_t m, size_t batch, void* ws, int num_cus,
-                                  hipStream_t s) {
+                                  hipStream_t s, const float* colscale) {
   hipError_t e;
   if (batch < 16) {
     hipLaunchKernelGGL(x_rows_hilo_kernel, dim3(16), dim3(256), 0, s, static_cast<u32x4*>(ws),
@@ -1284,7 +1284,7 @@ hipError_t launch_f16_gemm_stream(float* y, const uint8_t* w, const float* x, co
   a.splits = f16_stream_splits(n, m, batch, num_cus);
   a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) +
                                     round256(gemm_workspace_bytes(batch, m)));
-  a.colscale = nullptr;
+  a.colscale = colscale;
   a.xexp = gemm_x_exponents(ws, batch, m);
   const size_t mp = (batch + 127) / 128 * 128;  // the pre-pass's padded rows
   a.w_bytes = (uint32_t)(2 * n * m);
