@@ -84,8 +84,12 @@ def hk():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("n,m", [(4096, 4096), (14336, 4096), (4096, 14336), (2048, 2048),
-                                 (256, 2048), (96, 64), (100, 50), (4096, 1), (31, 8)])
+                                 (256, 2048), (96, 64), (100, 50), (4096, 1), (31, 8),
+                                 (100, 10)])
 def test_col_gemv(torch, hk, orc, n, m):
+    """Shapes from the Mistral projections down to a single block column; a
+    tail of n % 32 outputs (bias only); one k range written straight to y
+    (m = 10, with bias)."""
     print(f"col n={n} m={m}", flush=True)
     wq = _col_weights(orc, n + m, n, m)
     x = orc.normal_f32(n + 2 * m, m, 1.0)
@@ -135,3 +139,45 @@ def test_col_exact_short_unaligned_and_batch(torch, hk, orc):
     hk.matmul_vec_col(y16, w16, hk.DType.FP16, xf, None, 64, 128)   # ops.rs:47: not Q4_0
     ref16 = orc.matmul_f16(w16, xf, None, 64, 128)
     assert np.max(np.abs(y16 - ref16)) / np.max(np.abs(ref16)) <= GEMV_TOL
+
+
+@pytest.mark.gpu
+def test_col_nonfinite_x_and_missing_blocks(torch, hk, orc):
+    """An inf and a NaN in x at rows whose blocks lie past a short buffer add
+    nothing (kernels.rs:522: the column ends there), as in the scalar form;
+    an inf at a row that is present spreads as the oracle's does."""
+    n, m = 256, 64
+    wq = _col_weights(orc, 11, n, m)
+    cut = 40 * (n // 32) * 18 + 3 * 18 + 7             # rows >= 41 and most of row 40 missing
+    x = orc.normal_f32(12, m, 1.0)
+    x[50], x[45] = np.float32("inf"), np.float32("nan")
+    y = torch.empty(n, device="cuda")
+    dw = torch.from_numpy(wq[:cut].copy()).cuda()
+    hk.matmul_q4_0_col(y, dw, torch.from_numpy(x).cuda(), None, n, m)
+    want = orc.matmul_q4_0_col(wq[:cut], x, None, n, m)
+    got = y.cpu().numpy()
+    assert np.all(np.isfinite(want)) and np.all(np.isfinite(got))
+    assert np.max(np.abs(got - want)) / np.max(np.abs(want)) <= GEMV_TOL
+    x[3] = np.float32("inf")
+    hk.matmul_q4_0_col(y, dw, torch.from_numpy(x).cuda(), None, n, m)
+    want = orc.matmul_q4_0_col(wq[:cut], x, None, n, m)
+    got = y.cpu().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = np.isfinite(want)
+    assert np.array_equal(got[~fin & ~np.isnan(want)], want[~fin & ~np.isnan(want)])
+
+
+@pytest.mark.gpu
+def test_col_long_k_exact(torch, hk, orc):
+    """m past 65535 ranges of 128 rows (each work-group then loops over three
+    ranges): d = 1 and x in {-1, 1}, so every partial sum is a small integer
+    and the result is exact whatever the order."""
+    rng = np.random.default_rng(13)
+    n, m = 32, 65535 * 128 + 1000
+    print(f"col long k n={n} m={m}", flush=True)
+    wq = _int_weights(rng, n, m)
+    x = rng.choice(np.array([-1.0, 1.0], np.float32), m)
+    want = orc.matmul_q4_0_col(wq, x, None, n, m)
+    y = torch.empty(n, device="cuda")
+    hk.matmul_q4_0_col(y, torch.from_numpy(wq).cuda(), torch.from_numpy(x).cuda(), None, n, m)
+    assert np.array_equal(y.cpu().numpy(), want)

@@ -197,6 +197,7 @@ def test_small_batch_matches_per_token(torch, hk, orc, batch):
     (2, 37, 512), (7, 1000, 1024), (8, 4096, 4096), (9, 130, 2048), (15, 4097, 256),
     (16, 64, 768), (17, 300, 4096), (32, 1024, 3072), (33, 2048, 1024), (64, 4096, 4096),
     (6, 3000, 1536), (8, 12288, 512), (12, 12289, 256), (40, 12300, 256),
+    (5, 12300, 8192), (4, 12289, 256), (7, 14336, 4096),
 ])
 def test_skinny_q4_0(torch, hk, orc, batch, n, m):
     """2..64 tokens: against the oracle's per-token GEMVs (turbo.rs:329-331).
@@ -204,7 +205,8 @@ def test_skinny_q4_0(torch, hk, orc, batch, n, m):
     per token); from 16 the prefill GEMM's (fp16 activations, 2e-3 rel L2).
     N >= 12288, or 16-row tiles that would re-read more than 64 MiB of
     activations (64 tokens at 4096 x 4096), takes 64-row work-groups; the
-    other shapes here 16-row ones."""
+    other shapes here 16-row ones (one stage of K, 32 stages, a last tile of
+    one row or of 12 rows)."""
     q = _q4(orc, n, m, seed=batch * 7 + n)
     x = orc.normal_f32(batch + 100, (batch, m))
     bias = orc.normal_f32(batch + 200, n)
