@@ -307,8 +307,9 @@ int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
 // Q8_0 (ops.rs:33-36, turbo.rs:334-341): the reference dequantises the
 // whole tensor and slices rows of it, so a buffer shorter than n*m elements
 // is a panic there (EINVAL here).  From 16 tokens the fp16 GEMM path runs
-// (weights expanded to fp16 once per call); fewer go token by token through
-// the GEMV.
+// (weights expanded to fp16 once per call); 2 to 15 go through the few-row
+// GEMV in launches of 2 to 4 rows (the tokens split evenly), one token
+// through the GEMV.
 int q8_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const float* bias,
              size_t n, size_t m, size_t batch, hipStream_t s) {
   if (n == 0 || batch == 0) return HYPNO_HIP_OK;
@@ -337,6 +338,17 @@ int q8_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
     if (st) return st;
     e = launch_q8_0_gemm(y, w, x, bias, n, m, batch, ws.p, cus, s);
     if (e != hipSuccess) return hip_fail(e, "q8_0 GEMM launch");
+    return HYPNO_HIP_OK;
+  }
+  const size_t launches = (batch + kGemvMaxRows - 1) / kGemvMaxRows;
+  if (batch >= 2 && q8_0_gemv_rows_ok(w, w_len, n, m, (batch + launches - 1) / launches) &&
+      aligned16(x)) {
+    for (size_t c = 0, t0 = 0; c < launches; c++) {
+      const size_t t1 = batch * (c + 1) / launches;  // 2..4 rows each
+      e = launch_q8_0_gemv_rows(y + t0 * n, w, x + t0 * m, bias, n, m, (int)(t1 - t0), cus, s);
+      if (e != hipSuccess) return hip_fail(e, "q8_0 few-row GEMV launch");
+      t0 = t1;
+    }
     return HYPNO_HIP_OK;
   }
   if (q8_0_gemv_fast_ok(w, w_len, n, m) && aligned16(x)) {

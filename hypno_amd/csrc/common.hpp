@@ -273,12 +273,16 @@ struct GemvGroupGeom {
   size_t lds = 0;
 };
 
-// Few-row GEMV (2 <= rows <= kGemvMaxRows, Q4_0): the streaming kernel with every
-// weight block multiplied by `rows` consecutive x rows (K floats apart) in
-// one pass; y rows n floats apart.  Work-groups of at most 512 threads.
-constexpr int kGemvMaxRows = 4;  // the dispatch takes at most four rows (then few-token MFMA)
+// Few-row GEMV (2 <= rows <= kGemvMaxRows, Q4_0 or Q8_0): the streaming
+// kernel with every weight block multiplied by `rows` consecutive x rows (K
+// floats apart) in one pass; y rows n floats apart.  Work-groups of at most
+// 512 threads.
+constexpr int kGemvMaxRows = 4;  // rows per launch (Q4_0: then few-token MFMA)
 bool q4_0_gemv_rows_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t rows);
 hipError_t launch_q4_0_gemv_rows(float* y, const uint8_t* w, const float* x, const float* bias,
+                                 size_t n, size_t m, int rows, int num_cus, hipStream_t s);
+bool q8_0_gemv_rows_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t rows);
+hipError_t launch_q8_0_gemv_rows(float* y, const uint8_t* w, const float* x, const float* bias,
                                  size_t n, size_t m, int rows, int num_cus, hipStream_t s);
 
 // A launch that the staging rule holds to at most one work-group per CU

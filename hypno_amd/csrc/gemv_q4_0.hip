@@ -327,7 +327,7 @@ struct GemvHead {
 // in one pass (y rows n floats apart); only with one plain Q4_0 job.
 template <int F, bool PRO, int R, int MR = 1>
 __device__ __forceinline__ void gemv_jobs_body(const GemvHead& H, const GemvLaunch& L) {
-  static_assert(MR == 1 || (F == kFmtQ4_0 && !PRO), "several rows: plain Q4_0 only");
+  static_assert(MR == 1 || !PRO, "several rows: no prologue");
   using FT = Fmt<F>;
   constexpr int kLimbs = FT::kLimbs;
   constexpr int kLD = FT::kLimbDwords;
@@ -786,18 +786,23 @@ __device__ __forceinline__ void gemv_jobs_body(const GemvHead& H, const GemvLaun
         }
       } else {
         const float scale = f16_bits_to_f32(d[0] >> sh_d);
-        int acc[kLimbs] = {};
+        int acc[MR][kLimbs] = {};
 #pragma unroll
         for (int j = 0; j < 8; j++) {
           const uint32_t q = __builtin_amdgcn_perm(d[j + 1], d[j], sel_q) ^ 0x80808080u;
 #pragma unroll
-          for (int l = 0; l < kLimbs; l++)
-            acc[l] = __builtin_amdgcn_sdot4((int)q, (int)xl[0][2 * l + (j >> 2)][j & 3], acc[l],
-                                            false);
+          for (int m = 0; m < MR; m++)
+#pragma unroll
+            for (int l = 0; l < kLimbs; l++)
+              acc[m][l] = __builtin_amdgcn_sdot4((int)q, (int)xl[m][2 * l + (j >> 2)][j & 3],
+                                                 acc[m][l], false);
         }
-        const int h = acc[2] * 256 + acc[1];
-        const float r = fmaf((float)h, 256.0f, (float)acc[0]);
-        partial[0] = ldexpf(fmaf(scale, r, xnan[0]), xe[0]);
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+          const int h = acc[m][2] * 256 + acc[m][1];
+          const float r = fmaf((float)h, 256.0f, (float)acc[m][0]);
+          partial[m] = ldexpf(fmaf(scale, r, xnan[m]), xe[m]);
+        }
       }
     }
 #pragma unroll
@@ -844,8 +849,20 @@ __global__ void __launch_bounds__(512) q4_0_gemv_rows_kernel(GEMV_HEAD_PARAMS, G
   gemv_jobs_body<kFmtQ4_0, false, R, MR>(GEMV_HEAD_ARGS, L);
 }
 
+template <int R, int MR>
+__global__ void __launch_bounds__(512) q8_0_gemv_rows_kernel(GEMV_HEAD_PARAMS, GemvLaunch L) {
+  gemv_jobs_body<kFmtQ8_0, false, R, MR>(GEMV_HEAD_ARGS, L);
+}
+
 template <int R>
-static const void* gemv_rows_kernel_r(int rows) {
+static const void* gemv_rows_kernel_r(int rows, int fmt) {
+  if (fmt == kFmtQ8_0) {
+    switch (rows) {
+      case 2: return reinterpret_cast<const void*>(q8_0_gemv_rows_kernel<R, 2>);
+      case 3: return reinterpret_cast<const void*>(q8_0_gemv_rows_kernel<R, 3>);
+      default: return reinterpret_cast<const void*>(q8_0_gemv_rows_kernel<R, 4>);
+    }
+  }
   switch (rows) {
     case 2: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 2>);
     case 3: return reinterpret_cast<const void*>(q4_0_gemv_rows_kernel<R, 3>);
@@ -964,9 +981,9 @@ static hipError_t launch_gemv_fast(int fmt, float* y, const uint8_t* w, const fl
 // Work-groups of 512 threads where the row length allows (twice the steps in
 // flight per work-group of the 256 that the one-row geometry picks for
 // K = 4096; the grid below then needs half the work-groups).
-static bool rows_geometry(GemvGroupGeom& g, size_t m, size_t rows) {
+static bool rows_geometry(GemvGroupGeom& g, size_t m, size_t rows, int fmt) {
   if (rows < 2 || rows > kGemvMaxRows) return false;
-  g.fmt = kFmtQ4_0;
+  g.fmt = fmt;
   g.rows = (int)rows;
   if (!gemv_group_add(g, m) || g.T > 512) return false;
   if (g.T < 512 && 512 % g.Tbase == 0) {
@@ -979,13 +996,20 @@ static bool rows_geometry(GemvGroupGeom& g, size_t m, size_t rows) {
 
 bool q4_0_gemv_rows_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t rows) {
   GemvGroupGeom g;
-  return q4_0_gemv_fast_ok(w, w_len, n, m) && rows_geometry(g, m, rows);
+  return q4_0_gemv_fast_ok(w, w_len, n, m) && rows_geometry(g, m, rows, kFmtQ4_0);
 }
 
-hipError_t launch_q4_0_gemv_rows(float* y, const uint8_t* w, const float* x, const float* bias,
-                                 size_t n, size_t m, int rows, int num_cus, hipStream_t s) {
+bool q8_0_gemv_rows_ok(const uint8_t* w, size_t w_len, size_t n, size_t m, size_t rows) {
   GemvGroupGeom g;
-  if (!rows_geometry(g, m, (size_t)rows)) return hipErrorInvalidValue;
+  return q8_0_gemv_fast_ok(w, w_len, n, m) && rows_geometry(g, m, rows, kFmtQ8_0);
+}
+
+static hipError_t launch_gemv_rows(int fmt, float* y, const uint8_t* w, const float* x,
+                                   const float* bias, size_t n, size_t m, int rows, int num_cus,
+                                   hipStream_t s) {
+  GemvGroupGeom g;
+  if (!rows_geometry(g, m, (size_t)rows, fmt)) return hipErrorInvalidValue;
+  const int bbytes = fmt == kFmtQ8_0 ? Fmt<kFmtQ8_0>::kBytes : kBlockBytes;
   GemvJob J;
   J.w = w;
   J.x = x;
@@ -999,7 +1023,8 @@ hipError_t launch_q4_0_gemv_rows(float* y, const uint8_t* w, const float* x, con
   J.rps = g.T / J.B;
   J.step0 = 0;
   const int steps = (J.n + J.rps - 1) / J.rps;
-  const void* kern = g.ring == 3 ? gemv_rows_kernel_r<3>(rows) : gemv_rows_kernel_r<2>(rows);
+  const void* kern =
+      g.ring == 3 ? gemv_rows_kernel_r<3>(rows, fmt) : gemv_rows_kernel_r<2>(rows, fmt);
   {
     hipError_t e = set_lds_limit(kern, (int)kMaxLds);
     if (e != hipSuccess) return e;
@@ -1013,7 +1038,7 @@ hipError_t launch_q4_0_gemv_rows(float* y, const uint8_t* w, const float* x, con
     per_cu = 1;
   {
     const long long stage = 4LL * kBlockElems * g.maxB * rows;
-    const long long ws = (long long)n * J.B * kBlockBytes / (2 * stage);
+    const long long ws = (long long)n * J.B * bbytes / (2 * stage);
     long long per = (ws + num_cus / 2) / num_cus;
     if (per < 1) per = 1;
     if (per < per_cu) per_cu = (int)per;
@@ -1029,6 +1054,16 @@ hipError_t launch_q4_0_gemv_rows(float* y, const uint8_t* w, const float* x, con
                      steps, grid, g.T, (int)g.ring_off, 1, J.n, J.B, J.rps, J.w, J.x,
                      static_cast<const float*>(nullptr), L);
   return hipGetLastError();
+}
+
+hipError_t launch_q4_0_gemv_rows(float* y, const uint8_t* w, const float* x, const float* bias,
+                                 size_t n, size_t m, int rows, int num_cus, hipStream_t s) {
+  return launch_gemv_rows(kFmtQ4_0, y, w, x, bias, n, m, rows, num_cus, s);
+}
+
+hipError_t launch_q8_0_gemv_rows(float* y, const uint8_t* w, const float* x, const float* bias,
+                                 size_t n, size_t m, int rows, int num_cus, hipStream_t s) {
+  return launch_gemv_rows(kFmtQ8_0, y, w, x, bias, n, m, rows, num_cus, s);
 }
 
 hipError_t launch_q4_0_gemv_fast(float* y, const uint8_t* w, const float* x, const float* bias,

@@ -258,3 +258,45 @@ def test_q8_0_gemm(torch, hk, orc, batch, n, m):
         gb = yb.cpu().numpy().reshape(batch, n)
         assert np.all(np.isfinite(gb))
         assert orc.rel_l2(gb, refb) <= GEMM_TOL
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batch,n,m", [(2, 1000, 4096), (3, 37, 256), (4, 4096, 4096),
+                                       (5, 4096, 14336), (8, 14336, 4096), (13, 300, 2048),
+                                       (15, 2000, 1024)])
+def test_q8_0_few_tokens(torch, hk, orc, batch, n, m):
+    """2 to 15 tokens: the few-row GEMV, in launches of 2 to 4 rows (the
+    tokens split evenly).  Each token's row is bit-identical to its own
+    one-token call (same digits, block partials and fixed-order sums), within
+    the GEMV bar of the oracle; a NaN in one token stays in that token's row;
+    the bias reaches every row."""
+    print(f"q8_0 few tokens batch={batch} n={n} m={m}", flush=True)
+    import ctypes
+    from hypno_amd import _lib
+    lib = _lib.load()
+    wq = _q8(orc, batch + n, n, m)
+    x = orc.normal_f32(batch + 31, (batch, m), 1.0)
+    nan_row = batch // 2
+    x[nan_row, m // 3] = np.float32("nan")
+    bias = orc.normal_f32(n + 9, n, 1.0)
+    dw, dx, db = (torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in (wq, x, bias))
+
+    def call(xp, rows):
+        y = torch.full((rows * n,), float("nan"), device="cuda")
+        _lib.check(lib.hypno_hip_matmul_q8_0_dev(
+            ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(dw.data_ptr()), wq.size,
+            ctypes.c_void_p(xp), ctypes.c_void_p(db.data_ptr()), n, m, rows, None),
+            "matmul_q8_0_dev")
+        torch.cuda.synchronize()
+        return y.cpu().numpy().reshape(rows, n)
+
+    got = call(dx.data_ptr(), batch)
+    for t in range(batch):
+        one = call(dx.data_ptr() + 4 * t * m, 1)[0]
+        assert np.array_equal(got[t], one, equal_nan=True), t
+        ref = orc.matmul_q8_0(wq, x[t], bias, n, m)
+        if t == nan_row:
+            assert np.array_equal(np.isnan(got[t]), np.isnan(ref))
+        else:
+            assert orc.normwise_err(got[t], ref) <= GEMV_TOL, t
+    assert np.array_equal(got, call(dx.data_ptr(), batch), equal_nan=True)
