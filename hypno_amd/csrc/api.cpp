@@ -308,7 +308,7 @@ int q4_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
 // whole tensor and slices rows of it, so a buffer shorter than n*m elements
 // is a panic there (EINVAL here).  From 16 tokens the fp16 GEMM path runs
 // (weights expanded to fp16 once per call); 2 to 15 go through the few-row
-// GEMV in launches of 2 to 4 rows (the tokens split evenly), one token
+// GEMV in launches of 2 to 8 rows (the tokens split evenly), one token
 // through the GEMV.
 int q8_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const float* bias,
              size_t n, size_t m, size_t batch, hipStream_t s) {
@@ -340,11 +340,11 @@ int q8_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
     if (e != hipSuccess) return hip_fail(e, "q8_0 GEMM launch");
     return HYPNO_HIP_OK;
   }
-  const size_t launches = (batch + kGemvMaxRows - 1) / kGemvMaxRows;
+  const size_t launches = (batch + kQ8GemvMaxRows - 1) / kQ8GemvMaxRows;
   if (batch >= 2 && q8_0_gemv_rows_ok(w, w_len, n, m, (batch + launches - 1) / launches) &&
       aligned16(x)) {
     for (size_t c = 0, t0 = 0; c < launches; c++) {
-      const size_t t1 = batch * (c + 1) / launches;  // 2..4 rows each
+      const size_t t1 = batch * (c + 1) / launches;  // 2..8 rows each
       e = launch_q8_0_gemv_rows(y + t0 * n, w, x + t0 * m, bias, n, m, (int)(t1 - t0), cus, s);
       if (e != hipSuccess) return hip_fail(e, "q8_0 few-row GEMV launch");
       t0 = t1;

@@ -860,7 +860,11 @@ static const void* gemv_rows_kernel_r(int rows, int fmt) {
     switch (rows) {
       case 2: return reinterpret_cast<const void*>(q8_0_gemv_rows_kernel<R, 2>);
       case 3: return reinterpret_cast<const void*>(q8_0_gemv_rows_kernel<R, 3>);
-      default: return reinterpret_cast<const void*>(q8_0_gemv_rows_kernel<R, 4>);
+      case 4: return reinterpret_cast<const void*>(q8_0_gemv_rows_kernel<R, 4>);
+      case 5: return reinterpret_cast<const void*>(q8_0_gemv_rows_kernel<R, 5>);
+      case 6: return reinterpret_cast<const void*>(q8_0_gemv_rows_kernel<R, 6>);
+      case 7: return reinterpret_cast<const void*>(q8_0_gemv_rows_kernel<R, 7>);
+      default: return reinterpret_cast<const void*>(q8_0_gemv_rows_kernel<R, 8>);
     }
   }
   switch (rows) {
@@ -982,7 +986,7 @@ static hipError_t launch_gemv_fast(int fmt, float* y, const uint8_t* w, const fl
 // flight per work-group of the 256 that the one-row geometry picks for
 // K = 4096; the grid below then needs half the work-groups).
 static bool rows_geometry(GemvGroupGeom& g, size_t m, size_t rows, int fmt) {
-  if (rows < 2 || rows > kGemvMaxRows) return false;
+  if (rows < 2 || (int)rows > (fmt == kFmtQ8_0 ? kQ8GemvMaxRows : kGemvMaxRows)) return false;
   g.fmt = fmt;
   g.rows = (int)rows;
   if (!gemv_group_add(g, m) || g.T > 512) return false;

@@ -210,7 +210,7 @@ int hypno_hip_matmul_f16_dev(float* y, const uint8_t* w, size_t w_len, const flo
  * semantics for batch > 1).  batch >= 16 with m % 64 == 0 runs a prefill
  * GEMM on an fp16 expansion of the weights (rel-L2 <= 2e-3 of the exact
  * product); smaller batches (m % 256 == 0, x 16-byte aligned) read each
- * weight block once per 2 to 4 tokens, every token's row bit-identical to
+ * weight block once per 2 to 8 tokens, every token's row bit-identical to
  * its one-token call (normwise <= 1e-4); other shapes run token by token. */
 int hypno_hip_matmul_q8_0_dev(float* y, const uint8_t* w_q, size_t w_len, const float* x,
                               const float* bias, size_t n, size_t m, size_t batch,

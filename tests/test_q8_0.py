@@ -263,9 +263,9 @@ def test_q8_0_gemm(torch, hk, orc, batch, n, m):
 @pytest.mark.gpu
 @pytest.mark.parametrize("batch,n,m", [(2, 1000, 4096), (3, 37, 256), (4, 4096, 4096),
                                        (5, 4096, 14336), (8, 14336, 4096), (13, 300, 2048),
-                                       (15, 2000, 1024)])
+                                       (15, 2000, 1024), (6, 100, 512)])
 def test_q8_0_few_tokens(torch, hk, orc, batch, n, m):
-    """2 to 15 tokens: the few-row GEMV, in launches of 2 to 4 rows (the
+    """2 to 15 tokens: the few-row GEMV, in launches of 2 to 8 rows (the
     tokens split evenly).  Each token's row is bit-identical to its own
     one-token call (same digits, block partials and fixed-order sums), within
     the GEMV bar of the oracle; a NaN in one token stays in that token's row;
