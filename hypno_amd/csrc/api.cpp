@@ -370,7 +370,8 @@ int q4_0_col_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const
   if (n == 0 || batch == 0) return HYPNO_HIP_OK;
   if (!y || (!x && m)) return fail(HYPNO_HIP_EINVAL, "y and x must not be NULL");
   if (!w && w_len) return fail(HYPNO_HIP_EINVAL, "w_q is NULL but w_len > 0");
-  if (mul_overflows(n, batch) || mul_overflows(m, batch) || m > 0x7FFFFFFF ||
+  // (m below 2^31 - 2^16: the kernel's k loop steps up to 128 rows past a range)
+  if (mul_overflows(n, batch) || mul_overflows(m, batch) || m > 0x7FFF0000 ||
       n / kBlockElems > 0x7FFFFFFF)
     return fail(HYPNO_HIP_EINVAL, "shape out of range");
   int st = check_disjoint(y, n * batch * 4, w, w_len, x, m * batch * 4, bias, bias ? n * 4 : 0);
