@@ -1092,7 +1092,7 @@ def stream_traffic(path):
         return None
 
 
-# --- CPU baseline -----------------------------------------------
+# --- CPU baseline: the oracle's GEMVs on the host cores ---------------------------------
 
 def host_description():
     """nproc, CPU share, sockets, NUMA nodes and CPU model of this host."""
