@@ -363,8 +363,8 @@ int q8_0_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const flo
   return HYPNO_HIP_OK;
 }
 
-// Column-major Q4_0 (kernels.rs:403-535): tokens one by one, as
-// turbo.rs:322-326 does.
+// Column-major Q4_0 (kernels.rs:403-535): each token's product as
+// turbo.rs:322-326 computes it token by token, the tokens run in groups.
 int q4_0_col_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const float* bias,
                  size_t n, size_t m, size_t batch, hipStream_t s) {
   if (n == 0 || batch == 0) return HYPNO_HIP_OK;
@@ -384,15 +384,21 @@ int q4_0_col_dev(float* y, const uint8_t* w, size_t w_len, const float* x, const
     if (st) return st;
     cus = ds->cus;
   }
+  // Tokens go in groups (one main and one reduction launch each) whose
+  // partial planes fit 64 MB of workspace, at most 256 tokens a group.
   WsLock ws;
-  const size_t wsb = q4_0_col_workspace_bytes(n, m, cus);
+  const size_t per = q4_0_col_workspace_bytes(n, m, cus);
+  size_t group = batch < 256 ? batch : 256;
+  if (per && group > 1 && per * group > ((size_t)64 << 20))
+    group = ((size_t)64 << 20) / per > 1 ? ((size_t)64 << 20) / per : 1;
   hipError_t e;
-  if (wsb) {
-    st = lock_workspace(ds, s, wsb, ws, "column-major workspace");
+  if (per) {
+    st = lock_workspace(ds, s, per * group, ws, "column-major workspace");
     if (st) return st;
   }
-  for (size_t t = 0; t < batch; t++) {
-    e = launch_q4_0_col(y + t * n, w, w_len, x + t * m, bias, n, m, ws.p, cus, s);
+  for (size_t t = 0; t < batch; t += group) {
+    const size_t cnt = batch - t < group ? batch - t : group;
+    e = launch_q4_0_col(y + t * n, w, w_len, x + t * m, bias, n, m, (int)cnt, ws.p, cus, s);
     if (e != hipSuccess) return hip_fail(e, "column-major Q4_0 launch");
   }
   return HYPNO_HIP_OK;

@@ -388,12 +388,14 @@ hipError_t launch_f16_gemm_stream(float* y, const uint8_t* w, const float* x, co
                                   size_t n, size_t m, size_t batch, void* ws, int num_cus,
                                   hipStream_t s, const float* colscale = nullptr);
 
-// Column-major Q4_0 (gemv_col.hip): y[n] = W_col[m][n]^T x[m] (+ bias);
-// the workspace holds the split partial planes (0 bytes: none needed).
+// Column-major Q4_0 (gemv_col.hip): y[n] = W_col[m][n]^T x[m] (+ bias) for
+// `tokens` consecutive x rows (m floats apart) and y rows (n apart) in one
+// main and one reduction launch; the workspace holds each token's split
+// partial planes (q4_0_col_workspace_bytes per token; 0 bytes: none needed).
 size_t q4_0_col_workspace_bytes(size_t n, size_t m, int num_cus);
 hipError_t launch_q4_0_col(float* y, const uint8_t* w, size_t w_len, const float* x,
-                           const float* bias, size_t n, size_t m, void* ws, int num_cus,
-                           hipStream_t s);
+                           const float* bias, size_t n, size_t m, int tokens, void* ws,
+                           int num_cus, hipStream_t s);
 
 // Decode-step neighbours of the GEMV (prologue.hip).  rms_norm: `rows` rows
 // of n, out may alias x; silu_mul: n elements, out may alias gate.

@@ -93,9 +93,12 @@ template <int KW, int R, bool kWindow>
 __global__ void __launch_bounds__(64 * KW)
 q4_0_col_wide_kernel(float* __restrict__ part, const uint8_t* __restrict__ w, size_t avail_blocks,
                      uint32_t w_range, const float* __restrict__ x,
-                     const float* __restrict__ bias, int nb, int m, int k_per) {
+                     const float* __restrict__ bias, int nb, int m, int k_per, size_t part_tok) {
 #if defined(__HIP_DEVICE_COMPILE__)  // (the buffer builtins exist only in the device pass)
   extern __shared__ __align__(16) float4 red4[];  // [KW][8][64]
+  // token blockIdx.z: its x row and its planes (or its y row)
+  x += (size_t)blockIdx.z * m;
+  part += (size_t)blockIdx.z * part_tok;
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = blockIdx.x * 64 + lane;
@@ -197,7 +200,11 @@ constexpr int kRedOut = 32, kRedSlices = 8;
 
 __global__ void __launch_bounds__(kRedOut * kRedSlices)
 q4_0_col_reduce_kernel(float* __restrict__ y, const float* __restrict__ part,
-                       const float* __restrict__ bias, size_t n, size_t covered, int planes) {
+                       const float* __restrict__ bias, size_t n, size_t covered, int planes,
+                       size_t y_tok, size_t part_tok) {
+  // token blockIdx.y: its y row and its planes
+  y += (size_t)blockIdx.y * y_tok;
+  if (part) part += (size_t)blockIdx.y * part_tok;
   __shared__ float red[kRedSlices][kRedOut];
   const int jo = threadIdx.x % kRedOut, sl = threadIdx.x / kRedOut;
   const size_t j = (size_t)blockIdx.x * kRedOut + jo;
@@ -265,61 +272,72 @@ size_t q4_0_col_workspace_bytes(size_t n, size_t m, int num_cus) {
 template <int KW, int R, bool kWindow>
 static hipError_t launch_col_wide(const ColGeom& g, float* part, const uint8_t* w, size_t avail,
                                   uint32_t w_range, const float* x, const float* bias, int nb,
-                                  int m, hipStream_t s) {
+                                  int m, int tokens, size_t part_tok, hipStream_t s) {
   constexpr int lds = KW * 8 * 64 * (int)sizeof(float4);
   const void* k = reinterpret_cast<const void*>(q4_0_col_wide_kernel<KW, R, kWindow>);
   hipError_t e = set_lds_limit(k, lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((q4_0_col_wide_kernel<KW, R, kWindow>), dim3(g.gx, g.gy), dim3(64 * KW), lds,
-                     s, part, w, avail, w_range, x, bias, nb, m, g.k_per);
+  hipLaunchKernelGGL((q4_0_col_wide_kernel<KW, R, kWindow>), dim3(g.gx, g.gy, tokens),
+                     dim3(64 * KW), lds, s, part, w, avail, w_range, x, bias, nb, m, g.k_per,
+                     part_tok);
   return hipGetLastError();
 }
 
 template <bool kWindow>
 static hipError_t launch_col_main(const ColGeom& g, float* part, const uint8_t* w, size_t avail,
                                   uint32_t w_range, const float* x, const float* bias, int nb,
-                                  int m, hipStream_t s) {
+                                  int m, int tokens, size_t part_tok, hipStream_t s) {
   if (g.r == 8)
-    return launch_col_wide<8, 8, kWindow>(g, part, w, avail, w_range, x, bias, nb, m, s);
+    return launch_col_wide<8, 8, kWindow>(g, part, w, avail, w_range, x, bias, nb, m, tokens,
+                                          part_tok, s);
   if (g.kw == 16)
-    return launch_col_wide<16, 2, kWindow>(g, part, w, avail, w_range, x, bias, nb, m, s);
-  return launch_col_wide<8, 2, kWindow>(g, part, w, avail, w_range, x, bias, nb, m, s);
+    return launch_col_wide<16, 2, kWindow>(g, part, w, avail, w_range, x, bias, nb, m, tokens,
+                                           part_tok, s);
+  return launch_col_wide<8, 2, kWindow>(g, part, w, avail, w_range, x, bias, nb, m, tokens,
+                                        part_tok, s);
 }
 
 hipError_t launch_q4_0_col(float* y, const uint8_t* w, size_t w_len, const float* x,
-                           const float* bias, size_t n, size_t m, void* ws, int num_cus,
-                           hipStream_t s) {
+                           const float* bias, size_t n, size_t m, int tokens, void* ws,
+                           int num_cus, hipStream_t s) {
   const int nb = (int)(n / kBlockElems);
   const size_t covered = (size_t)nb * kBlockElems;
   const size_t avail = w_len / kBlockBytes;
+  const unsigned red_n = (unsigned)((n + kRedOut - 1) / kRedOut);
   if (nb > 0 && m > 0 && avail > 0) {
     const ColGeom g = col_geom(nb, m, num_cus);
     float* part = g.gy > 1 ? static_cast<float*>(ws) : y;
+    // a token's planes in the workspace, or its y row when y is written directly
+    const size_t part_tok = g.gy > 1 ? (size_t)g.gy * covered : n;
     // Windows need a dword-aligned w, 2 readable bytes after the last valid
     // block when its index is even, and 32-bit offsets.
     const bool window = ((uintptr_t)w & 3) == 0 && w_len <= kColOob &&
                         (avail % 2 == 0 || w_len >= avail * kBlockBytes + 2);
     const uint32_t range = (uint32_t)(w_len < kColOob ? w_len : kColOob);
-    hipError_t e =
-        window ? launch_col_main<true>(g, part, w, avail, range, x, bias, nb, (int)m, s)
-               : launch_col_main<false>(g, part, w, avail, range, x, bias, nb, (int)m, s);
+    hipError_t e = window ? launch_col_main<true>(g, part, w, avail, range, x, bias, nb, (int)m,
+                                                  tokens, part_tok, s)
+                          : launch_col_main<false>(g, part, w, avail, range, x, bias, nb, (int)m,
+                                                   tokens, part_tok, s);
     if (e != hipSuccess) return e;
     if (g.gy == 1) {
       if (covered == n) return hipSuccess;  // y written, bias included
       // y[0, covered) holds the sums (+ bias); the tail gets the bias.
       const size_t tail = n - covered;
-      hipLaunchKernelGGL(q4_0_col_reduce_kernel, dim3((unsigned)((tail + kRedOut - 1) / kRedOut)),
+      hipLaunchKernelGGL(q4_0_col_reduce_kernel,
+                         dim3((unsigned)((tail + kRedOut - 1) / kRedOut), (unsigned)tokens),
                          dim3(kRedOut * kRedSlices), 0, s, y + covered, nullptr,
-                         bias ? bias + covered : nullptr, tail, (size_t)0, 0);
+                         bias ? bias + covered : nullptr, tail, (size_t)0, 0, n, (size_t)0);
       return hipGetLastError();
     }
-    hipLaunchKernelGGL(q4_0_col_reduce_kernel, dim3((unsigned)((n + kRedOut - 1) / kRedOut)),
-                       dim3(kRedOut * kRedSlices), 0, s, y, part, bias, n, covered, g.gy);
+    hipLaunchKernelGGL(q4_0_col_reduce_kernel, dim3(red_n, (unsigned)tokens),
+                       dim3(kRedOut * kRedSlices), 0, s, y, part, bias, n, covered, g.gy, n,
+                       part_tok);
     return hipGetLastError();
   }
   // No whole block, no input or no weight block: y = bias (or 0).
-  hipLaunchKernelGGL(q4_0_col_reduce_kernel, dim3((unsigned)((n + kRedOut - 1) / kRedOut)),
-                     dim3(kRedOut * kRedSlices), 0, s, y, nullptr, bias, n, (size_t)0, 0);
+  hipLaunchKernelGGL(q4_0_col_reduce_kernel, dim3(red_n, (unsigned)tokens),
+                     dim3(kRedOut * kRedSlices), 0, s, y, nullptr, bias, n, (size_t)0, 0, n,
+                     (size_t)0);
   return hipGetLastError();
 }
 

@@ -196,7 +196,8 @@ int hypno_hip_matmul_q4_0_dev_noalloc(float* y, const uint8_t* w_q, size_t w_len
                                       size_t batch, void* stream);
 
 /* Column-major Q4_0 on device pointers (semantics of
- * hypno_hip_matmul_q4_0_col; batch > 1: token by token, turbo.rs:322-326). */
+ * hypno_hip_matmul_q4_0_col; batch > 1: each token's product as
+ * turbo.rs:322-326 computes it token by token, the tokens run in groups). */
 int hypno_hip_matmul_q4_0_col_dev(float* y, const uint8_t* w_q, size_t w_len, const float* x,
                                   const float* bias, size_t n, size_t m, size_t batch,
                                   void* stream);

@@ -181,3 +181,36 @@ def test_col_long_k_exact(torch, hk, orc):
     y = torch.empty(n, device="cuda")
     hk.matmul_q4_0_col(y, torch.from_numpy(wq).cuda(), torch.from_numpy(x).cuda(), None, n, m)
     assert np.array_equal(y.cpu().numpy(), want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batch,n,m", [(5, 4096, 4096), (3, 100, 10), (300, 96, 512)])
+def test_col_batch_groups(torch, hk, orc, batch, n, m):
+    """Several tokens on the device path run as groups (one main launch over
+    all the group's tokens, one reduction launch; 300 tokens make two
+    groups): every token's row bit-identical to its own one-token call, and
+    within the GEMV bar of the scalar restatement, bias included."""
+    import ctypes
+    from hypno_amd import _lib
+    lib = _lib.load()
+    print(f"col batch={batch} n={n} m={m}", flush=True)
+    wq = _col_weights(orc, batch + n, n, m)
+    x = orc.normal_f32(batch + 3 * n, (batch, m), 1.0)
+    bias = orc.normal_f32(n + 4, n, 1.0)
+    dw, dx, db = (torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in (wq, x, bias))
+
+    def call(xp, rows):
+        y = torch.full((rows * n,), float("nan"), device="cuda")
+        _lib.check(lib.hypno_hip_matmul_q4_0_col_dev(
+            ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(dw.data_ptr()), wq.size,
+            ctypes.c_void_p(xp), ctypes.c_void_p(db.data_ptr()), n, m, rows, None),
+            "matmul_q4_0_col_dev")
+        torch.cuda.synchronize()
+        return y.cpu().numpy().reshape(rows, n)
+
+    got = call(dx.data_ptr(), batch)
+    for t in sorted({0, 1, batch // 2, batch - 1}):
+        assert np.array_equal(got[t], call(dx.data_ptr() + 4 * t * m, 1)[0]), t
+    for t in range(batch):
+        ref = orc.matmul_q4_0_col(wq, x[t], bias, n, m)
+        assert np.max(np.abs(got[t] - ref)) / np.max(np.abs(ref)) <= GEMV_TOL, t
