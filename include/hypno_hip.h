@@ -45,9 +45,10 @@
  *         with fp32 accumulation (the 1e-4 bar per token; fp32 FMAs token by
  *         token if x is not 16-byte aligned); M >= 16 as the Q4_0 GEMM with
  *         fp16 weights.
- *       Q8_0: M < 16 token by token, activations as three exact int8 digit
- *         planes per block (to 2^-23); M >= 16 weights expanded once to fp16
- *         (row-normalised, relative 2^-11) and the FP16 GEMM.
+ *       Q8_0: M < 16 each token's activations as three exact int8 digit
+ *         planes per block (to 2^-23), each weight block read once for 2 to 8
+ *         tokens; M >= 16 weights expanded once to fp16 (row-normalised,
+ *         relative 2^-11) and the FP16 GEMM.
  *   - Every function returns a status (HYPNO_HIP_OK on success) and never
  *     aborts the process.  hypno_hip_last_error() describes the last failure
  *     on the calling thread.
